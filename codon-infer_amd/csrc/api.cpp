@@ -1,0 +1,723 @@
+// C ABI of the gfx950 ESM-2 encoder: model residency, workspace, and the
+// batched bidirectional forward that replaces codon-infer's
+// forward_bidirectional* family (src/lib.rs:5078-6147).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "host.h"
+#include "kernels.h"
+
+using namespace cih;
+
+namespace cih {
+static thread_local std::string g_err;
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+}  // namespace cih
+
+#define HIPCHK(expr)                                                                                     \
+    do {                                                                                                 \
+        hipError_t e_ = (expr);                                                                          \
+        if (e_ != hipSuccess) return set_error(CIH_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+namespace {
+
+struct Layer {
+    DevMatrix wqkv, wo, w1, w2;
+    float *bqkv = nullptr, *bo = nullptr, *b1 = nullptr, *b2 = nullptr;
+    float *ln1w = nullptr, *ln1b = nullptr, *ln2w = nullptr, *ln2b = nullptr;
+};
+
+struct Workspace {
+    int maxB = 0, maxS = 0;
+    uint32_t flags = 0;
+    int *tokens = nullptr, *cu = nullptr, *lens = nullptr;
+    int *h_meta = nullptr;  // pinned: cu[maxB] | lens[maxB]
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *ao = nullptr, *hbuf = nullptr, *logits = nullptr;
+    float *rope_c = nullptr, *rope_s = nullptr;
+    float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
+    float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
+    // device staging of outputs for host-pointer calls (padded layouts)
+    float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
+          *o_layer = nullptr;
+    std::vector<void *> dev, host;
+};
+
+struct Prof {
+    bool on = false;
+    std::vector<hipEvent_t> ev;  // pairs
+    std::vector<int> cls;
+    std::vector<double> flops, bytes;
+    size_t used = 0;
+    cih_kernel_stats st[CIH_KC_COUNT] = {};
+};
+
+}  // namespace
+
+struct cih_model {
+    cih_config cfg{};
+    int dtype = 0, hd = 0;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void *> allocs;
+    DevMatrix emb;
+    std::vector<Layer> layers;
+    float *lnfw = nullptr, *lnfb = nullptr;
+    bool has_head = false;
+    DevMatrix dense, dec;
+    float *dense_b = nullptr, *lm_lnw = nullptr, *lm_lnb = nullptr, *dec_b = nullptr;
+    std::vector<float> contact_w;
+    float contact_b = 0.0f;
+    bool has_contacts = false;
+    float *d_contact_w = nullptr;
+    int *d_heads = nullptr;  // [L][H] per-layer list of heads with nonzero weight
+    std::vector<int> nz;
+    Workspace ws;
+    Prof prof;
+};
+
+namespace {
+
+template <class T>
+hipError_t dalloc(T *&p, size_t n, std::vector<void *> &list) {
+    p = nullptr;
+    if (n == 0) return hipSuccess;
+    void *v = nullptr;
+    hipError_t e = hipMalloc(&v, n * sizeof(T));
+    if (e != hipSuccess) return e;
+    list.push_back(v);
+    p = (T *)v;
+    return hipSuccess;
+}
+
+template <class T>
+int upload(cih_model *m, T *&dst, const T *src, size_t n) {
+    HIPCHK(dalloc(dst, n, m->allocs));
+    if (n) HIPCHK(hipMemcpy(dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+    return 0;
+}
+
+// One [N][K] source matrix (FP32 values or reference row-major blocks) that
+// becomes rows [n_off, n_off + N) of a device matrix.
+struct Part {
+    const void *src;
+    int N;
+};
+
+// Repacks parts into the k-block-major device layout (see kernels.h) and
+// uploads.  Quantized blocks keep their exact bytes and scales.
+int upload_matrix(cih_model *m, int dtype, int K, const std::vector<Part> &parts, DevMatrix &out) {
+    int Ntot = 0;
+    for (auto &p : parts) Ntot += p.N;
+    const int KB = K / 32;
+    out.N = Ntot;
+    out.K = K;
+    out.fmt = dtype == DT_Q8 ? WF_Q8 : (dtype == DT_Q4 ? WF_Q4 : WF_F32);
+    if (dtype == DT_FP32) {
+        std::vector<float> h((size_t)KB * Ntot * 32);
+        int off = 0;
+        for (auto &p : parts) {
+            const float *src = (const float *)p.src;
+            parallel_for(p.N, [&](int64_t a, int64_t b) {
+                for (int64_t n = a; n < b; n++)
+                    for (int kb = 0; kb < KB; kb++)
+                        std::memcpy(&h[((size_t)kb * Ntot + off + n) * 32], src + (size_t)n * K + kb * 32, 128);
+            });
+            off += p.N;
+        }
+        float *d;
+        if (int rc = upload(m, d, h.data(), h.size())) return rc;
+        out.q = d;
+        out.sc = nullptr;
+        return 0;
+    }
+    const int bb = block_bytes(dtype), qb = bb - 4;
+    std::vector<uint8_t> hq((size_t)KB * Ntot * qb);
+    std::vector<float> hs((size_t)KB * Ntot);
+    int off = 0;
+    for (auto &p : parts) {
+        const uint8_t *src = (const uint8_t *)p.src;
+        parallel_for(p.N, [&](int64_t a, int64_t b) {
+            for (int64_t n = a; n < b; n++)
+                for (int kb = 0; kb < KB; kb++) {
+                    const uint8_t *blk = src + ((size_t)n * KB + kb) * bb;
+                    std::memcpy(&hs[(size_t)kb * Ntot + off + n], blk, 4);
+                    std::memcpy(&hq[((size_t)kb * Ntot + off + n) * qb], blk + 4, qb);
+                }
+        });
+        off += p.N;
+    }
+    uint8_t *dq;
+    float *ds;
+    if (int rc = upload(m, dq, hq.data(), hq.size())) return rc;
+    if (int rc = upload(m, ds, hs.data(), hs.size())) return rc;
+    out.q = dq;
+    out.sc = ds;
+    return 0;
+}
+
+const void *mat_ptr(const void *base, int dtype, int64_t elems) {
+    if (dtype == DT_FP32) return (const float *)base + elems;
+    return (const uint8_t *)base + elems / 32 * block_bytes(dtype);
+}
+
+void free_list(std::vector<void *> &l) {
+    for (void *p : l) hipFree(p);
+    l.clear();
+}
+
+void free_workspace(Workspace &ws) {
+    free_list(ws.dev);
+    for (void *p : ws.host) hipHostFree(p);
+    ws.host.clear();
+    ws = Workspace();
+}
+
+int check_config(const cih_config *c) {
+    if (!c) return set_error(CIH_ERR_ARG, "null config");
+    if (c->dim <= 0 || c->n_heads <= 0 || c->n_layers <= 0 || c->hidden_dim <= 0 || c->vocab_size <= 0)
+        return set_error(CIH_ERR_SHAPE, "non-positive config dimension");
+    if (c->dim % c->n_heads) return set_error(CIH_ERR_SHAPE, "dim %d not divisible by n_heads %d", c->dim, c->n_heads);
+    const int hd = c->dim / c->n_heads;
+    if (hd != 16 && hd != 24 && hd != 32 && hd != 64)
+        return set_error(CIH_ERR_SHAPE, "head_dim %d not in {16, 24, 32, 64}", hd);
+    if (c->dim % 32 || c->hidden_dim % 32)
+        return set_error(CIH_ERR_SHAPE, "dim and hidden_dim must be multiples of 32 (got %d, %d)", c->dim,
+                         c->hidden_dim);
+    if (c->dim > 2560) return set_error(CIH_ERR_SHAPE, "dim %d above the LayerNorm kernel's 2560", c->dim);
+    if (c->vocab_size <= 32) return set_error(CIH_ERR_SHAPE, "vocab_size must be > 32 (<mask> is id 32)");
+    return 0;
+}
+
+struct ProfScope {
+    cih_model *m;
+    int idx = -1;
+    ProfScope(cih_model *m_, int cls, double flops, double bytes) : m(m_) {
+        Prof &p = m->prof;
+        if (!p.on) return;
+        if (p.used >= p.cls.size()) {
+            hipEvent_t a, b;
+            if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return;
+            p.ev.push_back(a);
+            p.ev.push_back(b);
+            p.cls.push_back(0);
+            p.flops.push_back(0);
+            p.bytes.push_back(0);
+        }
+        idx = (int)p.used++;
+        p.cls[idx] = cls;
+        p.flops[idx] = flops;
+        p.bytes[idx] = bytes;
+        hipEventRecord(p.ev[2 * idx], m->stream);
+    }
+    ~ProfScope() {
+        if (idx >= 0) hipEventRecord(m->prof.ev[2 * idx + 1], m->stream);
+    }
+};
+
+double wbytes(const DevMatrix &W) {
+    const double e = (double)W.N * W.K;
+    return W.fmt == WF_F32 ? 4.0 * e : (W.fmt == WF_Q8 ? 1.125 * e : 0.625 * e);
+}
+
+hipError_t gemm(cih_model *m, const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
+                int epi) {
+    const double flops = 2.0 * M * W.N * W.K;
+    const double bytes = wbytes(W) + 4.0 * M * W.K + 4.0 * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
+    ProfScope ps(m, W.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, flops, bytes);
+    return launch_gemm(W, X, ldx, bias, Y, ldy, M, epi, m->stream);
+}
+
+}  // namespace
+
+// =============================================================================
+
+extern "C" {
+
+const char *cih_last_error(void) { return g_err.c_str(); }
+int cih_abi_version(void) { return CIH_ABI_VERSION; }
+
+int cih_model_create(const cih_config *cfg, int32_t dtype, const cih_host_weights *w, const float *contact_w,
+                     float contact_b, cih_model **out) {
+    if (!out || !w) return set_error(CIH_ERR_ARG, "null argument");
+    *out = nullptr;
+    if (int rc = check_config(cfg)) return rc;
+    if (dtype != DT_FP32 && dtype != DT_Q8 && dtype != DT_Q4) return set_error(CIH_ERR_ARG, "bad dtype %d", dtype);
+    const void *need[] = {w->token_embedding_table, w->ln_1_weight, w->ln_1_bias, w->wq, w->bq, w->wk, w->bk, w->wv,
+                          w->bv, w->wo, w->bo, w->ln_2_weight, w->ln_2_bias, w->fc1_weight, w->fc1_bias,
+                          w->fc2_weight, w->fc2_bias, w->ln_f_weight, w->ln_f_bias};
+    for (const void *p : need)
+        if (!p) return set_error(CIH_ERR_ARG, "null weight tensor");
+    int dev_count = 0;
+    if (hipGetDeviceCount(&dev_count) != hipSuccess || dev_count == 0)
+        return set_error(CIH_ERR_HIP, "no HIP device available");
+
+    cih_model *m = new cih_model();
+    m->cfg = *cfg;
+    m->dtype = dtype;
+    m->hd = cfg->dim / cfg->n_heads;
+    const int64_t d = cfg->dim, F = cfg->hidden_dim, L = cfg->n_layers, V = cfg->vocab_size, H = cfg->n_heads;
+    auto fail = [&](int rc) {
+        cih_model_destroy(m);
+        return rc;
+    };
+    if (hipGetDevice(&m->device) != hipSuccess || hipStreamCreate(&m->stream) != hipSuccess)
+        return fail(set_error(CIH_ERR_HIP, "stream creation failed"));
+
+    // token embedding [V][d]: Q8 blocks for Q8 models, FP32 otherwise (lib.rs:675-687 vs 1113-1125)
+    const int emb_dt = dtype == DT_Q8 ? DT_Q8 : DT_FP32;
+    if (int rc = upload_matrix(m, emb_dt, (int)d, {{w->token_embedding_table, (int)V}}, m->emb)) return fail(rc);
+
+    m->layers.resize(L);
+    for (int64_t l = 0; l < L; l++) {
+        Layer &ly = m->layers[l];
+        const int64_t dd = l * d * d;
+        int rc = upload_matrix(m, dtype, (int)d,
+                               {{mat_ptr(w->wq, dtype, dd), (int)d}, {mat_ptr(w->wk, dtype, dd), (int)d},
+                                {mat_ptr(w->wv, dtype, dd), (int)d}},
+                               ly.wqkv);
+        if (!rc) rc = upload_matrix(m, dtype, (int)d, {{mat_ptr(w->wo, dtype, dd), (int)d}}, ly.wo);
+        if (!rc) rc = upload_matrix(m, dtype, (int)d, {{mat_ptr(w->fc1_weight, dtype, l * F * d), (int)F}}, ly.w1);
+        if (!rc) rc = upload_matrix(m, dtype, (int)F, {{mat_ptr(w->fc2_weight, dtype, l * d * F), (int)d}}, ly.w2);
+        if (rc) return fail(rc);
+        std::vector<float> bqkv(3 * d);
+        std::memcpy(bqkv.data(), w->bq + l * d, d * 4);
+        std::memcpy(bqkv.data() + d, w->bk + l * d, d * 4);
+        std::memcpy(bqkv.data() + 2 * d, w->bv + l * d, d * 4);
+        if ((rc = upload(m, ly.bqkv, bqkv.data(), bqkv.size())) || (rc = upload(m, ly.bo, w->bo + l * d, d)) ||
+            (rc = upload(m, ly.b1, w->fc1_bias + l * F, F)) || (rc = upload(m, ly.b2, w->fc2_bias + l * d, d)) ||
+            (rc = upload(m, ly.ln1w, w->ln_1_weight + l * d, d)) || (rc = upload(m, ly.ln1b, w->ln_1_bias + l * d, d)) ||
+            (rc = upload(m, ly.ln2w, w->ln_2_weight + l * d, d)) || (rc = upload(m, ly.ln2b, w->ln_2_bias + l * d, d)))
+            return fail(rc);
+    }
+    if (int rc = upload(m, m->lnfw, w->ln_f_weight, d)) return fail(rc);
+    if (int rc = upload(m, m->lnfb, w->ln_f_bias, d)) return fail(rc);
+
+    // LM head (lib.rs:5379-5439): classifier = [ln_w, ln_b, dense_w, dense_b, dec_w, dec_b]
+    const int64_t req = 3 * d + d * d + V * d + V;
+    m->has_head = w->classifier_weights && w->classifier_len >= req;
+    if (m->has_head) {
+        const float *c = w->classifier_weights;
+        int rc = upload(m, m->lm_lnw, c, d);
+        if (!rc) rc = upload(m, m->lm_lnb, c + d, d);
+        if (!rc) rc = upload_matrix(m, DT_FP32, (int)d, {{c + 2 * d, (int)d}}, m->dense);
+        if (!rc) rc = upload(m, m->dense_b, c + 2 * d + d * d, d);
+        if (!rc) rc = upload_matrix(m, DT_FP32, (int)d, {{c + 3 * d + d * d, (int)V}}, m->dec);
+        if (!rc) rc = upload(m, m->dec_b, c + 3 * d + d * d + V * d, V);
+        if (rc) return fail(rc);
+    }
+
+    // contact regression weights (EsmConfig::contact_head_weights, lib.rs:154-177)
+    m->has_contacts = contact_w != nullptr;
+    m->contact_b = contact_b;
+    m->nz.assign(L, 0);
+    if (m->has_contacts) {
+        m->contact_w.assign(contact_w, contact_w + L * H);
+        std::vector<int> heads(L * H, 0);
+        for (int64_t l = 0; l < L; l++)
+            for (int64_t h = 0; h < H; h++)
+                if (m->contact_w[l * H + h] != 0.0f) heads[l * H + m->nz[l]++] = (int)h;
+        int rc = upload(m, m->d_contact_w, m->contact_w.data(), m->contact_w.size());
+        if (!rc) rc = upload(m, m->d_heads, heads.data(), heads.size());
+        if (rc) return fail(rc);
+    }
+    *out = m;
+    return CIH_OK;
+}
+
+int cih_model_create_from_file(const char *path, int32_t quantize_to, const float *contact_w, float contact_b,
+                               cih_model **out) {
+    if (!path || !out) return set_error(CIH_ERR_ARG, "null argument");
+    HostModel hm;
+    if (int rc = load_file(path, hm)) return rc;
+    if (quantize_to == DT_Q8 || quantize_to == DT_Q4) {
+        if (hm.dtype != DT_FP32 && hm.dtype != quantize_to)
+            return set_error(CIH_ERR_ARG, "cannot requantize a dtype %d file to %d", hm.dtype, quantize_to);
+        if (hm.dtype == DT_FP32) quantize_host_model(hm, quantize_to);
+    } else if (quantize_to != -1 && quantize_to != hm.dtype) {
+        return set_error(CIH_ERR_ARG, "bad quantize_to %d", quantize_to);
+    }
+    cih_host_weights w{};
+    const bool q = hm.dtype != DT_FP32;
+    w.token_embedding_table = hm.dtype == DT_Q8 ? (const void *)hm.q.emb.data() : (const void *)hm.f.emb.data();
+    w.ln_1_weight = hm.f.ln1w.data(); w.ln_1_bias = hm.f.ln1b.data();
+    w.wq = q ? (const void *)hm.q.wq.data() : hm.f.wq.data(); w.bq = hm.f.bq.data();
+    w.wk = q ? (const void *)hm.q.wk.data() : hm.f.wk.data(); w.bk = hm.f.bk.data();
+    w.wv = q ? (const void *)hm.q.wv.data() : hm.f.wv.data(); w.bv = hm.f.bv.data();
+    w.wo = q ? (const void *)hm.q.wo.data() : hm.f.wo.data(); w.bo = hm.f.bo.data();
+    w.ln_2_weight = hm.f.ln2w.data(); w.ln_2_bias = hm.f.ln2b.data();
+    w.fc1_weight = q ? (const void *)hm.q.fc1.data() : hm.f.fc1.data(); w.fc1_bias = hm.f.fc1b.data();
+    w.fc2_weight = q ? (const void *)hm.q.fc2.data() : hm.f.fc2.data(); w.fc2_bias = hm.f.fc2b.data();
+    w.ln_f_weight = hm.f.lnfw.data(); w.ln_f_bias = hm.f.lnfb.data();
+    w.classifier_weights = hm.f.cls.data();
+    w.classifier_len = (int64_t)hm.f.cls.size();
+    return cih_model_create(&hm.cfg, hm.dtype, &w, contact_w, contact_b, out);
+}
+
+int cih_model_config(const cih_model *m, cih_config *cfg, int32_t *dtype) {
+    if (!m) return set_error(CIH_ERR_ARG, "null model");
+    if (cfg) *cfg = m->cfg;
+    if (dtype) *dtype = m->dtype;
+    return CIH_OK;
+}
+
+int cih_model_destroy(cih_model *m) {
+    if (!m) return CIH_OK;
+    if (m->stream) hipStreamSynchronize(m->stream);
+    free_workspace(m->ws);
+    free_list(m->allocs);
+    for (auto e : m->prof.ev) hipEventDestroy(e);
+    if (m->stream) hipStreamDestroy(m->stream);
+    delete m;
+    return CIH_OK;
+}
+
+int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint32_t flags) {
+    if (!m) return set_error(CIH_ERR_ARG, "null model");
+    if (max_batch < 1 || max_seq_len < 1) return set_error(CIH_ERR_ARG, "max_batch and max_seq_len must be >= 1");
+    if ((flags & CIH_OUT_CONTACTS) && !m->has_contacts)
+        return set_error(CIH_ERR_ARG, "contacts requested but the model has no contact weights");
+    HIPCHK(hipStreamSynchronize(m->stream));
+    free_workspace(m->ws);
+    Workspace &ws = m->ws;
+    ws.maxB = max_batch;
+    ws.maxS = max_seq_len;
+    ws.flags = flags;
+    const size_t B = max_batch, S = max_seq_len, T = B * S;
+    const size_t d = m->cfg.dim, F = m->cfg.hidden_dim, V = m->cfg.vocab_size, H = m->cfg.n_heads,
+                 L = m->cfg.n_layers, half = m->hd / 2;
+    const size_t n = S >= 2 ? S - 2 : 0;
+    auto &dl = ws.dev;
+    auto ok = [&](hipError_t e) {
+        if (e != hipSuccess) set_error(CIH_ERR_HIP, "workspace allocation failed: %s", hipGetErrorString(e));
+        return e == hipSuccess;
+    };
+    bool good = ok(dalloc(ws.tokens, T, dl)) && ok(dalloc(ws.cu, B, dl)) && ok(dalloc(ws.lens, B, dl)) &&
+                ok(dalloc(ws.x, T * d, dl)) && ok(dalloc(ws.xb, T * d, dl)) && ok(dalloc(ws.qkv, T * 3 * d, dl)) &&
+                ok(dalloc(ws.ao, T * d, dl)) && ok(dalloc(ws.hbuf, T * std::max(F, d), dl)) &&
+                ok(dalloc(ws.logits, T * V, dl)) && ok(dalloc(ws.rope_c, S * half, dl)) &&
+                ok(dalloc(ws.rope_s, S * half, dl));
+    const bool need_P = flags & (CIH_OUT_CONTACTS | CIH_OUT_FINAL_ATT | CIH_OUT_ATTN);
+    if (good && need_P) good = ok(dalloc(ws.P, B * H * S * S, dl));
+    if (good && (flags & CIH_OUT_CONTACTS))
+        good = ok(dalloc(ws.M, B * n * n, dl)) && ok(dalloc(ws.r, L * H * B * n, dl)) &&
+               ok(dalloc(ws.coef, L * H * B, dl));
+    if (good && !(flags & CIH_IO_DEVICE)) {
+        if (flags & CIH_OUT_LOGITS) good = good && ok(dalloc(ws.o_logits, T * V, dl));
+        if (flags & CIH_OUT_HIDDEN) good = good && ok(dalloc(ws.o_hidden, T * d, dl));
+        if (flags & CIH_OUT_FINAL_ATT) good = good && ok(dalloc(ws.o_final, B * S * S, dl));
+        if (flags & CIH_OUT_CONTACTS) good = good && ok(dalloc(ws.o_contacts, B * n * n, dl));
+        if (flags & CIH_OUT_ATTN) good = good && ok(dalloc(ws.o_attn, B * L * H * S * S, dl));
+        if (flags & CIH_OUT_LAYER_HIDDEN) good = good && ok(dalloc(ws.o_layer, B * L * S * d, dl));
+    }
+    if (good) {
+        void *hp = nullptr;
+        if (!ok(hipHostMalloc(&hp, 2 * B * sizeof(int)))) good = false;
+        else { ws.host.push_back(hp); ws.h_meta = (int *)hp; }
+    }
+    if (!good) {
+        free_workspace(ws);
+        return CIH_ERR_HIP;
+    }
+    // RoPE tables (BidirectionalRunState::new, lib.rs:2513-2522): the same f32
+    // powf / cos / sin calls, evaluated on the host.
+    std::vector<float> c(S * half), s(S * half);
+    for (size_t pos = 0; pos < S; pos++)
+        for (size_t j = 0; j < half; j++) {
+            const float freq = 1.0f / std::pow(10000.0f, (float)(j * 2) / (float)m->hd);
+            const float val = (float)pos * freq;
+            c[pos * half + j] = std::cos(val);
+            s[pos * half + j] = std::sin(val);
+        }
+    HIPCHK(hipMemcpy(ws.rope_c, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(ws.rope_s, s.data(), s.size() * 4, hipMemcpyHostToDevice));
+    return CIH_OK;
+}
+
+int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B, int32_t S_max, uint32_t flags,
+                const cih_outputs *out) {
+    if (!m || !tokens || !lens || !out) return set_error(CIH_ERR_ARG, "null argument");
+    Workspace &ws = m->ws;
+    if (ws.maxB == 0) return set_error(CIH_ERR_CAPACITY, "cih_model_reserve has not been called");
+    if (B < 1 || S_max < 1) return set_error(CIH_ERR_ARG, "B and S_max must be >= 1");
+    if (B > ws.maxB || S_max > ws.maxS)
+        return set_error(CIH_ERR_CAPACITY, "batch %d x %d exceeds the reserved %d x %d", B, S_max, ws.maxB, ws.maxS);
+    const uint32_t kinds = flags & 0xFFFFu;
+    if (kinds & ~ws.flags & 0x3Fu) return set_error(CIH_ERR_CAPACITY, "output kinds 0x%x were not reserved", kinds);
+    const bool dev_io = flags & CIH_IO_DEVICE;
+    if (!dev_io && (ws.flags & CIH_IO_DEVICE) && (kinds & 0x3Fu))
+        return set_error(CIH_ERR_CAPACITY, "workspace reserved for device I/O only");
+    const bool want_logits = kinds & CIH_OUT_LOGITS, want_hidden = kinds & CIH_OUT_HIDDEN,
+               want_final = kinds & CIH_OUT_FINAL_ATT, want_contacts = kinds & CIH_OUT_CONTACTS,
+               want_attn = kinds & CIH_OUT_ATTN, want_layer = kinds & CIH_OUT_LAYER_HIDDEN;
+    if ((want_logits && !out->logits) || (want_hidden && !out->hidden) || (want_final && !out->final_att) ||
+        (want_contacts && !out->contacts) || (want_attn && !out->attn) || (want_layer && !out->layer_hidden))
+        return set_error(CIH_ERR_ARG, "null output buffer for a requested output");
+
+    const int d = m->cfg.dim, F = m->cfg.hidden_dim, V = m->cfg.vocab_size, H = m->cfg.n_heads, L = m->cfg.n_layers;
+    int *cu = ws.h_meta, *hl = ws.h_meta + ws.maxB;
+    int T = 0;
+    for (int b = 0; b < B; b++) {
+        if (lens[b] < 1 || lens[b] > S_max)
+            return set_error(CIH_ERR_ARG, "lens[%d] = %d outside [1, %d]", b, lens[b], S_max);
+        // accumulate_head_apc's row_sums is [f32; 1024] (lib.rs:5046)
+        if (want_contacts && lens[b] - 2 > 1024)
+            return set_error(CIH_ERR_CONTACTS, "contacts need n_res <= 1024 (sequence %d has %d)", b, lens[b] - 2);
+        cu[b] = T;
+        hl[b] = lens[b];
+        T += lens[b];
+    }
+    if (!dev_io) {
+        for (int b = 0; b < B; b++)
+            for (int s = 0; s < lens[b]; s++) {
+                const int t = tokens[(size_t)b * S_max + s];
+                if (t < 0 || t >= V) return set_error(CIH_ERR_TOKEN, "token %d at [%d][%d] outside [0, %d)", t, b, s, V);
+            }
+    }
+    hipStream_t st = m->stream;
+    const int n_max = S_max >= 2 ? S_max - 2 : 0;
+    const size_t SS = (size_t)S_max * S_max;
+
+    HIPCHK(hipMemcpyAsync(ws.tokens, tokens, (size_t)B * S_max * 4, dev_io ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(ws.cu, cu, B * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(ws.lens, hl, B * 4, hipMemcpyHostToDevice, st));
+    const SeqMeta sm{ws.cu, ws.lens, B, S_max};
+
+    // output targets on the device (caller's buffers or staging)
+    float *t_logits = dev_io ? out->logits : ws.o_logits, *t_hidden = dev_io ? out->hidden : ws.o_hidden,
+          *t_final = dev_io ? out->final_att : ws.o_final, *t_contacts = dev_io ? out->contacts : ws.o_contacts,
+          *t_attn = dev_io ? out->attn : ws.o_attn, *t_layer = dev_io ? out->layer_hidden : ws.o_layer;
+
+    m->prof.used = 0;
+    {
+        ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
+        HIPCHK(launch_embed(ws.tokens, sm, m->emb.fmt, m->emb.q, m->emb.sc, d, V, ws.x, st));
+    }
+    if (want_contacts) HIPCHK(hipMemsetAsync(ws.M, 0, (size_t)B * n_max * n_max * 4, st));
+
+    for (int l = 0; l < L; l++) {
+        const Layer &ly = m->layers[l];
+        {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
+            HIPCHK(launch_layernorm(ws.x, ly.ln1w, ly.ln1b, ws.xb, T, d, st));
+        }
+        HIPCHK(gemm(m, ly.wqkv, ws.xb, d, ly.bqkv, ws.qkv, 3 * d, T, EPI_NONE));
+        // probabilities: straight into the attention-map output when exported
+        float *P = nullptr;
+        int64_t pb = 0, ph = SS;
+        const bool need_P = want_attn || want_contacts || (want_final && l == L - 1);
+        if (want_attn) {
+            P = t_attn + (size_t)l * H * SS;
+            pb = (int64_t)L * H * SS;
+        } else if (need_P) {
+            P = ws.P;
+            pb = (int64_t)H * SS;
+        }
+        {
+            double fl = 0;
+            for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
+            ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
+            HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, P, pb, ph, st));
+        }
+        if (want_contacts && m->nz[l] > 0) {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 0);
+            HIPCHK(launch_apc_layer(P, pb, ph, H, l, m->d_contact_w, m->d_heads + (size_t)l * H, m->nz[l], sm, ws.M,
+                                    ws.r, st));
+        }
+        if (want_final && l == L - 1) {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 0);
+            HIPCHK(launch_head_mean(P, pb, ph, H, sm, t_final, st));
+        }
+        HIPCHK(gemm(m, ly.wo, ws.ao, d, ly.bo, ws.x, d, T, EPI_RESIDUAL));
+        {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
+            HIPCHK(launch_layernorm(ws.x, ly.ln2w, ly.ln2b, ws.xb, T, d, st));
+        }
+        HIPCHK(gemm(m, ly.w1, ws.xb, d, ly.b1, ws.hbuf, F, T, EPI_GELU));
+        HIPCHK(gemm(m, ly.w2, ws.hbuf, F, ly.b2, ws.x, d, T, EPI_RESIDUAL));
+        if (want_layer) HIPCHK(launch_scatter_rows(ws.x, d, sm, t_layer + (size_t)l * S_max * d, (int64_t)L * S_max * d, st));
+    }
+    if (want_contacts) {
+        ProfScope ps(m, CIH_KC_OTHER, 0, 0);
+        HIPCHK(launch_apc_finalize(ws.M, ws.r, ws.coef, m->d_contact_w, L * H, sm, m->contact_b, t_contacts, n_max, st));
+    }
+    // final LayerNorm: state.x = LN_f(x) (lib.rs:5379-5387)
+    {
+        ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
+        HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, T, d, st));
+    }
+    if (want_hidden) HIPCHK(launch_scatter_rows(ws.ao, d, sm, t_hidden, (int64_t)S_max * d, st));
+    if (want_logits) {
+        if (m->has_head) {
+            HIPCHK(gemm(m, m->dense, ws.ao, d, m->dense_b, ws.hbuf, d, T, EPI_GELU));
+            {
+                ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
+                HIPCHK(launch_layernorm(ws.hbuf, m->lm_lnw, m->lm_lnb, ws.xb, T, d, st));
+            }
+            HIPCHK(gemm(m, m->dec, ws.xb, d, m->dec_b, ws.logits, V, T, EPI_NONE));
+        } else {
+            HIPCHK(gemm(m, m->emb, ws.ao, d, nullptr, ws.logits, V, T, EPI_NONE));
+        }
+        HIPCHK(launch_scatter_rows(ws.logits, V, sm, t_logits, (int64_t)S_max * V, st));
+    }
+    HIPCHK(hipStreamSynchronize(st));
+
+    if (!dev_io) {
+        auto rows_out = [&](float *dst, const float *src, int width, int64_t bstride) -> int {
+            for (int b = 0; b < B; b++)
+                HIPCHK(hipMemcpy(dst + b * bstride, src + b * bstride, (size_t)lens[b] * width * 4,
+                                 hipMemcpyDeviceToHost));
+            return 0;
+        };
+        auto square_out = [&](float *dst, const float *src, int nb, int stride, int64_t off) -> int {
+            if (nb <= 0) return 0;
+            HIPCHK(hipMemcpy2D(dst + off, (size_t)stride * 4, src + off, (size_t)stride * 4, (size_t)nb * 4, nb,
+                               hipMemcpyDeviceToHost));
+            return 0;
+        };
+        int rc = 0;
+        if (want_logits && (rc = rows_out(out->logits, t_logits, V, (int64_t)S_max * V))) return rc;
+        if (want_hidden && (rc = rows_out(out->hidden, t_hidden, d, (int64_t)S_max * d))) return rc;
+        for (int b = 0; b < B; b++) {
+            if (want_final && (rc = square_out(out->final_att, t_final, lens[b], S_max, (int64_t)b * SS))) return rc;
+            if (want_contacts &&
+                (rc = square_out(out->contacts, t_contacts, lens[b] - 2, n_max, (int64_t)b * n_max * n_max)))
+                return rc;
+            for (int l = 0; l < L; l++) {
+                if (want_layer)
+                    HIPCHK(hipMemcpy(out->layer_hidden + ((int64_t)b * L + l) * S_max * d,
+                                     t_layer + ((int64_t)b * L + l) * S_max * d, (size_t)lens[b] * d * 4,
+                                     hipMemcpyDeviceToHost));
+                for (int h = 0; want_attn && h < H; h++)
+                    if ((rc = square_out(out->attn, t_attn, lens[b], S_max, (((int64_t)b * L + l) * H + h) * SS)))
+                        return rc;
+            }
+        }
+    }
+    if (m->prof.on) {
+        for (size_t i = 0; i < m->prof.used; i++) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, m->prof.ev[2 * i], m->prof.ev[2 * i + 1]) != hipSuccess) continue;
+            cih_kernel_stats &s = m->prof.st[m->prof.cls[i]];
+            s.launches++;
+            s.total_ms += ms;
+            s.flops += m->prof.flops[i];
+            s.bytes += m->prof.bytes[i];
+        }
+    }
+    return CIH_OK;
+}
+
+int cih_profile_enable(cih_model *m, int32_t enable) {
+    if (!m) return set_error(CIH_ERR_ARG, "null model");
+    m->prof.on = enable != 0;
+    for (auto &s : m->prof.st) s = cih_kernel_stats{};
+    return CIH_OK;
+}
+
+int cih_profile_read(const cih_model *m, int32_t kc, cih_kernel_stats *out) {
+    if (!m || !out || kc < 0 || kc >= CIH_KC_COUNT) return set_error(CIH_ERR_ARG, "bad argument");
+    *out = m->prof.st[kc];
+    return CIH_OK;
+}
+
+// ---- kernel-level entry points ------------------------------------------------
+
+int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w, const float *bias, int32_t in_dim,
+                     int32_t out_dim, int32_t seq_len) {
+    if (!out || !x || !w || !bias) return set_error(CIH_ERR_ARG, "null argument");
+    if (in_dim <= 0 || out_dim <= 0 || seq_len < 0 || in_dim % 32)
+        return set_error(CIH_ERR_SHAPE, "bad GEMM shape %d x %d x %d", seq_len, out_dim, in_dim);
+    if (dtype != DT_FP32 && dtype != DT_Q8 && dtype != DT_Q4) return set_error(CIH_ERR_ARG, "bad dtype");
+    if (seq_len == 0) return CIH_OK;
+    cih_model tmp;  // owns the temporary allocations
+    int rc = upload_matrix(&tmp, dtype, in_dim, {{w, out_dim}}, tmp.emb);
+    float *dx = nullptr, *db = nullptr, *dy = nullptr;
+    if (!rc) rc = upload(&tmp, dx, x, (size_t)seq_len * in_dim);
+    if (!rc) rc = upload(&tmp, db, bias, (size_t)out_dim);
+    if (!rc && dalloc(dy, (size_t)seq_len * out_dim, tmp.allocs) != hipSuccess)
+        rc = set_error(CIH_ERR_HIP, "allocation failed");
+    if (!rc) {
+        hipError_t e = launch_gemm(tmp.emb, dx, in_dim, db, dy, out_dim, seq_len, EPI_NONE, nullptr);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = hipMemcpy(out, dy, (size_t)seq_len * out_dim * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = set_error(CIH_ERR_HIP, "GEMM failed: %s", hipGetErrorString(e));
+    }
+    free_list(tmp.allocs);
+    return rc;
+}
+
+int cih_dequantize_device(int32_t dtype, const void *blocks, int64_t nblocks, float *out) {
+    if (!blocks || !out || nblocks < 0) return set_error(CIH_ERR_ARG, "bad argument");
+    if (dtype != DT_Q8 && dtype != DT_Q4) return set_error(CIH_ERR_ARG, "dtype must be Q8_0 or Q4_0");
+    if (nblocks == 0) return CIH_OK;
+    if (nblocks > (int64_t)1 << 30) return set_error(CIH_ERR_SHAPE, "too many blocks");
+    // one row of nblocks blocks: K = 32 * nblocks, N = 1
+    cih_model tmp;
+    int rc = upload_matrix(&tmp, dtype, (int)(nblocks * 32), {{blocks, 1}}, tmp.emb);
+    float *dy = nullptr;
+    if (!rc && dalloc(dy, (size_t)nblocks * 32, tmp.allocs) != hipSuccess) rc = set_error(CIH_ERR_HIP, "alloc failed");
+    if (!rc) {
+        hipError_t e = launch_dequant(tmp.emb, dy, nullptr);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = hipMemcpy(out, dy, (size_t)nblocks * 32 * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = set_error(CIH_ERR_HIP, "dequantize failed: %s", hipGetErrorString(e));
+    }
+    free_list(tmp.allocs);
+    return rc;
+}
+
+// ---- host helpers ----------------------------------------------------------------
+
+int cih_quantize_q8(const float *src, int64_t n, void *dst) {
+    if (!src || !dst || n < 0 || n % 32) return set_error(CIH_ERR_ARG, "n must be a non-negative multiple of 32");
+    quantize_matrix(DT_Q8, src, n, (uint8_t *)dst);
+    return CIH_OK;
+}
+
+int cih_quantize_q4(const float *src, int64_t n, void *dst) {
+    if (!src || !dst || n < 0 || n % 32) return set_error(CIH_ERR_ARG, "n must be a non-negative multiple of 32");
+    quantize_matrix(DT_Q4, src, n, (uint8_t *)dst);
+    return CIH_OK;
+}
+
+int cih_dequantize_q8(const void *blocks, int64_t nblocks, float *dst) {
+    if (!blocks || !dst || nblocks < 0) return set_error(CIH_ERR_ARG, "bad argument");
+    for (int64_t b = 0; b < nblocks; b++) dequantize_q8_block((const uint8_t *)blocks + b * 36, dst + b * 32);
+    return CIH_OK;
+}
+
+int cih_dequantize_q4(const void *blocks, int64_t nblocks, float *dst) {
+    if (!blocks || !dst || nblocks < 0) return set_error(CIH_ERR_ARG, "bad argument");
+    for (int64_t b = 0; b < nblocks; b++) dequantize_q4_block((const uint8_t *)blocks + b * 20, dst + b * 32);
+    return CIH_OK;
+}
+
+int cih_tokenize(const char *text, int32_t *out, int32_t cap) {
+    if (!text || !out) return set_error(CIH_ERR_ARG, "null argument");
+    const int n = tokenize(text, out, cap);
+    return n < 0 ? set_error(CIH_ERR_ARG, "output capacity %d too small", cap) : n;
+}
+
+int cih_log_softmax_canonical(const float *logits, float *out33) {
+    if (!logits || !out33) return set_error(CIH_ERR_ARG, "null argument");
+    log_softmax_canonical(logits, out33);
+    return CIH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,206 @@
+// Bidirectional rotary multi-head attention for gfx950 (FP32 MFMA).
+//
+// Replaces the per-head, per-query loops of forward_bidirectional*
+// (codon-infer src/lib.rs:5206-5301; Q8 5558-5653; Q4 ~5905-6005) together
+// with apply_rope (3533-3552), softmax (3500-3504) and the dot/axpy
+// micro-kernels (3292-3434):
+//   s_t = (q_p . k_t) * (1/sqrt(hd)) over every key t of the same sequence,
+//   P = softmax(s), o_p = sum_t P_pt v_t.
+// Sequences are packed back to back (row cu[b] + position); keys past a
+// sequence's length are masked, so each sequence sees exactly the keys the
+// reference's unpadded call sees.
+//
+// One workgroup = (query block of 128, head, sequence); 4 waves x 32
+// queries.  Scores are computed transposed, S^T = K Q^T, with
+// v_mfma_f32_32x32x2_f32 so that each lane holds one query column and 16
+// keys: the softmax reductions are lane-local plus one swap between the two
+// lane halves, and the probabilities feed the P.V MFMA (O^T = V^T P^T) as the
+// B operand straight from the accumulator registers: register s of lane
+// (j, half) holds key 8*(s/4) + 4*half + s%4, which is the k index that lane
+// supplies at step s.
+// Two passes over the keys: pass 1 keeps a running max/sum per lane, pass 2
+// recomputes the scores, forms p = exp(s - max) * (1/sum) exactly as the
+// reference does, optionally stores P, and accumulates P.V.
+// RoPE is applied while staging K into LDS and Q into registers, from the
+// host-built cos/sin tables (the reference's f32 powf/cos/sin values).
+#include "kernels.h"
+
+namespace cih {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
+                                                   const int *__restrict__ lens, int S_max,
+                                                   const float *__restrict__ rc, const float *__restrict__ rsn,
+                                                   float *__restrict__ out, float *__restrict__ P, long long pb,
+                                                   long long ph, float inv_scale) {
+    constexpr int HALF = HD / 2;
+    constexpr int VW = HD < 32 ? 32 : HD;  // V tile width, zero padded for small heads
+    constexpr int DT = VW / 32;            // 32-wide output tiles
+    constexpr int K_LD = HD + 4;
+    constexpr int V_LD = VW + 4;
+    __shared__ __attribute__((aligned(16))) float Ks[32 * K_LD];
+    __shared__ __attribute__((aligned(16))) float Vs[32 * V_LD];
+
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int len = lens[b], base = cu[b];
+    const int qblk = blockIdx.x * 128;
+    if (qblk >= len) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, hh = lane >> 5;
+    const size_t ld = (size_t)3 * d;
+    const float *Qg = qkv + h * HD;
+    const float *Kg = qkv + d + h * HD;
+    const float *Vg = qkv + 2 * d + h * HD;
+
+    const int qi = qblk + wave * 32 + li;
+    const int qc = min(qi, len - 1);
+    float qr[HALF];
+    {
+        const float *qrow = Qg + (size_t)(base + qc) * ld;
+        const float *cs = rc + (size_t)qc * HALF, *sn = rsn + (size_t)qc * HALF;
+#pragma unroll
+        for (int s = 0; s < HALF; s++) {
+            const float q0 = qrow[s], q1 = qrow[s + HALF];
+            qr[s] = hh == 0 ? q0 * cs[s] - q1 * sn[s] : q1 * cs[s] + q0 * sn[s];
+        }
+    }
+
+    auto load_k = [&](int kt0) {
+        for (int idx = tid; idx < 32 * HALF; idx += 256) {
+            const int key = idx / HALF, c = idx % HALF;
+            const int kk = min(kt0 + key, len - 1);
+            const float *krow = Kg + (size_t)(base + kk) * ld;
+            const float k0 = krow[c], k1 = krow[c + HALF];
+            const float cs = rc[(size_t)kk * HALF + c], sn = rsn[(size_t)kk * HALF + c];
+            Ks[key * K_LD + c] = k0 * cs - k1 * sn;
+            Ks[key * K_LD + c + HALF] = k1 * cs + k0 * sn;
+        }
+    };
+    auto load_v = [&](int kt0) {
+        for (int idx = tid; idx < 32 * VW; idx += 256) {
+            const int key = idx / VW, c = idx % VW;
+            const int kk = min(kt0 + key, len - 1);
+            Vs[key * V_LD + c] = c < HD ? Vg[(size_t)(base + kk) * ld + c] : 0.0f;
+        }
+    };
+    auto scores = [&](f32x16 &acc) {
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[q] = 0.0f;
+        const float *kr = &Ks[li * K_LD + hh * HALF];
+#pragma unroll
+        for (int s4 = 0; s4 < HALF / 4; s4++) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(kr + 4 * s4);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.x, qr[4 * s4 + 0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.y, qr[4 * s4 + 1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.z, qr[4 * s4 + 2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.w, qr[4 * s4 + 3], acc, 0, 0, 0);
+        }
+    };
+
+    // ---- pass 1: running max / sum of exp per lane (16 keys per tile)
+    float m = -INFINITY, l = 0.0f;
+    for (int kt0 = 0; kt0 < len; kt0 += 32) {
+        __syncthreads();
+        load_k(kt0);
+        __syncthreads();
+        f32x16 acc;
+        scores(acc);
+        float sv[16];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+            sv[q] = key < len ? acc[q] * inv_scale : -INFINITY;
+            tmax = fmaxf(tmax, sv[q]);
+        }
+        const float mn = fmaxf(m, tmax);
+        if (mn != -INFINITY) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) sum += expf(sv[q] - mn);
+            l = l * expf(m - mn) + sum;
+            m = mn;
+        }
+    }
+    const float mo = __shfl_xor(m, 32), lo = __shfl_xor(l, 32);
+    const float mx = fmaxf(m, mo);
+    const float tot = l * expf(m - mx) + lo * expf(mo - mx);
+    const float inv_sum = 1.0f / tot;
+
+    // ---- pass 2: normalized probabilities, optional export, P.V
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
+    float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+    for (int kt0 = 0; kt0 < len; kt0 += 32) {
+        __syncthreads();
+        load_k(kt0);
+        load_v(kt0);
+        __syncthreads();
+        f32x16 acc;
+        scores(acc);
+        float p[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+            p[q] = key < len ? expf(acc[q] * inv_scale - mx) * inv_sum : 0.0f;
+        }
+        if (Prow) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                if (key < len) Prow[key] = p[q];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+#pragma unroll
+            for (int s = 0; s < 16; s++) {
+                const float v = Vs[(8 * (s >> 2) + 4 * hh + (s & 3)) * V_LD + t * 32 + li];
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, p[s], oacc[t], 0, 0, 0);
+            }
+        }
+    }
+    if (qi < len) {
+        float *orow = out + (size_t)(base + qi) * d + h * HD;
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int dd = t * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                if (dd < HD) orow[dd] = oacc[t][q];
+            }
+    }
+}
+
+hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos, const float *rope_sin,
+                            float *out, float *P, int64_t pb, int64_t ph, hipStream_t st) {
+    const int hd = d / H;
+    const float inv_scale = 1.0f / sqrtf((float)hd);
+    dim3 grid((sm.S_max + 127) / 128, H, sm.B);
+    switch (hd) {
+    case 16:
+        hipLaunchKernelGGL(k_attention<16>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
+                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+        break;
+    case 24:
+        hipLaunchKernelGGL(k_attention<24>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
+                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+        break;
+    case 32:
+        hipLaunchKernelGGL(k_attention<32>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
+                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+        break;
+    case 64:
+        hipLaunchKernelGGL(k_attention<64>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
+                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace cih

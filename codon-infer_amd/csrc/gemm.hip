@@ -1,0 +1,329 @@
+// Dequantizing GEMMs for gfx950: Y = epi(X * W^T + b) on FP32 MFMA.
+//
+// Replaces matmul_tiled_{fp32,q8,q4}_parallel (codon-infer src/lib.rs:4766-4961).
+// The reference unpacks each weight row to FP32 as (float)q * d
+// (lib.rs:4687, 4724-4741) and runs an FP32 FMA dot product per token; this
+// kernel forms the same FP32 weights in registers (one f32 multiply of the
+// exact integer by the block scale) and feeds them, with FP32 activations, to
+// v_mfma_f32_32x32x2_f32.  Products are exact-precision FP32; only the
+// summation order differs from the CPU path.
+//
+// Tiling: 256 threads = 4 waves (2x2), workgroup tile BM x BN, BK = 32 (one
+// quantization block).  Each wave owns (BM/2) x (BN/2) outputs as 32x32 MFMA
+// tiles.  Within a k-block, lane (i = lane%32, half = lane/32) feeds k-slot
+// `half` with k = half*16 + s at step s; for Q4_0 that makes half 0 read the
+// low nibbles and half 1 the high nibbles of the same 16 bytes, which is the
+// reference's packing (element j low, element j+16 high, lib.rs:1064-1068).
+// A and the raw quantized B tile are double-buffered in LDS; the next k-block
+// is fetched into registers while the current one is multiplied.
+#include "kernels.h"
+
+namespace cih {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// erf_f32 (lib.rs:3485-3491, Abramowitz & Stegun 7.1.26) and gelu (3493-3498)
+__device__ __forceinline__ float erf_as(float x) {
+    float sign = x < 0.0f ? -1.0f : 1.0f;
+    float ax = fabsf(x);
+    float t = 1.0f / (1.0f + 0.3275911f * ax);
+    float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                       0.254829592f) * t * expf(-ax * ax);
+    return sign * y;
+}
+__device__ __forceinline__ float gelu_ref(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f)); }
+
+constexpr int A_LD = 36;    // floats per LDS row of the A tile (32 + 4 pad: conflict-free b128 reads)
+constexpr int F32_LD = 36;  // same for FP32 weight rows
+constexpr int Q8_LD = 48;   // bytes per LDS column of Q8 quants (32 + 16 pad)
+constexpr int Q4_LD = 16;   // bytes per LDS column of Q4 quants
+
+template <int WF, int BN>
+struct BTileBytes {
+    static constexpr int value = WF == WF_F32 ? BN * F32_LD * 4 : (WF == WF_Q8 ? BN * Q8_LD : BN * Q4_LD);
+};
+
+// Tile order: bijective remap so that the workgroups the dispatcher sends to
+// one XCD (round-robin over 8) are consecutive in tile order, then grouped
+// rows (GROUP_M row tiles swept across N) so concurrently resident tiles
+// share A rows and B columns in that XCD's L2.
+__device__ __forceinline__ void tile_of(int bid, int total, int nM, int nN, int &mt, int &nt) {
+    constexpr int XCD = 8, GROUP_M = 8;
+    int xcd = bid % XCD, local = bid / XCD;
+    int per = total / XCD, rem = total % XCD;
+    int id = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    int in_group = GROUP_M * nN;
+    int g = id / in_group;
+    int first = g * GROUP_M;
+    int gsize = min(nM - first, GROUP_M);
+    int r = id % in_group;
+    mt = first + r % gsize;
+    nt = r / gsize;
+}
+
+template <int WF, int EPI, int BM, int BN>
+__global__ __launch_bounds__(256, 2) void k_gemm(const float *__restrict__ X, int ldx, const void *__restrict__ Wq,
+                                                 const float *__restrict__ Wsc, const float *__restrict__ bias,
+                                                 float *__restrict__ Y, int ldy, int M, int N, int K) {
+    constexpr int MT = BM / 64;  // 32-row MFMA tiles per wave
+    constexpr int NT = BN / 64;  // 32-col MFMA tiles per wave
+    constexpr int A_LOADS = BM / 32;  // float4 per thread for the A tile
+    constexpr int BBYTES = BTileBytes<WF, BN>::value;
+    __shared__ __attribute__((aligned(16))) float As[2][BM * A_LD];
+    __shared__ __attribute__((aligned(16))) unsigned char Bs[2][BBYTES];
+    __shared__ float Ss[2][BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 31, hh = lane >> 5;
+    const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+    int mt, nt;
+    tile_of(blockIdx.x, nM * nN, nM, nN, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int KB = K / 32;
+
+    // ---- global -> register prefetch state
+    float4 ra[A_LOADS];
+    constexpr int B_LOADS = WF == WF_F32 ? (BN * 8 + 255) / 256 : (WF == WF_Q8 ? (BN * 2 + 255) / 256 : (BN + 255) / 256);
+    uint4 rb[B_LOADS];
+    float rs = 0.0f;
+
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; i++) {
+            int row = (tid >> 3) + 32 * i, c4 = tid & 7;
+            int gr = m0 + row;
+            ra[i] = gr < M ? *reinterpret_cast<const float4 *>(X + (size_t)gr * ldx + kb * 32 + c4 * 4)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if constexpr (WF == WF_F32) {
+            const float *w = reinterpret_cast<const float *>(Wq) + (size_t)kb * N * 32;
+#pragma unroll
+            for (int i = 0; i < B_LOADS; i++) {
+                int idx = tid + 256 * i, col = idx >> 3, c4 = idx & 7;
+                int gc = n0 + col;
+                rb[i] = (col < BN && gc < N) ? *reinterpret_cast<const uint4 *>(w + (size_t)gc * 32 + c4 * 4)
+                                             : make_uint4(0, 0, 0, 0);
+            }
+        } else if constexpr (WF == WF_Q8) {
+            const unsigned char *w = reinterpret_cast<const unsigned char *>(Wq) + (size_t)kb * N * 32;
+#pragma unroll
+            for (int i = 0; i < B_LOADS; i++) {
+                int idx = tid + 256 * i, col = idx >> 1, half = idx & 1;
+                int gc = n0 + col;
+                rb[i] = (col < BN && gc < N) ? *reinterpret_cast<const uint4 *>(w + (size_t)gc * 32 + half * 16)
+                                             : make_uint4(0, 0, 0, 0);
+            }
+        } else {
+            const unsigned char *w = reinterpret_cast<const unsigned char *>(Wq) + (size_t)kb * N * 16;
+#pragma unroll
+            for (int i = 0; i < B_LOADS; i++) {
+                int col = tid + 256 * i;
+                int gc = n0 + col;
+                rb[i] = (col < BN && gc < N) ? *reinterpret_cast<const uint4 *>(w + (size_t)gc * 16)
+                                             : make_uint4(0, 0, 0, 0);
+            }
+        }
+        if constexpr (WF != WF_F32) {
+            int gc = n0 + tid;
+            rs = (tid < BN && gc < N) ? Wsc[(size_t)kb * N + gc] : 0.0f;
+        }
+    };
+
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; i++) {
+            int row = (tid >> 3) + 32 * i, c4 = tid & 7;
+            *reinterpret_cast<float4 *>(&As[buf][row * A_LD + c4 * 4]) = ra[i];
+        }
+        if constexpr (WF == WF_F32) {
+#pragma unroll
+            for (int i = 0; i < B_LOADS; i++) {
+                int idx = tid + 256 * i, col = idx >> 3, c4 = idx & 7;
+                if (col < BN) *reinterpret_cast<uint4 *>(&Bs[buf][(col * F32_LD + c4 * 4) * 4]) = rb[i];
+            }
+        } else if constexpr (WF == WF_Q8) {
+#pragma unroll
+            for (int i = 0; i < B_LOADS; i++) {
+                int idx = tid + 256 * i, col = idx >> 1, half = idx & 1;
+                if (col < BN) *reinterpret_cast<uint4 *>(&Bs[buf][col * Q8_LD + half * 16]) = rb[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < B_LOADS; i++) {
+                int col = tid + 256 * i;
+                if (col < BN) *reinterpret_cast<uint4 *>(&Bs[buf][col * Q4_LD]) = rb[i];
+            }
+        }
+        if constexpr (WF != WF_F32) {
+            if (tid < BN) Ss[buf][tid] = rs;
+        }
+    };
+
+    f32x16 acc[MT][NT];
+#pragma unroll
+    for (int r = 0; r < MT; r++)
+#pragma unroll
+        for (int c = 0; c < NT; c++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+
+    for (int kb = 0; kb < KB; kb++) {
+        const int cur = kb & 1;
+        if (kb + 1 < KB) gload(kb + 1);
+
+        float a[MT][16];
+#pragma unroll
+        for (int r = 0; r < MT; r++) {
+            const float *src = &As[cur][(wm * (BM / 2) + r * 32 + li) * A_LD + hh * 16];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                float4 t = *reinterpret_cast<const float4 *>(src + 4 * v);
+                a[r][4 * v + 0] = t.x; a[r][4 * v + 1] = t.y; a[r][4 * v + 2] = t.z; a[r][4 * v + 3] = t.w;
+            }
+        }
+        float b[NT][16];
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const int col = wn * (BN / 2) + c * 32 + li;
+            if constexpr (WF == WF_F32) {
+                const float *src = reinterpret_cast<const float *>(&Bs[cur][0]) + col * F32_LD + hh * 16;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    float4 t = *reinterpret_cast<const float4 *>(src + 4 * v);
+                    b[c][4 * v + 0] = t.x; b[c][4 * v + 1] = t.y; b[c][4 * v + 2] = t.z; b[c][4 * v + 3] = t.w;
+                }
+            } else if constexpr (WF == WF_Q8) {
+                const uint4 raw = *reinterpret_cast<const uint4 *>(&Bs[cur][col * Q8_LD + hh * 16]);
+                const float d = Ss[cur][col];
+                const unsigned w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        b[c][4 * v + e] = (float)(signed char)((w4[v] >> (8 * e)) & 0xFF) * d;
+            } else {
+                const uint4 raw = *reinterpret_cast<const uint4 *>(&Bs[cur][col * Q4_LD]);
+                const float d = Ss[cur][col];
+                const unsigned w4[4] = {raw.x, raw.y, raw.z, raw.w};
+                const int sh = hh * 4;
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        b[c][4 * v + e] = (float)((int)((w4[v] >> (8 * e + sh)) & 0xF) - 8) * d;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; s++)
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int c = 0; c < NT; c++)
+                    acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[r][s], b[c][s], acc[r][c], 0, 0, 0);
+
+        if (kb + 1 < KB) sstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: lane holds column li of each 32x32 tile, rows 8*(q/4) + 4*hh + q%4
+#pragma unroll
+    for (int c = 0; c < NT; c++) {
+        const int col = n0 + wn * (BN / 2) + c * 32 + li;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < MT; r++) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                if (row < M) {
+                    float v = acc[r][c][q] + bv;
+                    float *dst = Y + (size_t)row * ldy + col;
+                    if constexpr (EPI == EPI_GELU) v = gelu_ref(v);
+                    if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+                    *dst = v;
+                }
+            }
+        }
+    }
+}
+
+template <int WF, int EPI, int BM, int BN>
+static hipError_t launch_t(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
+                           hipStream_t st) {
+    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN;
+    hipLaunchKernelGGL((k_gemm<WF, EPI, BM, BN>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc, bias, Y, ldy, M,
+                       W.N, W.K);
+    return hipGetLastError();
+}
+
+template <int WF, int EPI>
+static hipError_t launch_shape(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
+                               int M, hipStream_t st) {
+    const bool small_m = M <= 64, small_n = W.N <= 64;
+    if (small_m && small_n) return launch_t<WF, EPI, 64, 64>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_m) return launch_t<WF, EPI, 64, 128>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_n) return launch_t<WF, EPI, 128, 64>(W, X, ldx, bias, Y, ldy, M, st);
+    return launch_t<WF, EPI, 128, 128>(W, X, ldx, bias, Y, ldy, M, st);
+}
+
+template <int WF>
+static hipError_t launch_epi(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
+                             int epi, hipStream_t st) {
+    switch (epi) {
+    case EPI_GELU: return launch_shape<WF, EPI_GELU>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_RESIDUAL: return launch_shape<WF, EPI_RESIDUAL>(W, X, ldx, bias, Y, ldy, M, st);
+    default: return launch_shape<WF, EPI_NONE>(W, X, ldx, bias, Y, ldy, M, st);
+    }
+}
+
+hipError_t launch_gemm(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
+                       int epi, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    if (W.K % 32 != 0 || ldx % 4 != 0) return hipErrorInvalidValue;
+    switch (W.fmt) {
+    case WF_Q8: return launch_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    case WF_Q4: return launch_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    default: return launch_epi<WF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    }
+}
+
+// Test path: k-block-major device matrix -> row-major [N][K] FP32, with the
+// exact decode expression the GEMM uses.
+__global__ void k_dequant(int fmt, const void *__restrict__ q, const float *__restrict__ sc, int N, int K,
+                          float *__restrict__ out) {
+    const int KB = K / 32;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // (kb, n, e)
+    const size_t total = (size_t)KB * N * 32;
+    if (idx >= total) return;
+    const int e = idx % 32;
+    const int n = (idx / 32) % N;
+    const int kb = idx / ((size_t)32 * N);
+    float v;
+    if (fmt == WF_Q8) {
+        const signed char qv = reinterpret_cast<const signed char *>(q)[((size_t)kb * N + n) * 32 + e];
+        v = (float)qv * sc[(size_t)kb * N + n];
+    } else if (fmt == WF_Q4) {
+        const unsigned char byte = reinterpret_cast<const unsigned char *>(q)[((size_t)kb * N + n) * 16 + (e & 15)];
+        const int nib = e < 16 ? (byte & 0xF) : (byte >> 4);
+        v = (float)(nib - 8) * sc[(size_t)kb * N + n];
+    } else {
+        v = reinterpret_cast<const float *>(q)[((size_t)kb * N + n) * 32 + e];
+    }
+    out[(size_t)n * K + kb * 32 + e] = v;
+}
+
+hipError_t launch_dequant(const DevMatrix &W, float *out, hipStream_t st) {
+    const size_t total = (size_t)(W.K / 32) * W.N * 32;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, W.fmt, W.q, W.sc, W.N, W.K,
+                       out);
+    return hipGetLastError();
+}
+
+}  // namespace cih

@@ -1,0 +1,266 @@
+// Memory-bound kernels of the forward: embedding, LayerNorm, last-layer head
+// mean, contact-map (APC) statistics and finalisation, output scatter.
+#include "kernels.h"
+
+namespace cih {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Embedding + token-dropout rescale (codon-infer src/lib.rs:5117-5131; Q8
+// 5461-5479; Q4 5820-5833).  scale = 0.88 / (1 - mask_count/len) for the
+// sequence's own length; <mask> (id 32) rows are zero.  The Q8 embedding is
+// dequantized as q*d first and then scaled, as the reference does.
+// One workgroup per (position, sequence); the mask count is recomputed per
+// row from the sequence's tokens (len <= a few thousand ints).
+__global__ __launch_bounds__(256) void k_embed(const int *__restrict__ tokens, const int *__restrict__ cu,
+                                               const int *__restrict__ lens, int S_max, int fmt,
+                                               const void *__restrict__ eq, const float *__restrict__ esc, int d,
+                                               int V, float *__restrict__ x) {
+    const int s = blockIdx.x, b = blockIdx.y;
+    const int len = lens[b];
+    if (s >= len) return;
+    const int *tk = tokens + (size_t)b * S_max;
+    __shared__ int cnt[4];
+    int c = 0;
+    for (int i = threadIdx.x; i < len; i += 256) c += tk[i] == 32;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+    if ((threadIdx.x & 63) == 0) cnt[threadIdx.x >> 6] = c;
+    __syncthreads();
+    const int mask_count = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+    const float ratio = (float)mask_count / (float)len;
+    const float scale = ratio >= 1.0f ? 0.0f : (1.0f - 0.12f) / (1.0f - ratio);
+    // ids outside [0, V) cannot occur on host-pointer calls (validated
+    // there); device-pointer calls are clamped so no read leaves the table.
+    const int t = min(max(tk[s], 0), V - 1);
+    float *xr = x + (size_t)(cu[b] + s) * d;
+    for (int i = threadIdx.x; i < d; i += 256) {
+        float v = 0.0f;
+        if (t != 32) {
+            const size_t blk = (size_t)(i >> 5) * V + t;  // k-block-major [d/32][V][32]
+            float e;
+            if (fmt == WF_Q8)
+                e = (float)reinterpret_cast<const signed char *>(eq)[blk * 32 + (i & 31)] * esc[blk];
+            else
+                e = reinterpret_cast<const float *>(eq)[blk * 32 + (i & 31)];
+            v = e * scale;
+        }
+        xr[i] = v;
+    }
+}
+
+hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *emb_q, const float *emb_sc, int d,
+                        int V, float *x, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed, dim3(sm.S_max, sm.B), dim3(256), 0, st, tokens, sm.cu, sm.lens, sm.S_max, emb_fmt,
+                       emb_q, emb_sc, d, V, x);
+    return hipGetLastError();
+}
+
+// layer_norm (lib.rs:2556-2562): mean, variance of (x - mean), 1/sqrt(var +
+// 1e-5), out = w * (x - mean) * inv + b.  One wave per row.
+template <int PER>
+__global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, const float *__restrict__ w,
+                                                   const float *__restrict__ b, float *__restrict__ out, int rows,
+                                                   int d) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + (size_t)row * d;
+    float v[PER];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = lane + 64 * i;
+        v[i] = c < d ? xr[c] : 0.0f;
+        s += v[i];
+    }
+    const float mean = wave_sum(s) / (float)d;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = lane + 64 * i;
+        const float t = v[i] - mean;
+        q += c < d ? t * t : 0.0f;
+    }
+    const float var = wave_sum(q) / (float)d;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+    float *orow = out + (size_t)row * d;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = lane + 64 * i;
+        if (c < d) orow[c] = w[c] * (v[i] - mean) * inv + b[c];
+    }
+}
+
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, int rows, int d,
+                            hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    const dim3 grid((rows + 3) / 4), blk(256);
+    const int per = (d + 63) / 64;
+    if (per <= 5) hipLaunchKernelGGL(k_layernorm<5>, grid, blk, 0, st, x, w, b, out, rows, d);
+    else if (per <= 10) hipLaunchKernelGGL(k_layernorm<10>, grid, blk, 0, st, x, w, b, out, rows, d);
+    else if (per <= 20) hipLaunchKernelGGL(k_layernorm<20>, grid, blk, 0, st, x, w, b, out, rows, d);
+    else if (per <= 40) hipLaunchKernelGGL(k_layernorm<40>, grid, blk, 0, st, x, w, b, out, rows, d);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// final_layer_att (lib.rs:5201-5204, 5256-5261): acc = 0; acc += P_h * (1/H)
+// in ascending h.
+__global__ __launch_bounds__(256) void k_head_mean(const float *__restrict__ P, long long pb, long long ph, int H,
+                                                   const int *__restrict__ lens, int S_max,
+                                                   float *__restrict__ fa) {
+    const int p = blockIdx.x, b = blockIdx.y;
+    const int len = lens[b];
+    if (p >= len) return;
+    const float hw = 1.0f / (float)H;
+    for (int t = threadIdx.x; t < len; t += 256) {
+        float acc = 0.0f;
+        for (int h = 0; h < H; h++) acc += P[b * pb + h * ph + (size_t)p * S_max + t] * hw;
+        fa[((size_t)b * S_max + p) * S_max + t] = acc;
+    }
+}
+
+hipError_t launch_head_mean(const float *P, int64_t pb, int64_t ph, int H, SeqMeta sm, float *final_att,
+                            hipStream_t st) {
+    hipLaunchKernelGGL(k_head_mean, dim3(sm.S_max, sm.B), dim3(256), 0, st, P, (long long)pb, (long long)ph, H,
+                       sm.lens, sm.S_max, final_att);
+    return hipGetLastError();
+}
+
+// ---- contacts: accumulate_head_apc (lib.rs:5036-5076) restated over a batch.
+// For a head with weight w and residue block A (rows/cols 1..n of P):
+//   s_ij = A_ij + A_ji, r_i = sum_j s_ij, T = sum_i r_i,
+//   logit_ij += w * (s_ij - (r_i / T) * r_j)
+// Summed over heads: logit = M + M^T - sum_h (w_h / T_h) r_h r_h^T with
+// M = sum_h w_h A_h.  Row sums of A go with M's accumulation (one workgroup
+// per residue row), column sums are a separate coalesced pass.
+// M: [B][n_max][n_max], r: [L*H][B][n_max], n_max = S_max - 2.
+__global__ __launch_bounds__(256) void k_apc_rows(const float *__restrict__ P, long long pb, long long ph, int H, int l,
+                                                  const float *__restrict__ w, const int *__restrict__ heads, int nz,
+                                                  const int *__restrict__ lens, int S_max, float *__restrict__ M,
+                                                  float *__restrict__ r, int B) {
+    const int i = blockIdx.x, b = blockIdx.y;
+    const int n = lens[b] - 2, n_max = S_max - 2;
+    if (i >= n) return;
+    __shared__ float red[4];
+    float *Mrow = M + ((size_t)b * n_max + i) * n_max;
+    // row sums per head
+    for (int k = 0; k < nz; k++) {
+        const int h = heads[k];
+        const float *A = P + b * pb + h * ph + (size_t)(i + 1) * S_max + 1;
+        float s = 0.0f;
+        for (int j = threadIdx.x; j < n; j += 256) s += A[j];
+        s = wave_sum(s);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        if (threadIdx.x == 0) r[((size_t)(l * H + h) * B + b) * n_max + i] = red[0] + red[1] + red[2] + red[3];
+        __syncthreads();
+    }
+    for (int j = threadIdx.x; j < n; j += 256) {
+        float acc = Mrow[j];
+        for (int k = 0; k < nz; k++) {
+            const int h = heads[k];
+            acc += w[l * H + h] * P[b * pb + h * ph + (size_t)(i + 1) * S_max + 1 + j];
+        }
+        Mrow[j] = acc;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_apc_cols(const float *__restrict__ P, long long pb, long long ph, int H, int l,
+                                                  const int *__restrict__ heads, const int *__restrict__ lens,
+                                                  int S_max, float *__restrict__ r, int B) {
+    const int b = blockIdx.y, h = heads[blockIdx.z];
+    const int n = lens[b] - 2, n_max = S_max - 2;
+    const int i = blockIdx.x * 256 + threadIdx.x;  // column (residue) index
+    if (i >= n) return;
+    const float *A = P + b * pb + h * ph + S_max + 1 + i;
+    float s = 0.0f;
+    for (int j = 0; j < n; j++) s += A[(size_t)j * S_max];
+    r[((size_t)(l * H + h) * B + b) * n_max + i] += s;
+}
+
+hipError_t launch_apc_layer(const float *P, int64_t pb, int64_t ph, int H, int l, const float *w_dev,
+                            const int *heads_dev, int n_heads_nz, SeqMeta sm, float *M, float *r, hipStream_t st) {
+    if (n_heads_nz <= 0 || sm.S_max < 3) return hipSuccess;
+    const int n_max = sm.S_max - 2;
+    hipLaunchKernelGGL(k_apc_rows, dim3(n_max, sm.B), dim3(256), 0, st, P, (long long)pb, (long long)ph, H, l, w_dev,
+                       heads_dev, n_heads_nz, sm.lens, sm.S_max, M, r, sm.B);
+    hipLaunchKernelGGL(k_apc_cols, dim3((n_max + 255) / 256, sm.B, n_heads_nz), dim3(256), 0, st, P, (long long)pb,
+                       (long long)ph, H, l, heads_dev, sm.lens, sm.S_max, r, sm.B);
+    return hipGetLastError();
+}
+
+// coef[lh][b] = w_lh / T_lh (0 when |T| <= 1e-12 or w == 0), T = sum_i r_i
+__global__ __launch_bounds__(256) void k_apc_coef(const float *__restrict__ r, const float *__restrict__ w,
+                                                  const int *__restrict__ lens, int S_max, int B,
+                                                  float *__restrict__ coef) {
+    const int lh = blockIdx.x, b = blockIdx.y;
+    const int n = lens[b] - 2, n_max = S_max - 2;
+    __shared__ float red[4];
+    float s = 0.0f;
+    if (w[lh] != 0.0f)
+        for (int i = threadIdx.x; i < n; i += 256) s += r[((size_t)lh * B + b) * n_max + i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float T = red[0] + red[1] + red[2] + red[3];
+        coef[(size_t)lh * B + b] = (w[lh] != 0.0f && fabsf(T) > 1e-12f) ? w[lh] * (1.0f / T) : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_apc_final(const float *__restrict__ M, const float *__restrict__ r,
+                                                   const float *__restrict__ coef, int LH, const int *__restrict__ lens,
+                                                   int S_max, int B, float bias, float *__restrict__ out,
+                                                   int n_stride) {
+    const int i = blockIdx.x, b = blockIdx.y;
+    const int n = lens[b] - 2, n_max = S_max - 2;
+    if (i >= n) return;
+    const float *Mb = M + (size_t)b * n_max * n_max;
+    for (int j = threadIdx.x; j < n; j += 256) {
+        float corr = 0.0f;
+        for (int lh = 0; lh < LH; lh++) {
+            const float c = coef[(size_t)lh * B + b];
+            if (c != 0.0f) {
+                const float *rr = r + ((size_t)lh * B + b) * n_max;
+                corr += c * rr[i] * rr[j];
+            }
+        }
+        const float logit = Mb[(size_t)i * n_max + j] + Mb[(size_t)j * n_max + i] - corr;
+        out[((size_t)b * n_stride + i) * n_stride + j] = 1.0f / (1.0f + expf(-(logit + bias)));
+    }
+}
+
+hipError_t launch_apc_finalize(const float *M, const float *r, float *coef, const float *w_dev, int LH, SeqMeta sm,
+                               float bias, float *contacts, int n_stride, hipStream_t st) {
+    if (sm.S_max < 3) return hipSuccess;
+    const int n_max = sm.S_max - 2;
+    hipLaunchKernelGGL(k_apc_coef, dim3(LH, sm.B), dim3(256), 0, st, r, w_dev, sm.lens, sm.S_max, sm.B, coef);
+    hipLaunchKernelGGL(k_apc_final, dim3(n_max, sm.B), dim3(256), 0, st, M, r, coef, LH, sm.lens, sm.S_max, sm.B, bias,
+                       contacts, n_stride);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_scatter_rows(const float *__restrict__ src, int width,
+                                                      const int *__restrict__ cu, const int *__restrict__ lens,
+                                                      int S_max, float *__restrict__ dst, long long bstride) {
+    const int s = blockIdx.x, b = blockIdx.y;
+    if (s >= lens[b]) return;
+    const float *sr = src + (size_t)(cu[b] + s) * width;
+    float *dr = dst + b * bstride + (size_t)s * width;
+    for (int i = threadIdx.x; i < width; i += 256) dr[i] = sr[i];
+}
+
+hipError_t launch_scatter_rows(const float *src, int width, SeqMeta sm, float *dst, int64_t dst_b_stride,
+                               hipStream_t st) {
+    hipLaunchKernelGGL(k_scatter_rows, dim3(sm.S_max, sm.B), dim3(256), 0, st, src, width, sm.cu, sm.lens, sm.S_max,
+                       dst, (long long)dst_b_stride);
+    return hipGetLastError();
+}
+
+}  // namespace cih

@@ -1,0 +1,166 @@
+"""GPU parity of the full batched forward (cih_forward) against the oracle run
+one unpadded sequence at a time (forward_bidirectional / _q8 / _q4,
+src/lib.rs:5078-6147).
+
+Tolerances (FP32 accumulate throughout):
+  logits        max |gpu - oracle| <= 1e-3
+  hidden        max |gpu - oracle| <= 1e-3
+  attention P   max |gpu - oracle| <= 1e-5
+  final_att     max |gpu - oracle| <= 1e-5
+  contacts      max |gpu - oracle| <= 1e-4
+  argmax        identical wherever the oracle's top-1/top-2 margin > 2e-3
+"""
+import numpy as np
+import pytest
+
+import codon_hip as ch
+import cpu_ref as cr
+from conftest import PEPTIDE, decode
+
+pytestmark = pytest.mark.gpu
+
+ALL = ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT | ch.OUT_CONTACTS | ch.OUT_ATTN | ch.OUT_LAYER_HIDDEN
+TOL = {"logits": 1e-3, "hidden": 1e-3, "attn": 1e-5, "final_att": 1e-5, "contacts": 1e-4, "layer_hidden": 1e-3}
+
+
+def rand_tokens(rng, n):
+    t = np.empty(n + 2, np.int32)
+    t[0], t[-1] = 0, 2
+    t[1:-1] = 4 + rng.integers(0, 20, n)
+    return t
+
+
+def quantized(w, dtype):
+    return w if dtype == 0 else (w.quantize_q8() if dtype == 1 else w.quantize_q4())
+
+
+def check_batch(cfg, w, seqs, flags, contact=None, nthreads=8, margin=2e-3):
+    model = ch.GpuModel(cfg, w, contact_head=contact, max_batch=len(seqs), max_len=max(len(s) for s in seqs),
+                        outputs=flags)
+    got = model.forward(seqs, flags)
+    worst = {}
+    for b, toks in enumerate(seqs):
+        S = len(toks)
+        ref = cr.forward(cfg, w, toks, nthreads, contacts=contact if flags & ch.OUT_CONTACTS else None,
+                         attn=bool(flags & ch.OUT_ATTN), layer_hidden=bool(flags & ch.OUT_LAYER_HIDDEN))
+        n = S - 2
+        pairs = [("logits", got["logits"][b, :S], ref["logits"])]
+        if flags & ch.OUT_HIDDEN:
+            pairs.append(("hidden", got["hidden"][b, :S], ref["hidden"]))
+        if flags & ch.OUT_FINAL_ATT:
+            pairs.append(("final_att", got["final_att"][b, :S, :S], ref["final_att"]))
+        if flags & ch.OUT_CONTACTS and n > 0:
+            pairs.append(("contacts", got["contacts"][b, :n, :n], ref["contacts"]))
+        if flags & ch.OUT_ATTN:
+            pairs.append(("attn", got["attn"][b, :, :, :S, :S], ref["attn"]))
+        if flags & ch.OUT_LAYER_HIDDEN:
+            pairs.append(("layer_hidden", got["layer_hidden"][b, :, :S], ref["layer_hidden"]))
+        for name, g, r in pairs:
+            e = float(np.abs(g.astype(np.float64) - r).max())
+            worst[name] = max(worst.get(name, 0.0), e)
+            assert e <= TOL[name], (name, b, S, e)
+        # argmax exact where the oracle's decision is not a near tie
+        lr = ref["logits"]
+        top2 = np.sort(lr, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > margin
+        assert np.array_equal(got["logits"][b, :S].argmax(1)[clear], lr.argmax(1)[clear]), b
+    print("worst abs errors:", {k: f"{v:.2e}" for k, v in worst.items()}, flush=True)
+    model.close()
+    return got
+
+
+@pytest.mark.parametrize("hd,H", [(16, 4), (24, 4), (32, 2), (64, 2)])
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_forward_small_configs(hd, H, dtype):
+    """Every head size, every weight format, ragged batch crossing the 32-key
+    and 128-query tile edges, all outputs including contacts and maps."""
+    rng = np.random.default_rng(hd * 10 + dtype)
+    d = hd * H
+    cfg = ch.EsmConfig(d, 4 * d, 2, H)
+    w = quantized(ch.EsmWeights.random(cfg, seed=hd + dtype, bias_std=0.02), dtype)
+    cw = rng.standard_normal(cfg.n_layers * H).astype(np.float32)
+    cw[::3] = 0.0
+    seqs = [rand_tokens(rng, n) for n in (3, 35, 70, 128, 1)]
+    seqs[1][5] = 32  # a <mask> changes the embedding scale of that sequence only
+    print(f"small config hd={hd} H={H} dtype={dtype}", flush=True)
+    check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(-0.5)))
+
+
+def test_forward_8m_peptide(w8m_path):
+    """Shipped 8M weights: every format reproduces the published prediction
+    (docs/benchmarks_v1.6.0.md:61-62) and matches the oracle within tolerance."""
+    cfg = ch.EsmConfig.esm2_8m()
+    w = ch.EsmWeights.from_grouped_canonical(w8m_path, cfg)
+    toks = ch.Tokenizer.encode(PEPTIDE)
+    masked = ch.Tokenizer.encode("MCMP*TTD")
+    for dtype in (0, 1, 2):
+        print(f"8M peptide dtype={dtype}", flush=True)
+        got = check_batch(cfg, quantized(w, dtype), [toks, masked], ALL, contact=cfg.contact_head_weights())
+        assert decode(got["logits"][0, 1:len(toks) - 1].argmax(1)) == PEPTIDE
+
+
+def test_forward_batch_invariance():
+    """A sequence's outputs do not depend on its batch neighbours: bit-identical
+    alone and inside a ragged batch."""
+    rng = np.random.default_rng(3)
+    cfg = ch.EsmConfig(128, 512, 2, 2)
+    w = ch.EsmWeights.random(cfg, seed=9, bias_std=0.02).quantize_q8()
+    seqs = [rand_tokens(rng, n) for n in (50, 200, 17)]
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN
+    m = ch.GpuModel(cfg, w, max_batch=3, max_len=202, outputs=flags)
+    batch = m.forward(seqs, flags)
+    for b, s in enumerate(seqs):
+        alone = m.forward([s], flags)
+        S = len(s)
+        assert np.array_equal(alone["logits"][0, :S], batch["logits"][b, :S])
+        assert np.array_equal(alone["hidden"][0, :S], batch["hidden"][b, :S])
+    m.close()
+
+
+@pytest.mark.parametrize("arch,dtype,B,lo,hi", [("35M", 1, 4, 20, 130), ("150M", 2, 2, 60, 100)])
+def test_forward_preset_archs(arch, dtype, B, lo, hi):
+    """Preset ESM-2 shapes (35M Q8_0 ragged, 150M Q4_0 with contacts) at
+    oracle-friendly lengths."""
+    rng = np.random.default_rng(11)
+    cfg = ch.EsmConfig.by_name(arch)
+    w = quantized(ch.EsmWeights.random(cfg, seed=1, bias_std=0.02), dtype)
+    seqs = [rand_tokens(rng, int(rng.integers(lo, hi))) for _ in range(B)]
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT | ch.OUT_CONTACTS
+    print(f"preset {arch} dtype={dtype}", flush=True)
+    check_batch(cfg, w, seqs, flags, contact=cfg.contact_head_weights())
+
+
+def test_forward_650m_q8_short():
+    """The headline architecture (650M, Q8_0) on two short sequences."""
+    rng = np.random.default_rng(12)
+    cfg = ch.EsmConfig.esm2_650m()
+    w = ch.EsmWeights.random(cfg, seed=2, bias_std=0.02).quantize_q8()
+    seqs = [rand_tokens(rng, 62), rand_tokens(rng, 40)]
+    print("650M Q8 short", flush=True)
+    check_batch(cfg, w, seqs, ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT, nthreads=16)
+
+
+def test_tied_embedding_decoder():
+    """A classifier shorter than the LM head selects logits = x . emb^T
+    (lib.rs:5427-5439, Q8: 5775-5787)."""
+    rng = np.random.default_rng(4)
+    cfg = ch.EsmConfig(64, 256, 2, 4)
+    for dtype in (0, 1, 2):
+        w = quantized(ch.EsmWeights.random(cfg, seed=4, bias_std=0.02), dtype)
+        w.classifier_weights = w.classifier_weights[:10]
+        check_batch(cfg, w, [rand_tokens(rng, 30)], ch.OUT_LOGITS | ch.OUT_HIDDEN)
+
+
+def test_forward_errors():
+    cfg = ch.EsmConfig(64, 256, 1, 4)
+    w = ch.EsmWeights.random(cfg, seed=0)
+    m = ch.GpuModel(cfg, w, max_batch=2, max_len=16, outputs=ch.OUT_LOGITS)
+    with pytest.raises(ch.CihError, match="CAPACITY"):
+        m.forward([np.zeros(20, np.int32)])
+    with pytest.raises(ch.CihError, match="CAPACITY"):
+        m.forward([np.zeros(5, np.int32)], ch.OUT_LOGITS | ch.OUT_HIDDEN)
+    with pytest.raises(ch.CihError, match="TOKEN"):
+        m.forward([np.array([0, 40, 2], np.int32)])
+    with pytest.raises(ch.CihError, match="CONTACTS|ARG"):
+        m.reserve(1, 1030, ch.OUT_CONTACTS)
+    m.close()
