@@ -9,6 +9,7 @@ Names and argument meanings follow the reference crate (src/lib.rs):
 family (5078-6147).  The forward itself always runs on the GPU through
 libcodon_hip.so.
 """
+import concurrent.futures
 import ctypes
 import json
 import os
@@ -114,6 +115,26 @@ def dequantize_blocks(dtype, blocks):
     return out
 
 
+def _normal(n, std, seed, stream, chunk=1 << 22):
+    """N(0, std) float32 samples; chunk c of tensor `stream` is drawn from
+    default_rng([seed, stream, c]), so the result does not depend on the
+    number of threads that fill it."""
+    out = np.empty(n, np.float32)
+    nch = (n + chunk - 1) // chunk
+
+    def fill(c):
+        sl = out[c * chunk:min(n, (c + 1) * chunk)]
+        np.random.default_rng([seed, stream, c]).standard_normal(sl.size, dtype=np.float32, out=sl)
+        sl *= np.float32(std)
+
+    if nch == 1:
+        fill(0)
+    else:
+        with concurrent.futures.ThreadPoolExecutor(min(16, os.cpu_count() or 1)) as ex:
+            list(ex.map(fill, range(nch)))
+    return out
+
+
 class _Weights:
     dtype = C.DTYPE_FP32
 
@@ -156,15 +177,14 @@ class EsmWeights(_Weights):
     def random(cls, cfg, seed=0, std=0.02, bias_std=0.0):
         """Seeded N(0, std) weights of the given architecture; LayerNorm gamma 1,
         beta 0; biases N(0, bias_std) (0 by default, the HF init)."""
-        rng = np.random.default_rng(seed)
         d, F, L, V = cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.vocab_size
+        counter = [0]
 
         def nrm(n, s):
+            counter[0] += 1
             if s == 0:
                 return np.zeros(n, np.float32)
-            a = rng.standard_normal(n, dtype=np.float32)
-            a *= np.float32(s)
-            return a
+            return _normal(n, s, seed, counter[0])
 
         ones = lambda n: np.ones(n, np.float32)  # noqa: E731
         zeros = lambda n: np.zeros(n, np.float32)  # noqa: E731

@@ -625,8 +625,10 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
 
 int cih_profile_enable(cih_model *m, int32_t enable) {
     if (!m) return set_error(CIH_ERR_ARG, "null model");
+    // enabling starts a new measurement; disabling keeps the totals readable
+    if (enable && !m->prof.on)
+        for (auto &s : m->prof.st) s = cih_kernel_stats{};
     m->prof.on = enable != 0;
-    for (auto &s : m->prof.st) s = cih_kernel_stats{};
     return CIH_OK;
 }
 

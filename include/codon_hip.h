@@ -181,7 +181,10 @@ typedef struct cih_kernel_stats {
     double bytes;      /* algorithmic HBM bytes (weights + activations)   */
 } cih_kernel_stats;
 
-int cih_profile_enable(cih_model *m, int32_t enable); /* also resets */
+/* enable != 0 resets the totals and starts recording (one event pair per
+ * launch, summed after each cih_forward); enable == 0 stops recording and
+ * keeps the totals for cih_profile_read. */
+int cih_profile_enable(cih_model *m, int32_t enable);
 int cih_profile_read(const cih_model *m, int32_t kernel_class, cih_kernel_stats *out);
 
 const char *cih_last_error(void);
