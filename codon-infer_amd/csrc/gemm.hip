@@ -16,6 +16,9 @@
 // reference's packing (element j low, element j+16 high, lib.rs:1064-1068).
 // A and the raw quantized B tile are double-buffered in LDS; the next k-block
 // is fetched into registers while the current one is multiplied.
+#include <stdlib.h>
+#include <string.h>
+
 #include "kernels.h"
 
 namespace cih {
@@ -286,11 +289,13 @@ hipError_t launch_gemm(const DevMatrix &W, const float *X, int ldx, const float 
                        int epi, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0 || ldx % 4 != 0) return hipErrorInvalidValue;
-    switch (W.fmt) {
-    case WF_Q8: return launch_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    case WF_Q4: return launch_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    default: return launch_epi<WF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    }
+    if (W.fmt == WF_F32) return launch_epi<WF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    // Quantized weights: bf16-limb MFMA kernel unless CIH_QGEMM=fp32 selects
+    // the FP32-MFMA kernel (same results to FP32 rounding; kept for A/B runs).
+    const char *path = getenv("CIH_QGEMM");
+    if (!(path && !strcmp(path, "fp32"))) return launch_gemm_x3(W, X, ldx, bias, Y, ldy, M, epi, st);
+    if (W.fmt == WF_Q8) return launch_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    return launch_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
 }
 
 // Test path: k-block-major device matrix -> row-major [N][K] FP32, with the

@@ -1,0 +1,290 @@
+// Quantized GEMM on bf16 MFMA with exact integer weights:
+//   Y = epi(X * W^T + b),  W in Q8_0 / Q4_0 blocks of 32.
+//
+// Same result as matmul_tiled_q8/q4_parallel (codon-infer src/lib.rs:4870,
+// 4937) to FP32 rounding, several times the FP32-MFMA rate:
+//   * The block's quants q (|q| <= 127, or -8..7 for Q4_0) are exact in bf16.
+//   * Each FP32 activation is split into three bf16 limbs
+//     x = b0 + b1 + b2 (b0 = bf16(x), b1 = bf16(x - b0), b2 = bf16(x - b0 - b1)),
+//     24 significant bits: the split is exact to below FP32 rounding.
+//   * Every limb x q product is exact in the MFMA's FP32 accumulator, so per
+//     32-element block tmp = sum_k (b0 + b1 + b2)_k q_k is the FP32 dot product
+//     of the block, and acc += d * tmp applies the block scale in FP32.
+// The reference forms w = q*d first and then sums w*x (lib.rs:4687, 4724-4741,
+// 4476-4492); this is the same sum regrouped per block, with FP32 rounding.
+//
+// Tiling: 256 threads = 4 waves (2x2), workgroup tile BM x BN, BK = 32 = one
+// block.  v_mfma_f32_32x32x16_bf16: lane (i = lane%32, half = lane/32) feeds
+// the 8 elements 16*kh + 8*half + e of k-half kh.  For Q4_0 that is the low
+// nibbles (kh = 0) and high nibbles (kh = 1) of bytes 8*half..8*half+7: the
+// reference's packing.  The activation split and the integer-to-bf16
+// conversion happen once per workgroup while staging into LDS; the next
+// k-block is fetched into registers during the current block's MFMAs.
+#include "kernels.h"
+
+namespace cih {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float erf_as3(float x) {
+    float sign = x < 0.0f ? -1.0f : 1.0f;
+    float ax = fabsf(x);
+    float t = 1.0f / (1.0f + 0.3275911f * ax);
+    float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                       0.254829592f) * t * expf(-ax * ax);
+    return sign * y;
+}
+__device__ __forceinline__ float gelu_ref3(float x) { return 0.5f * x * (1.0f + erf_as3(x * 0.70710678118654752440f)); }
+
+constexpr int XL = 40;  // bf16 per LDS row (32 + 8 pad): conflict-free 16-byte reads
+
+__device__ __forceinline__ unsigned pack_bf16(float lo, float hi) {
+    // round-to-nearest-even f32 -> bf16 for both halves (v_cvt_pk_bf16_f32)
+    __bf16 a = (__bf16)lo, b = (__bf16)hi;
+    return (unsigned)__builtin_bit_cast(unsigned short, a) | ((unsigned)__builtin_bit_cast(unsigned short, b) << 16);
+}
+__device__ __forceinline__ float bf16_lo(unsigned p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(unsigned p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// x0..x3 -> three limbs, each as two packed bf16 dwords
+__device__ __forceinline__ void split4(float4 x, uint2 &l0, uint2 &l1, uint2 &l2) {
+    l0.x = pack_bf16(x.x, x.y);
+    l0.y = pack_bf16(x.z, x.w);
+    float r0 = x.x - bf16_lo(l0.x), r1 = x.y - bf16_hi(l0.x), r2 = x.z - bf16_lo(l0.y), r3 = x.w - bf16_hi(l0.y);
+    l1.x = pack_bf16(r0, r1);
+    l1.y = pack_bf16(r2, r3);
+    r0 -= bf16_lo(l1.x); r1 -= bf16_hi(l1.x); r2 -= bf16_lo(l1.y); r3 -= bf16_hi(l1.y);
+    l2.x = pack_bf16(r0, r1);
+    l2.y = pack_bf16(r2, r3);
+}
+
+__device__ __forceinline__ void tile_of3(int bid, int total, int nM, int nN, int &mt, int &nt) {
+    constexpr int XCD = 8, GROUP_M = 8;
+    int xcd = bid % XCD, local = bid / XCD;
+    int per = total / XCD, rem = total % XCD;
+    int id = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    int in_group = GROUP_M * nN;
+    int g = id / in_group;
+    int first = g * GROUP_M;
+    int gsize = min(nM - first, GROUP_M);
+    int r = id % in_group;
+    mt = first + r % gsize;
+    nt = r / gsize;
+}
+
+template <int WF, int EPI, int BM, int BN>
+__global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X, int ldx,
+                                                    const void *__restrict__ Wq, const float *__restrict__ Wsc,
+                                                    const float *__restrict__ bias, float *__restrict__ Y, int ldy,
+                                                    int M, int N, int K) {
+    constexpr int MT = BM / 64, NT = BN / 64;
+    constexpr int A_LOADS = BM / 32;                 // float4 per thread
+    constexpr int B_ITEMS = BN * 2;                  // (column, half of the block's bytes)
+    constexpr int B_LOADS = (B_ITEMS + 255) / 256;
+    constexpr int QB = WF == WF_Q8 ? 32 : 16;        // quant bytes per block
+    __shared__ __attribute__((aligned(16))) unsigned short Al[3][BM * XL];
+    __shared__ __attribute__((aligned(16))) unsigned short Bl[BN * XL];
+    __shared__ float Ss[BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 31, hh = lane >> 5;
+    const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+    int mt, nt;
+    tile_of3(blockIdx.x, nM * nN, nM, nN, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int KB = K / 32;
+
+    float4 ra[A_LOADS];
+    uint4 rb[B_LOADS];  // Q8: 16 bytes (elements 16*part..+15); Q4: 8 bytes in .x/.y
+    float rs = 0.0f;
+
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; i++) {
+            const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
+            const int gr = m0 + row;
+            ra[i] = gr < M ? *reinterpret_cast<const float4 *>(X + (size_t)gr * ldx + kb * 32 + c4 * 4)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < B_LOADS; i++) {
+            const int idx = tid + 256 * i, col = idx >> 1, part = idx & 1;
+            const int gc = n0 + col;
+            const unsigned char *src = reinterpret_cast<const unsigned char *>(Wq) + ((size_t)kb * N + gc) * QB;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (idx < B_ITEMS && gc < N) {
+                if constexpr (WF == WF_Q8) {
+                    v = *reinterpret_cast<const uint4 *>(src + part * 16);
+                } else {
+                    const uint2 h = *reinterpret_cast<const uint2 *>(src + part * 8);
+                    v.x = h.x;
+                    v.y = h.y;
+                }
+            }
+            rb[i] = v;
+        }
+        const int gc = n0 + tid;
+        rs = (tid < BN && gc < N) ? Wsc[(size_t)kb * N + gc] : 0.0f;
+    };
+
+    auto sstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; i++) {
+            const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
+            uint2 l0, l1, l2;
+            split4(ra[i], l0, l1, l2);
+            *reinterpret_cast<uint2 *>(&Al[0][row * XL + c4 * 4]) = l0;
+            *reinterpret_cast<uint2 *>(&Al[1][row * XL + c4 * 4]) = l1;
+            *reinterpret_cast<uint2 *>(&Al[2][row * XL + c4 * 4]) = l2;
+        }
+#pragma unroll
+        for (int i = 0; i < B_LOADS; i++) {
+            const int idx = tid + 256 * i, col = idx >> 1, part = idx & 1;
+            if (idx >= B_ITEMS) continue;
+            const unsigned w[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+            if constexpr (WF == WF_Q8) {
+                // 16 int8 = elements 16*part .. 16*part+15, exact in bf16
+                unsigned o[8];
+#pragma unroll
+                for (int p = 0; p < 8; p++) {
+                    const unsigned word = w[p >> 1];
+                    const int sh = (p & 1) * 16;
+                    o[p] = pack_bf16((float)(signed char)((word >> sh) & 0xFF),
+                                     (float)(signed char)((word >> (sh + 8)) & 0xFF));
+                }
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16]) = make_uint4(o[0], o[1], o[2], o[3]);
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16 + 8]) = make_uint4(o[4], o[5], o[6], o[7]);
+            } else {
+                // 8 bytes = elements 8*part+e (low nibble) and 16+8*part+e (high nibble)
+                unsigned lo[4], hi[4];
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const unsigned word = w[p >> 1];
+                    const int sh = (p & 1) * 16;
+                    const unsigned b0 = (word >> sh) & 0xFF, b1 = (word >> (sh + 8)) & 0xFF;
+                    lo[p] = pack_bf16((float)((int)(b0 & 0xF) - 8), (float)((int)(b1 & 0xF) - 8));
+                    hi[p] = pack_bf16((float)((int)(b0 >> 4) - 8), (float)((int)(b1 >> 4) - 8));
+                }
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 8]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + 16 + part * 8]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            }
+        }
+        if (tid < BN) Ss[tid] = rs;
+    };
+
+    f32x16 acc[MT][NT];
+#pragma unroll
+    for (int r = 0; r < MT; r++)
+#pragma unroll
+        for (int c = 0; c < NT; c++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
+
+    gload(0);
+    for (int kb = 0; kb < KB; kb++) {
+        __syncthreads();  // every wave is done reading the previous block
+        sstore();
+        __syncthreads();
+        if (kb + 1 < KB) gload(kb + 1);  // in flight during this block's MFMAs
+
+        f32x16 tmp[MT][NT];
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            bf16x8 a[MT][3], b[NT];
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int l = 0; l < 3; l++)
+                    a[r][l] = *reinterpret_cast<const bf16x8 *>(
+                        &Al[l][(wm * (BM / 2) + r * 32 + li) * XL + kh * 16 + hh * 8]);
+#pragma unroll
+            for (int c = 0; c < NT; c++)
+                b[c] = *reinterpret_cast<const bf16x8 *>(&Bl[(wn * (BN / 2) + c * 32 + li) * XL + kh * 16 + hh * 8]);
+#pragma unroll
+            for (int l = 0; l < 3; l++)
+#pragma unroll
+                for (int r = 0; r < MT; r++)
+#pragma unroll
+                    for (int c = 0; c < NT; c++) {
+                        if (kh == 0 && l == 0) {
+                            f32x16 z;
+#pragma unroll
+                            for (int q = 0; q < 16; q++) z[q] = 0.0f;
+                            tmp[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][l], b[c], z, 0, 0, 0);
+                        } else {
+                            tmp[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][l], b[c], tmp[r][c], 0, 0, 0);
+                        }
+                    }
+        }
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const float d = Ss[wn * (BN / 2) + c * 32 + li];
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) acc[r][c][q] += d * tmp[r][c][q];
+        }
+    }
+
+#pragma unroll
+    for (int c = 0; c < NT; c++) {
+        const int col = n0 + wn * (BN / 2) + c * 32 + li;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < MT; r++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                if (row < M) {
+                    float v = acc[r][c][q] + bv;
+                    float *dst = Y + (size_t)row * ldy + col;
+                    if constexpr (EPI == EPI_GELU) v = gelu_ref3(v);
+                    if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+                    *dst = v;
+                }
+            }
+    }
+}
+
+template <int WF, int EPI, int BM, int BN>
+static hipError_t launch_x3_t(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
+                              int M, hipStream_t st) {
+    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN;
+    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc, bias, Y,
+                       ldy, M, W.N, W.K);
+    return hipGetLastError();
+}
+
+template <int WF, int EPI>
+static hipError_t launch_x3_shape(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
+                                  int M, hipStream_t st) {
+    const bool small_m = M <= 64, small_n = W.N <= 64;
+    if (small_m && small_n) return launch_x3_t<WF, EPI, 64, 64>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_m) return launch_x3_t<WF, EPI, 64, 128>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_n) return launch_x3_t<WF, EPI, 128, 64>(W, X, ldx, bias, Y, ldy, M, st);
+    return launch_x3_t<WF, EPI, 128, 128>(W, X, ldx, bias, Y, ldy, M, st);
+}
+
+template <int WF>
+static hipError_t launch_x3_epi(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
+                                int M, int epi, hipStream_t st) {
+    switch (epi) {
+    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL>(W, X, ldx, bias, Y, ldy, M, st);
+    default: return launch_x3_shape<WF, EPI_NONE>(W, X, ldx, bias, Y, ldy, M, st);
+    }
+}
+
+hipError_t launch_gemm_x3(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
+                          int epi, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    if (W.K % 32 != 0 || ldx % 4 != 0) return hipErrorInvalidValue;
+    if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace cih

@@ -27,6 +27,11 @@ struct DevMatrix {
 hipError_t launch_gemm(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y,
                        int ldy, int M, int epi, hipStream_t st);
 
+// Q8_0/Q4_0 GEMM on bf16 MFMA: exact integer weights, activations split
+// into three bf16 limbs (FP32-equivalent products), block scale in FP32.
+hipError_t launch_gemm_x3(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y,
+                          int ldy, int M, int epi, hipStream_t st);
+
 // Dequantizes nblocks of a device matrix in k-block-major layout back to the
 // reference's row-major [N][K] FP32 (test path).
 hipError_t launch_dequant(const DevMatrix &W, float *out, hipStream_t st);

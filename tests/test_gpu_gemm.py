@@ -25,15 +25,22 @@ def _weights(dtype, N, K, rng):
     return q, wd
 
 
+@pytest.mark.parametrize("path", ["x3", "fp32"])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
 @pytest.mark.parametrize("N,K", SHAPES)
-def test_gemm_matches_oracle(dtype, N, K):
+def test_gemm_matches_oracle(dtype, N, K, path, monkeypatch):
+    """Both quantized GEMM kernels: the default bf16-limb MFMA kernel (x3)
+    and the FP32-MFMA kernel selected by CIH_QGEMM=fp32."""
+    if path == "fp32":
+        monkeypatch.setenv("CIH_QGEMM", "fp32")
+    elif dtype == 0:
+        pytest.skip("FP32 weights always use the FP32-MFMA kernel")
     rng = np.random.default_rng(N * 7 + K + dtype)
     w, wd = _weights(dtype, N, K, rng)
     bias = rng.standard_normal(N, dtype=np.float32) * np.float32(0.02)
     for M in MS:
         x = rng.standard_normal(M * K, dtype=np.float32)
-        print(f"gemm dtype={dtype} M={M} N={N} K={K}", flush=True)
+        print(f"gemm {path} dtype={dtype} M={M} N={N} K={K}", flush=True)
         got = ch.matmul_tiled(dtype, x, w, bias, K, N)
         ref = cr.matmul_tiled(dtype, x, w, bias, K, N, num_threads=8)
         scale = np.abs(x.reshape(M, K)).astype(np.float64) @ np.abs(wd.reshape(N, K)).astype(np.float64).T
