@@ -105,6 +105,9 @@ def main():
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="issue one device-to-device copy of this many MiB first (a known-size kernel that "
+                         "calibrates FETCH_SIZE / WRITE_SIZE counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the ESM-2 forward is data parallel over "
@@ -131,6 +134,13 @@ def main():
     d_log = hip.malloc(B * S * cfg.vocab_size * 4)
     hip.h2d(d_tok, toks)
     outs = {"logits": d_log}
+    if args.copy_probe_mb:
+        nbytes = args.copy_probe_mb << 20
+        src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+        hip.L.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3)
+        hip.sync()
+        hip.free(src)
+        hip.free(dst)
     print(f"[bench] model resident ({time.perf_counter() - t0:.1f} s); warmup {args.warmup}", file=sys.stderr,
           flush=True)
 

@@ -235,12 +235,13 @@ double wbytes(const DevMatrix &W) {
     return W.fmt == WF_F32 ? 4.0 * e : (W.fmt == WF_Q8 ? 1.125 * e : 0.625 * e);
 }
 
-hipError_t gemm(cih_model *m, const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
-                int epi) {
+hipError_t gemm(cih_model *m, const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
+                int M, int epi) {
     const double flops = 2.0 * M * W.N * W.K;
-    const double bytes = wbytes(W) + 4.0 * M * W.K + 4.0 * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
+    const double in_b = a_fmt == AF_X3 ? 6.0 : 4.0, out_b = epi == EPI_GELU_X3 ? 6.0 : 4.0;
+    const double bytes = wbytes(W) + in_b * M * W.K + out_b * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
     ProfScope ps(m, W.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, flops, bytes);
-    return launch_gemm(W, X, ldx, bias, Y, ldy, M, epi, m->stream);
+    return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, m->stream);
 }
 
 }  // namespace
@@ -408,8 +409,10 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
         return e == hipSuccess;
     };
     bool good = ok(dalloc(ws.tokens, T, dl)) && ok(dalloc(ws.cu, B, dl)) && ok(dalloc(ws.lens, B, dl)) &&
-                ok(dalloc(ws.x, T * d, dl)) && ok(dalloc(ws.xb, T * d, dl)) && ok(dalloc(ws.qkv, T * 3 * d, dl)) &&
-                ok(dalloc(ws.ao, T * d, dl)) && ok(dalloc(ws.hbuf, T * std::max(F, d), dl)) &&
+                // xb, ao and hbuf also hold the three-limb bf16 form (6 B/element)
+                ok(dalloc(ws.x, T * d, dl)) && ok(dalloc(ws.xb, T * d * 3 / 2, dl)) &&
+                ok(dalloc(ws.qkv, T * 3 * d, dl)) && ok(dalloc(ws.ao, T * d * 3 / 2, dl)) &&
+                ok(dalloc(ws.hbuf, T * std::max(F * 3 / 2, d), dl)) &&
                 ok(dalloc(ws.logits, T * V, dl)) && ok(dalloc(ws.rope_c, S * half, dl)) &&
                 ok(dalloc(ws.rope_s, S * half, dl));
     const bool need_P = flags & (CIH_OUT_CONTACTS | CIH_OUT_FINAL_ATT | CIH_OUT_ATTN);
@@ -503,6 +506,16 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
           *t_final = dev_io ? out->final_att : ws.o_final, *t_contacts = dev_io ? out->contacts : ws.o_contacts,
           *t_attn = dev_io ? out->attn : ws.o_attn, *t_layer = dev_io ? out->layer_hidden : ws.o_layer;
 
+    // Activations reach the quantized GEMMs as FP32 and are split into bf16
+    // limbs inside the GEMM (measured faster at the 650M B=16 L=512 shape).
+    // CIH_ACT=x3 makes LayerNorm / attention / FC1's epilogue write the
+    // pre-split three-limb form instead; CIH_QGEMM=fp32 selects the FP32-MFMA
+    // GEMM (FP32 activations).
+    const char *qpath = getenv("CIH_QGEMM"), *apath = getenv("CIH_ACT");
+    const bool x3 = m->dtype != DT_FP32 && !(qpath && !std::strcmp(qpath, "fp32")) &&
+                    (apath && !std::strcmp(apath, "x3"));
+    const int af = x3 ? AF_X3 : AF_F32;
+
     m->prof.used = 0;
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
@@ -514,9 +527,9 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
         const Layer &ly = m->layers[l];
         {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-            HIPCHK(launch_layernorm(ws.x, ly.ln1w, ly.ln1b, ws.xb, T, d, st));
+            HIPCHK(launch_layernorm(ws.x, ly.ln1w, ly.ln1b, ws.xb, af, T, d, st));
         }
-        HIPCHK(gemm(m, ly.wqkv, ws.xb, d, ly.bqkv, ws.qkv, 3 * d, T, EPI_NONE));
+        HIPCHK(gemm(m, ly.wqkv, ws.xb, d, af, ly.bqkv, ws.qkv, 3 * d, T, EPI_NONE));
         // probabilities: straight into the attention-map output when exported
         float *P = nullptr;
         int64_t pb = 0, ph = SS;
@@ -532,7 +545,7 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
             double fl = 0;
             for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
             ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
-            HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, P, pb, ph, st));
+            HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, af, P, pb, ph, st));
         }
         if (want_contacts && m->nz[l] > 0) {
             ProfScope ps(m, CIH_KC_OTHER, 0, 0);
@@ -543,13 +556,13 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
             ProfScope ps(m, CIH_KC_OTHER, 0, 0);
             HIPCHK(launch_head_mean(P, pb, ph, H, sm, t_final, st));
         }
-        HIPCHK(gemm(m, ly.wo, ws.ao, d, ly.bo, ws.x, d, T, EPI_RESIDUAL));
+        HIPCHK(gemm(m, ly.wo, ws.ao, d, af, ly.bo, ws.x, d, T, EPI_RESIDUAL));
         {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-            HIPCHK(launch_layernorm(ws.x, ly.ln2w, ly.ln2b, ws.xb, T, d, st));
+            HIPCHK(launch_layernorm(ws.x, ly.ln2w, ly.ln2b, ws.xb, af, T, d, st));
         }
-        HIPCHK(gemm(m, ly.w1, ws.xb, d, ly.b1, ws.hbuf, F, T, EPI_GELU));
-        HIPCHK(gemm(m, ly.w2, ws.hbuf, F, ly.b2, ws.x, d, T, EPI_RESIDUAL));
+        HIPCHK(gemm(m, ly.w1, ws.xb, d, af, ly.b1, ws.hbuf, F, T, x3 ? EPI_GELU_X3 : EPI_GELU));
+        HIPCHK(gemm(m, ly.w2, ws.hbuf, F, af, ly.b2, ws.x, d, T, EPI_RESIDUAL));
         if (want_layer) HIPCHK(launch_scatter_rows(ws.x, d, sm, t_layer + (size_t)l * S_max * d, (int64_t)L * S_max * d, st));
     }
     if (want_contacts) {
@@ -559,19 +572,19 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
     // final LayerNorm: state.x = LN_f(x) (lib.rs:5379-5387)
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-        HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, T, d, st));
+        HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, AF_F32, T, d, st));
     }
     if (want_hidden) HIPCHK(launch_scatter_rows(ws.ao, d, sm, t_hidden, (int64_t)S_max * d, st));
     if (want_logits) {
         if (m->has_head) {
-            HIPCHK(gemm(m, m->dense, ws.ao, d, m->dense_b, ws.hbuf, d, T, EPI_GELU));
+            HIPCHK(gemm(m, m->dense, ws.ao, d, AF_F32, m->dense_b, ws.hbuf, d, T, EPI_GELU));
             {
                 ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-                HIPCHK(launch_layernorm(ws.hbuf, m->lm_lnw, m->lm_lnb, ws.xb, T, d, st));
+                HIPCHK(launch_layernorm(ws.hbuf, m->lm_lnw, m->lm_lnb, ws.xb, AF_F32, T, d, st));
             }
-            HIPCHK(gemm(m, m->dec, ws.xb, d, m->dec_b, ws.logits, V, T, EPI_NONE));
+            HIPCHK(gemm(m, m->dec, ws.xb, d, AF_F32, m->dec_b, ws.logits, V, T, EPI_NONE));
         } else {
-            HIPCHK(gemm(m, m->emb, ws.ao, d, nullptr, ws.logits, V, T, EPI_NONE));
+            HIPCHK(gemm(m, m->emb, ws.ao, d, AF_F32, nullptr, ws.logits, V, T, EPI_NONE));
         }
         HIPCHK(launch_scatter_rows(ws.logits, V, sm, t_logits, (int64_t)S_max * V, st));
     }
@@ -655,7 +668,7 @@ int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w, c
     if (!rc && dalloc(dy, (size_t)seq_len * out_dim, tmp.allocs) != hipSuccess)
         rc = set_error(CIH_ERR_HIP, "allocation failed");
     if (!rc) {
-        hipError_t e = launch_gemm(tmp.emb, dx, in_dim, db, dy, out_dim, seq_len, EPI_NONE, nullptr);
+        hipError_t e = launch_gemm(tmp.emb, dx, in_dim, AF_F32, db, dy, out_dim, seq_len, EPI_NONE, nullptr);
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e == hipSuccess) e = hipMemcpy(out, dy, (size_t)seq_len * out_dim * 4, hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = set_error(CIH_ERR_HIP, "GEMM failed: %s", hipGetErrorString(e));

@@ -33,8 +33,8 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
                                                    const int *__restrict__ lens, int S_max,
                                                    const float *__restrict__ rc, const float *__restrict__ rsn,
-                                                   float *__restrict__ out, float *__restrict__ P, long long pb,
-                                                   long long ph, float inv_scale) {
+                                                   void *__restrict__ out, int out_fmt, float *__restrict__ P,
+                                                   long long pb, long long ph, float inv_scale) {
     constexpr int HALF = HD / 2;
     constexpr int VW = HD < 32 ? 32 : HD;  // V tile width, zero padded for small heads
     constexpr int DT = VW / 32;            // 32-wide output tiles
@@ -165,38 +165,44 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
         }
     }
     if (qi < len) {
-        float *orow = out + (size_t)(base + qi) * d + h * HD;
+        // lane holds output dims dd = t*32 + 8*(q/4) + 4*half + q%4: groups of 4
 #pragma unroll
         for (int t = 0; t < DT; t++)
 #pragma unroll
-            for (int q = 0; q < 16; q++) {
-                const int dd = t * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                if (dd < HD) orow[dd] = oacc[t][q];
+            for (int g = 0; g < 4; g++) {
+                const int dd = t * 32 + 8 * g + 4 * hh;
+                if (dd >= HD) continue;
+                const float4 v = make_float4(oacc[t][4 * g], oacc[t][4 * g + 1], oacc[t][4 * g + 2], oacc[t][4 * g + 3]);
+                if (out_fmt == AF_X3)
+                    x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                else
+                    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d + h * HD + dd) = v;
             }
     }
 }
 
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos, const float *rope_sin,
-                            float *out, float *P, int64_t pb, int64_t ph, hipStream_t st) {
+                            void *out, int out_fmt, float *P, int64_t pb, int64_t ph, hipStream_t st) {
+    if (out_fmt == AF_X3 && d % 32) return hipErrorInvalidValue;
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
     dim3 grid((sm.S_max + 127) / 128, H, sm.B);
     switch (hd) {
     case 16:
         hipLaunchKernelGGL(k_attention<16>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
         break;
     case 24:
         hipLaunchKernelGGL(k_attention<24>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
         break;
     case 32:
         hipLaunchKernelGGL(k_attention<32>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
         break;
     case 64:
         hipLaunchKernelGGL(k_attention<64>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, P, (long long)pb, (long long)ph, inv_scale);
+                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
         break;
     default: return hipErrorInvalidValue;
     }

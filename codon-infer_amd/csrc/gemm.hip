@@ -285,17 +285,24 @@ static hipError_t launch_epi(const DevMatrix &W, const float *X, int ldx, const 
     }
 }
 
-hipError_t launch_gemm(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
-                       int epi, hipStream_t st) {
+hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, const float *bias, void *Yv, int ldy,
+                       int M, int epi, hipStream_t st) {
     if (M <= 0) return hipSuccess;
-    if (W.K % 32 != 0 || ldx % 4 != 0) return hipErrorInvalidValue;
-    if (W.fmt == WF_F32) return launch_epi<WF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    // Quantized weights: bf16-limb MFMA kernel unless CIH_QGEMM=fp32 selects
-    // the FP32-MFMA kernel (same results to FP32 rounding; kept for A/B runs).
-    const char *path = getenv("CIH_QGEMM");
-    if (!(path && !strcmp(path, "fp32"))) return launch_gemm_x3(W, X, ldx, bias, Y, ldy, M, epi, st);
+    if (W.K % 32 != 0) return hipErrorInvalidValue;
+    // Quantized weights go to the bf16-limb MFMA kernel (FP32 or pre-split
+    // activations) unless CIH_QGEMM=fp32 selects the FP32-MFMA kernel, which
+    // gives the same results to FP32 rounding and is kept for A/B runs.
+    if (W.fmt != WF_F32) {
+        const char *path = getenv("CIH_QGEMM");
+        if (a_fmt == AF_X3 || !(path && !strcmp(path, "fp32")))
+            return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, st);
+    }
+    if (a_fmt != AF_F32 || epi == EPI_GELU_X3 || ldx % 4 != 0) return hipErrorInvalidValue;
+    const float *X = reinterpret_cast<const float *>(Xv);
+    float *Y = reinterpret_cast<float *>(Yv);
     if (W.fmt == WF_Q8) return launch_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    return launch_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    if (W.fmt == WF_Q4) return launch_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    return launch_epi<WF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
 }
 
 // Test path: k-block-major device matrix -> row-major [N][K] FP32, with the

@@ -21,6 +21,7 @@
 // conversion happen once per workgroup while staging into LDS; the next
 // k-block is fetched into registers during the current block's MFMAs.
 #include "kernels.h"
+#include "x3.h"
 
 namespace cih {
 
@@ -37,12 +38,17 @@ __device__ __forceinline__ float erf_as3(float x) {
 }
 __device__ __forceinline__ float gelu_ref3(float x) { return 0.5f * x * (1.0f + erf_as3(x * 0.70710678118654752440f)); }
 
-constexpr int XL = 40;  // bf16 per LDS row (32 + 8 pad): conflict-free 16-byte reads
+constexpr int XL = 40;    // bf16 per LDS column of B (32 + 8 pad): conflict-free 16-byte reads
+constexpr int AROW = 104; // bf16 per LDS row of A: 3 limbs x 32 + 8 pad (208 B, conflict-free)
 
 __device__ __forceinline__ unsigned pack_bf16(float lo, float hi) {
-    // round-to-nearest-even f32 -> bf16 for both halves (v_cvt_pk_bf16_f32)
+    // round-to-nearest-even f32 -> bf16 for both halves
     __bf16 a = (__bf16)lo, b = (__bf16)hi;
     return (unsigned)__builtin_bit_cast(unsigned short, a) | ((unsigned)__builtin_bit_cast(unsigned short, b) << 16);
+}
+// bf16 of two floats that are exact in bf16 (small integers): the high halves
+__device__ __forceinline__ unsigned pack_exact(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 __device__ __forceinline__ float bf16_lo(unsigned p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf16_hi(unsigned p) { return __uint_as_float(p & 0xFFFF0000u); }
@@ -73,17 +79,18 @@ __device__ __forceinline__ void tile_of3(int bid, int total, int nM, int nN, int
     nt = r / gsize;
 }
 
-template <int WF, int EPI, int BM, int BN>
-__global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X, int ldx,
+template <int WF, int EPI, int BM, int BN, int AF>
+__global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv, int ldx,
                                                     const void *__restrict__ Wq, const float *__restrict__ Wsc,
-                                                    const float *__restrict__ bias, float *__restrict__ Y, int ldy,
+                                                    const float *__restrict__ bias, void *__restrict__ Yv, int ldy,
                                                     int M, int N, int K) {
     constexpr int MT = BM / 64, NT = BN / 64;
-    constexpr int A_LOADS = BM / 32;                 // float4 per thread
+    // A tile per k-block: FP32 -> BM*8 float4 (split here); X3 -> BM*12 16-byte chunks (copied)
+    constexpr int A_LOADS = AF == AF_X3 ? BM * 12 / 256 : BM / 32;
     constexpr int B_ITEMS = BN * 2;                  // (column, half of the block's bytes)
     constexpr int B_LOADS = (B_ITEMS + 255) / 256;
     constexpr int QB = WF == WF_Q8 ? 32 : 16;        // quant bytes per block
-    __shared__ __attribute__((aligned(16))) unsigned short Al[3][BM * XL];
+    __shared__ __attribute__((aligned(16))) unsigned short Al[BM * AROW];
     __shared__ __attribute__((aligned(16))) unsigned short Bl[BN * XL];
     __shared__ float Ss[BN];
 
@@ -96,17 +103,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X,
     const int m0 = mt * BM, n0 = nt * BN;
     const int KB = K / 32;
 
-    float4 ra[A_LOADS];
-    uint4 rb[B_LOADS];  // Q8: 16 bytes (elements 16*part..+15); Q4: 8 bytes in .x/.y
-    float rs = 0.0f;
+    // two register stages: block kb+2 is in flight while block kb is multiplied
+    uint4 ra[2][A_LOADS];
+    uint4 rb[2][B_LOADS];  // Q8: 16 bytes (elements 16*part..+15); Q4: 8 bytes in .x/.y
+    float rs[2];
 
-    auto gload = [&](int kb) {
+    auto gload = [&](int kb, uint4 (&a)[A_LOADS], uint4 (&b)[B_LOADS], float &sc) {
 #pragma unroll
         for (int i = 0; i < A_LOADS; i++) {
-            const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
-            const int gr = m0 + row;
-            ra[i] = gr < M ? *reinterpret_cast<const float4 *>(X + (size_t)gr * ldx + kb * 32 + c4 * 4)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (AF == AF_X3) {
+                const int c = tid + 256 * i, row = c / 12, part = c % 12;
+                const int gr = m0 + row;
+                a[i] = gr < M ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const unsigned short *>(Xv) +
+                                                                 ((size_t)gr * KB + kb) * 96 + part * 8)
+                              : make_uint4(0, 0, 0, 0);
+            } else {
+                const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
+                const int gr = m0 + row;
+                a[i] = gr < M ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(Xv) +
+                                                                 (size_t)gr * ldx + kb * 32 + c4 * 4)
+                              : make_uint4(0, 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; i++) {
@@ -123,27 +140,35 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X,
                     v.y = h.y;
                 }
             }
-            rb[i] = v;
+            b[i] = v;
         }
         const int gc = n0 + tid;
-        rs = (tid < BN && gc < N) ? Wsc[(size_t)kb * N + gc] : 0.0f;
+        sc = (tid < BN && gc < N) ? Wsc[(size_t)kb * N + gc] : 0.0f;
     };
 
-    auto sstore = [&]() {
+    auto sstore = [&](const uint4 (&a)[A_LOADS], const uint4 (&b)[B_LOADS], float sc) {
 #pragma unroll
         for (int i = 0; i < A_LOADS; i++) {
-            const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
-            uint2 l0, l1, l2;
-            split4(ra[i], l0, l1, l2);
-            *reinterpret_cast<uint2 *>(&Al[0][row * XL + c4 * 4]) = l0;
-            *reinterpret_cast<uint2 *>(&Al[1][row * XL + c4 * 4]) = l1;
-            *reinterpret_cast<uint2 *>(&Al[2][row * XL + c4 * 4]) = l2;
+            if constexpr (AF == AF_X3) {
+                // chunk part p of a row = bf16 elements 8p..8p+7 of [limb0|limb1|limb2]
+                const int c = tid + 256 * i, row = c / 12, part = c % 12;
+                *reinterpret_cast<uint4 *>(&Al[row * AROW + part * 8]) = a[i];
+            } else {
+                const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
+                uint2 l0, l1, l2;
+                split4(make_float4(__uint_as_float(a[i].x), __uint_as_float(a[i].y), __uint_as_float(a[i].z),
+                                   __uint_as_float(a[i].w)),
+                       l0, l1, l2);
+                *reinterpret_cast<uint2 *>(&Al[row * AROW + c4 * 4]) = l0;
+                *reinterpret_cast<uint2 *>(&Al[row * AROW + 32 + c4 * 4]) = l1;
+                *reinterpret_cast<uint2 *>(&Al[row * AROW + 64 + c4 * 4]) = l2;
+            }
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; i++) {
             const int idx = tid + 256 * i, col = idx >> 1, part = idx & 1;
             if (idx >= B_ITEMS) continue;
-            const unsigned w[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+            const unsigned w[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
             if constexpr (WF == WF_Q8) {
                 // 16 int8 = elements 16*part .. 16*part+15, exact in bf16
                 unsigned o[8];
@@ -151,8 +176,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X,
                 for (int p = 0; p < 8; p++) {
                     const unsigned word = w[p >> 1];
                     const int sh = (p & 1) * 16;
-                    o[p] = pack_bf16((float)(signed char)((word >> sh) & 0xFF),
-                                     (float)(signed char)((word >> (sh + 8)) & 0xFF));
+                    o[p] = pack_exact((float)(signed char)((word >> sh) & 0xFF),
+                                      (float)(signed char)((word >> (sh + 8)) & 0xFF));
                 }
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16]) = make_uint4(o[0], o[1], o[2], o[3]);
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16 + 8]) = make_uint4(o[4], o[5], o[6], o[7]);
@@ -164,14 +189,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X,
                     const unsigned word = w[p >> 1];
                     const int sh = (p & 1) * 16;
                     const unsigned b0 = (word >> sh) & 0xFF, b1 = (word >> (sh + 8)) & 0xFF;
-                    lo[p] = pack_bf16((float)((int)(b0 & 0xF) - 8), (float)((int)(b1 & 0xF) - 8));
-                    hi[p] = pack_bf16((float)((int)(b0 >> 4) - 8), (float)((int)(b1 >> 4) - 8));
+                    lo[p] = pack_exact((float)((int)(b0 & 0xF) - 8), (float)((int)(b1 & 0xF) - 8));
+                    hi[p] = pack_exact((float)((int)(b0 >> 4) - 8), (float)((int)(b1 >> 4) - 8));
                 }
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 8]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + 16 + part * 8]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
             }
         }
-        if (tid < BN) Ss[tid] = rs;
+        if (tid < BN) Ss[tid] = sc;
     };
 
     f32x16 acc[MT][NT];
@@ -182,50 +207,60 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X,
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
 
-    gload(0);
-    for (int kb = 0; kb < KB; kb++) {
-        __syncthreads();  // every wave is done reading the previous block
-        sstore();
-        __syncthreads();
-        if (kb + 1 < KB) gload(kb + 1);  // in flight during this block's MFMAs
-
-        f32x16 tmp[MT][NT];
+    auto compute = [&]() {
+        // A operands of this wave's rows for both k-halves and all three limbs
+        bf16x8 a[2][3][MT];
 #pragma unroll
-        for (int kh = 0; kh < 2; kh++) {
-            bf16x8 a[MT][3], b[NT];
-#pragma unroll
-            for (int r = 0; r < MT; r++)
-#pragma unroll
-                for (int l = 0; l < 3; l++)
-                    a[r][l] = *reinterpret_cast<const bf16x8 *>(
-                        &Al[l][(wm * (BM / 2) + r * 32 + li) * XL + kh * 16 + hh * 8]);
-#pragma unroll
-            for (int c = 0; c < NT; c++)
-                b[c] = *reinterpret_cast<const bf16x8 *>(&Bl[(wn * (BN / 2) + c * 32 + li) * XL + kh * 16 + hh * 8]);
+        for (int kh = 0; kh < 2; kh++)
 #pragma unroll
             for (int l = 0; l < 3; l++)
 #pragma unroll
                 for (int r = 0; r < MT; r++)
+                    a[kh][l][r] = *reinterpret_cast<const bf16x8 *>(
+                        &Al[(wm * (BM / 2) + r * 32 + li) * AROW + l * 32 + kh * 16 + hh * 8]);
 #pragma unroll
-                    for (int c = 0; c < NT; c++) {
+        for (int c = 0; c < NT; c++) {
+            const int col = wn * (BN / 2) + c * 32 + li;
+            f32x16 tmp[MT];
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++) {
+                const bf16x8 b = *reinterpret_cast<const bf16x8 *>(&Bl[col * XL + kh * 16 + hh * 8]);
+#pragma unroll
+                for (int l = 0; l < 3; l++)
+#pragma unroll
+                    for (int r = 0; r < MT; r++) {
                         if (kh == 0 && l == 0) {
                             f32x16 z;
 #pragma unroll
                             for (int q = 0; q < 16; q++) z[q] = 0.0f;
-                            tmp[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][l], b[c], z, 0, 0, 0);
+                            tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kh][l][r], b, z, 0, 0, 0);
                         } else {
-                            tmp[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][l], b[c], tmp[r][c], 0, 0, 0);
+                            tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kh][l][r], b, tmp[r], 0, 0, 0);
                         }
                     }
-        }
-#pragma unroll
-        for (int c = 0; c < NT; c++) {
-            const float d = Ss[wn * (BN / 2) + c * 32 + li];
+            }
+            const float d = Ss[col];
 #pragma unroll
             for (int r = 0; r < MT; r++)
 #pragma unroll
-                for (int q = 0; q < 16; q++) acc[r][c][q] += d * tmp[r][c][q];
+                for (int q = 0; q < 16; q++) acc[r][c][q] += d * tmp[r][q];
         }
+    };
+
+    gload(0, ra[0], rb[0], rs[0]);
+    if (KB > 1) gload(1, ra[1], rb[1], rs[1]);
+    for (int kb = 0; kb < KB; kb += 2) {
+        __syncthreads();  // every wave is done reading the previous block
+        sstore(ra[0], rb[0], rs[0]);
+        __syncthreads();
+        if (kb + 2 < KB) gload(kb + 2, ra[0], rb[0], rs[0]);
+        compute();
+        if (kb + 1 >= KB) break;
+        __syncthreads();
+        sstore(ra[1], rb[1], rs[1]);
+        __syncthreads();
+        if (kb + 3 < KB) gload(kb + 3, ra[1], rb[1], rs[1]);
+        compute();
     }
 
 #pragma unroll
@@ -240,50 +275,61 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const float *__restrict__ X,
                 const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
                 if (row < M) {
                     float v = acc[r][c][q] + bv;
-                    float *dst = Y + (size_t)row * ldy + col;
-                    if constexpr (EPI == EPI_GELU) v = gelu_ref3(v);
-                    if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
-                    *dst = v;
+                    if constexpr (EPI == EPI_GELU_X3) {
+                        x3_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_ref3(v));
+                    } else {
+                        float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
+                        if constexpr (EPI == EPI_GELU) v = gelu_ref3(v);
+                        if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+                        *dst = v;
+                    }
                 }
             }
     }
 }
 
-template <int WF, int EPI, int BM, int BN>
-static hipError_t launch_x3_t(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
-                              int M, hipStream_t st) {
+template <int WF, int EPI, int BM, int BN, int AF>
+static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy, int M,
+                              hipStream_t st) {
     const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc, bias, Y,
+    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc, bias, Y,
                        ldy, M, W.N, W.K);
     return hipGetLastError();
 }
 
-template <int WF, int EPI>
-static hipError_t launch_x3_shape(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
+template <int WF, int EPI, int AF>
+static hipError_t launch_x3_shape(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
                                   int M, hipStream_t st) {
     const bool small_m = M <= 64, small_n = W.N <= 64;
-    if (small_m && small_n) return launch_x3_t<WF, EPI, 64, 64>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_m) return launch_x3_t<WF, EPI, 64, 128>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_n) return launch_x3_t<WF, EPI, 128, 64>(W, X, ldx, bias, Y, ldy, M, st);
-    return launch_x3_t<WF, EPI, 128, 128>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_m && small_n) return launch_x3_t<WF, EPI, 64, 64, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_m) return launch_x3_t<WF, EPI, 64, 128, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_n) return launch_x3_t<WF, EPI, 128, 64, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    return launch_x3_t<WF, EPI, 128, 128, AF>(W, X, ldx, bias, Y, ldy, M, st);
 }
 
-template <int WF>
-static hipError_t launch_x3_epi(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
+template <int WF, int AF>
+static hipError_t launch_x3_epi(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
                                 int M, int epi, hipStream_t st) {
     switch (epi) {
-    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU>(W, X, ldx, bias, Y, ldy, M, st);
-    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL>(W, X, ldx, bias, Y, ldy, M, st);
-    default: return launch_x3_shape<WF, EPI_NONE>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    default: return launch_x3_shape<WF, EPI_NONE, AF>(W, X, ldx, bias, Y, ldy, M, st);
     }
 }
 
-hipError_t launch_gemm_x3(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
-                          int epi, hipStream_t st) {
+hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
+                          int M, int epi, hipStream_t st) {
     if (M <= 0) return hipSuccess;
-    if (W.K % 32 != 0 || ldx % 4 != 0) return hipErrorInvalidValue;
-    if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
+    if (epi == EPI_GELU_X3 && W.N % 32 != 0) return hipErrorInvalidValue;
+    if (a_fmt == AF_X3) {
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    } else {
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    }
     return hipErrorInvalidValue;
 }
 

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "x3.h"
+
 namespace cih {
 
 // Weight formats of the device-resident matrices.  All use a k-block-major
@@ -13,8 +15,9 @@ namespace cih {
 //   Q4 : qs [K/32][N][16] uint8,  sc [K/32][N] float   (reference nibble order)
 enum WFmt { WF_F32 = 0, WF_Q8 = 1, WF_Q4 = 2 };
 
-// GEMM epilogue applied to v = acc + bias[n]
-enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2 };
+// GEMM epilogue applied to v = acc + bias[n]; EPI_GELU_X3 writes gelu(v)
+// in the three-limb bf16 format of x3.h (for the next quantized GEMM).
+enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_GELU_X3 = 3 };
 
 struct DevMatrix {
     int fmt = WF_F32;
@@ -23,13 +26,14 @@ struct DevMatrix {
     const float *sc = nullptr; // per-block scales (quantized formats)
 };
 
-// Y[M][N] (row stride ldy) = epi(X[M][K] (row stride ldx) * W^T + bias)
-hipError_t launch_gemm(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y,
+// Y[M][N] (row stride ldy) = epi(X[M][K] * W^T + bias).  X is FP32 with row
+// stride ldx (a_fmt AF_F32) or three-limb bf16 (AF_X3, quantized W only).
+hipError_t launch_gemm(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
                        int ldy, int M, int epi, hipStream_t st);
 
 // Q8_0/Q4_0 GEMM on bf16 MFMA: exact integer weights, activations split
 // into three bf16 limbs (FP32-equivalent products), block scale in FP32.
-hipError_t launch_gemm_x3(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y,
+hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
                           int ldy, int M, int epi, hipStream_t st);
 
 // Dequantizes nblocks of a device matrix in k-block-major layout back to the
@@ -46,14 +50,15 @@ struct SeqMeta {
 hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *emb_q,
                         const float *emb_sc, int d, int V, float *x, hipStream_t st);
 
-// out = LayerNorm(x) over rows of width d (eps 1e-5)
-hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, int rows,
+// out = LayerNorm(x) over rows of width d (eps 1e-5); out_fmt AF_F32 or AF_X3
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, void *out, int out_fmt, int rows,
                             int d, hipStream_t st);
 
 // Bidirectional rotary attention over packed Q|K|V rows.  When P != nullptr
 // every softmax row is stored at P[b*pb + h*ph + q*S_max + k].
+// out: [T][d] FP32 (out_fmt AF_F32) or three-limb bf16 (AF_X3).
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos,
-                            const float *rope_sin, float *out, float *P, int64_t pb, int64_t ph,
+                            const float *rope_sin, void *out, int out_fmt, float *P, int64_t pb, int64_t ph,
                             hipStream_t st);
 
 // final_att[b][p][t] = sum_h P_h[p][t] * (1/H), h ascending

@@ -62,9 +62,9 @@ hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *
 
 // layer_norm (lib.rs:2556-2562): mean, variance of (x - mean), 1/sqrt(var +
 // 1e-5), out = w * (x - mean) * inv + b.  One wave per row.
-template <int PER>
+template <int PER, int OF>
 __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, const float *__restrict__ w,
-                                                   const float *__restrict__ b, float *__restrict__ out, int rows,
+                                                   const float *__restrict__ b, void *__restrict__ out, int rows,
                                                    int d) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -88,25 +88,37 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     }
     const float var = wave_sum(q) / (float)d;
     const float inv = 1.0f / sqrtf(var + 1e-5f);
-    float *orow = out + (size_t)row * d;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int c = lane + 64 * i;
-        if (c < d) orow[c] = w[c] * (v[i] - mean) * inv + b[c];
+        if (c < d) {
+            const float y = w[c] * (v[i] - mean) * inv + b[c];
+            if constexpr (OF == AF_X3)
+                x3_store(reinterpret_cast<unsigned short *>(out), row, c, d, y);
+            else
+                reinterpret_cast<float *>(out)[(size_t)row * d + c] = y;
+        }
     }
 }
 
-hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, int rows, int d,
-                            hipStream_t st) {
-    if (rows <= 0) return hipSuccess;
+template <int OF>
+static hipError_t launch_ln_t(const float *x, const float *w, const float *b, void *out, int rows, int d,
+                              hipStream_t st) {
     const dim3 grid((rows + 3) / 4), blk(256);
     const int per = (d + 63) / 64;
-    if (per <= 5) hipLaunchKernelGGL(k_layernorm<5>, grid, blk, 0, st, x, w, b, out, rows, d);
-    else if (per <= 10) hipLaunchKernelGGL(k_layernorm<10>, grid, blk, 0, st, x, w, b, out, rows, d);
-    else if (per <= 20) hipLaunchKernelGGL(k_layernorm<20>, grid, blk, 0, st, x, w, b, out, rows, d);
-    else if (per <= 40) hipLaunchKernelGGL(k_layernorm<40>, grid, blk, 0, st, x, w, b, out, rows, d);
+    if (per <= 5) hipLaunchKernelGGL((k_layernorm<5, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+    else if (per <= 10) hipLaunchKernelGGL((k_layernorm<10, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+    else if (per <= 20) hipLaunchKernelGGL((k_layernorm<20, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+    else if (per <= 40) hipLaunchKernelGGL((k_layernorm<40, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
     else return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, void *out, int out_fmt, int rows, int d,
+                            hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (out_fmt == AF_X3) return d % 32 ? hipErrorInvalidValue : launch_ln_t<AF_X3>(x, w, b, out, rows, d, st);
+    return launch_ln_t<AF_F32>(x, w, b, out, rows, d, st);
 }
 
 // final_layer_att (lib.rs:5201-5204, 5256-5261): acc = 0; acc += P_h * (1/H)

@@ -1,0 +1,55 @@
+// Three-limb bf16 activation format ("X3") shared by the producers
+// (LayerNorm, attention output, FC1's GELU epilogue) and the quantized GEMM.
+//
+// A row of K FP32 values is stored as K/32 chunks of 96 bf16:
+//   chunk kb = [limb0[32] | limb1[32] | limb2[32]]  for elements kb*32 .. kb*32+31
+// with x = limb0 + limb1 + limb2, limb0 = bf16(x), limb1 = bf16(x - limb0),
+// limb2 = bf16(x - limb0 - limb1) (round to nearest even): 24 significant
+// bits, so the split reproduces x to below FP32 rounding.  6 bytes/element.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace cih {
+
+enum AFmt { AF_F32 = 0, AF_X3 = 1 };
+
+__device__ __forceinline__ unsigned short bf16_bits(float x) {
+    return __builtin_bit_cast(unsigned short, (__bf16)x);
+}
+__device__ __forceinline__ float bf16_val(unsigned short b) { return __uint_as_float((unsigned)b << 16); }
+
+// element index of (row, col) limb l in an X3 matrix with K columns
+__device__ __forceinline__ size_t x3_index(size_t row, int col, int K, int l) {
+    return (row * (size_t)(K / 32) + (col >> 5)) * 96 + l * 32 + (col & 31);
+}
+
+__device__ __forceinline__ void x3_store(unsigned short *base, size_t row, int col, int K, float x) {
+    const unsigned short a = bf16_bits(x);
+    const float r1 = x - bf16_val(a);
+    const unsigned short b = bf16_bits(r1);
+    const unsigned short c = bf16_bits(r1 - bf16_val(b));
+    const size_t i = x3_index(row, col, K, 0);
+    base[i] = a;
+    base[i + 32] = b;
+    base[i + 64] = c;
+}
+
+// four consecutive columns col..col+3 (col % 4 == 0) as 8-byte stores per limb
+__device__ __forceinline__ void x3_store4(unsigned short *base, size_t row, int col, int K, float4 x) {
+    const float v[4] = {x.x, x.y, x.z, x.w};
+    unsigned short l[3][4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        l[0][e] = bf16_bits(v[e]);
+        const float r1 = v[e] - bf16_val(l[0][e]);
+        l[1][e] = bf16_bits(r1);
+        l[2][e] = bf16_bits(r1 - bf16_val(l[1][e]));
+    }
+    const size_t i = x3_index(row, col, K, 0);
+#pragma unroll
+    for (int k = 0; k < 3; k++)
+        *reinterpret_cast<uint2 *>(base + i + 32 * k) =
+            make_uint2((unsigned)l[k][0] | ((unsigned)l[k][1] << 16), (unsigned)l[k][2] | ((unsigned)l[k][3] << 16));
+}
+
+}  // namespace cih

@@ -69,11 +69,18 @@ def check_batch(cfg, w, seqs, flags, contact=None, nthreads=8, margin=2e-3):
     return got
 
 
+@pytest.mark.parametrize("act", ["f32", "x3"])
 @pytest.mark.parametrize("hd,H", [(16, 4), (24, 4), (32, 2), (64, 2)])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
-def test_forward_small_configs(hd, H, dtype):
+def test_forward_small_configs(hd, H, dtype, act, monkeypatch):
     """Every head size, every weight format, ragged batch crossing the 32-key
-    and 128-query tile edges, all outputs including contacts and maps."""
+    and 128-query tile edges, all outputs including contacts and maps; both
+    activation hand-offs to the quantized GEMMs (FP32, split in the GEMM; and
+    three-limb bf16 written by the producers, CIH_ACT=x3)."""
+    if act == "x3":
+        if dtype == 0:
+            pytest.skip("FP32 weights never use the three-limb hand-off")
+        monkeypatch.setenv("CIH_ACT", "x3")
     rng = np.random.default_rng(hd * 10 + dtype)
     d = hd * H
     cfg = ch.EsmConfig(d, 4 * d, 2, H)
