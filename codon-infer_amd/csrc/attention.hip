@@ -18,9 +18,11 @@
 // B operand straight from the accumulator registers: register s of lane
 // (j, half) holds key 8*(s/4) + 4*half + s%4, which is the k index that lane
 // supplies at step s.
-// Two passes over the keys: pass 1 keeps a running max/sum per lane, pass 2
-// recomputes the scores, forms p = exp(s - max) * (1/sum) exactly as the
-// reference does, optionally stores P, and accumulates P.V.
+// When probabilities are requested (attention maps, contacts, last-layer
+// map): two passes over the keys — pass 1 keeps a running max/sum per lane,
+// pass 2 recomputes the scores, forms p = exp(s - max) * (1/sum) exactly as
+// the reference does, stores P and accumulates P.V.  Otherwise one pass with
+// an online softmax (P.V accumulated unnormalised, divided by the sum once).
 // RoPE is applied while staging K into LDS and Q into registers, from the
 // host-built cos/sin tables (the reference's f32 powf/cos/sin values).
 #include "kernels.h"
@@ -29,7 +31,7 @@ namespace cih {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int HD>
+template <int HD, bool ONEPASS>
 __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
                                                    const int *__restrict__ lens, int S_max,
                                                    const float *__restrict__ rc, const float *__restrict__ rsn,
@@ -97,6 +99,74 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.w, qr[4 * s4 + 3], acc, 0, 0, 0);
         }
     };
+
+    if constexpr (ONEPASS) {
+        // ---- no probabilities requested: one pass with online softmax.
+        // The tile max is combined across the two lane halves so that both
+        // halves scale their P.V contributions by the same running max; the
+        // output is divided by the sum of exponentials at the end.
+        f32x16 oacc[DT];
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
+        float m = -INFINITY, l = 0.0f;
+        for (int kt0 = 0; kt0 < len; kt0 += 32) {
+            __syncthreads();
+            load_k(kt0);
+            load_v(kt0);
+            __syncthreads();
+            f32x16 acc;
+            scores(acc);
+            float sv[16];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                sv[q] = key < len ? acc[q] * inv_scale : -INFINITY;
+                tmax = fmaxf(tmax, sv[q]);
+            }
+            // key kt0 (< len) sits in half 0, so the combined tile max is finite
+            const float mn = fmaxf(m, fmaxf(tmax, __shfl_xor(tmax, 32)));
+            const float corr = expf(m - mn);
+            float p[16], sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                p[q] = expf(sv[q] - mn);
+                sum += p[q];
+            }
+            l = l * corr + sum;
+            m = mn;
+#pragma unroll
+            for (int t = 0; t < DT; t++) {
+#pragma unroll
+                for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
+#pragma unroll
+                for (int s2 = 0; s2 < 16; s2++) {
+                    const float v = Vs[(8 * (s2 >> 2) + 4 * hh + (s2 & 3)) * V_LD + t * 32 + li];
+                    oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, p[s2], oacc[t], 0, 0, 0);
+                }
+            }
+        }
+        const float inv_sum = 1.0f / (l + __shfl_xor(l, 32));
+        if (qi < len) {
+#pragma unroll
+            for (int t = 0; t < DT; t++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int dd = t * 32 + 8 * g + 4 * hh;
+                    if (dd >= HD) continue;
+                    const float4 v = make_float4(oacc[t][4 * g] * inv_sum, oacc[t][4 * g + 1] * inv_sum,
+                                                 oacc[t][4 * g + 2] * inv_sum, oacc[t][4 * g + 3] * inv_sum);
+                    if (out_fmt == AF_X3)
+                        x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                    else
+                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d +
+                                                    h * HD + dd) = v;
+                }
+        }
+        return;
+    }
 
     // ---- pass 1: running max / sum of exp per lane (16 keys per tile)
     float m = -INFINITY, l = 0.0f;
@@ -187,25 +257,21 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
     dim3 grid((sm.S_max + 127) / 128, H, sm.B);
+#define CIH_ATT(HDV)                                                                                          \
+    if (P)                                                                                                     \
+        hipLaunchKernelGGL((k_attention<HDV, false>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, \
+                           rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);       \
+    else                                                                                                       \
+        hipLaunchKernelGGL((k_attention<HDV, true>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max,  \
+                           rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
     switch (hd) {
-    case 16:
-        hipLaunchKernelGGL(k_attention<16>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
-        break;
-    case 24:
-        hipLaunchKernelGGL(k_attention<24>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
-        break;
-    case 32:
-        hipLaunchKernelGGL(k_attention<32>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
-        break;
-    case 64:
-        hipLaunchKernelGGL(k_attention<64>, grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,
-                           rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
-        break;
+    case 16: CIH_ATT(16) break;
+    case 24: CIH_ATT(24) break;
+    case 32: CIH_ATT(32) break;
+    case 64: CIH_ATT(64) break;
     default: return hipErrorInvalidValue;
     }
+#undef CIH_ATT
     return hipGetLastError();
 }
 
