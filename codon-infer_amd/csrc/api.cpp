@@ -52,6 +52,7 @@ struct Workspace {
     float *rope_c = nullptr, *rope_s = nullptr;
     float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
     float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
+    GemvScratch gemv;                                   // split-K partial sums of the GEMV path
     // device staging of outputs for host-pointer calls (padded layouts)
     float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
           *o_layer = nullptr;
@@ -235,12 +236,20 @@ double wbytes(const DevMatrix &W) {
     return W.fmt == WF_F32 ? 4.0 * e : (W.fmt == WF_Q8 ? 1.125 * e : 0.625 * e);
 }
 
+// A few tokens go to the weight-streaming GEMV (CIH_GEMV=0 turns it off).
+bool use_gemv(int M, int a_fmt, int epi) {
+    const char *e = getenv("CIH_GEMV");
+    return !(e && !std::strcmp(e, "0")) && M <= GEMV_MAX_M && a_fmt == AF_F32 && epi != EPI_GELU_X3;
+}
+
 hipError_t gemm(cih_model *m, const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
                 int M, int epi) {
     const double flops = 2.0 * M * W.N * W.K;
     const double in_b = a_fmt == AF_X3 ? 6.0 : 4.0, out_b = epi == EPI_GELU_X3 ? 6.0 : 4.0;
     const double bytes = wbytes(W) + in_b * M * W.K + out_b * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
     ProfScope ps(m, W.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, flops, bytes);
+    if (use_gemv(M, a_fmt, epi))
+        return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, m->ws.gemv, m->stream);
     return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, m->stream);
 }
 
@@ -415,6 +424,18 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
                 ok(dalloc(ws.hbuf, T * std::max(F * 3 / 2, d), dl)) &&
                 ok(dalloc(ws.logits, T * V, dl)) && ok(dalloc(ws.rope_c, S * half, dl)) &&
                 ok(dalloc(ws.rope_s, S * half, dl));
+    if (good) {
+        size_t pf = 0;
+        std::vector<const DevMatrix *> mats = {&m->emb};
+        if (m->has_head) mats.insert(mats.end(), {&m->dense, &m->dec});
+        if (!m->layers.empty()) {
+            const Layer &ly = m->layers[0];
+            mats.insert(mats.end(), {&ly.wqkv, &ly.wo, &ly.w1, &ly.w2});
+        }
+        for (const DevMatrix *w : mats) pf = std::max(pf, gemv_part_floats(w->N, w->K));
+        ws.gemv.part_floats = pf;
+        good = ok(dalloc(ws.gemv.part, pf, dl));
+    }
     const bool need_P = flags & (CIH_OUT_CONTACTS | CIH_OUT_FINAL_ATT | CIH_OUT_ATTN);
     if (good && need_P) good = ok(dalloc(ws.P, B * H * S * S, dl));
     if (good && (flags & CIH_OUT_CONTACTS))
@@ -514,7 +535,7 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
     const char *qpath = getenv("CIH_QGEMM"), *apath = getenv("CIH_ACT");
     const bool x3 = m->dtype != DT_FP32 && !(qpath && !std::strcmp(qpath, "fp32")) &&
                     (apath && !std::strcmp(apath, "x3"));
-    const int af = x3 ? AF_X3 : AF_F32;
+    const int af = x3 && T > GEMV_MAX_M ? AF_X3 : AF_F32;
 
     m->prof.used = 0;
     {
@@ -561,7 +582,7 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
             HIPCHK(launch_layernorm(ws.x, ly.ln2w, ly.ln2b, ws.xb, af, T, d, st));
         }
-        HIPCHK(gemm(m, ly.w1, ws.xb, d, af, ly.b1, ws.hbuf, F, T, x3 ? EPI_GELU_X3 : EPI_GELU));
+        HIPCHK(gemm(m, ly.w1, ws.xb, d, af, ly.b1, ws.hbuf, F, T, af == AF_X3 ? EPI_GELU_X3 : EPI_GELU));
         HIPCHK(gemm(m, ly.w2, ws.hbuf, F, af, ly.b2, ws.x, d, T, EPI_RESIDUAL));
         if (want_layer) HIPCHK(launch_scatter_rows(ws.x, d, sm, t_layer + (size_t)l * S_max * d, (int64_t)L * S_max * d, st));
     }
@@ -667,8 +688,15 @@ int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w, c
     if (!rc) rc = upload(&tmp, db, bias, (size_t)out_dim);
     if (!rc && dalloc(dy, (size_t)seq_len * out_dim, tmp.allocs) != hipSuccess)
         rc = set_error(CIH_ERR_HIP, "allocation failed");
+    GemvScratch gs;
+    const bool gv = use_gemv(seq_len, AF_F32, EPI_NONE);
+    if (!rc && gv) {
+        gs.part_floats = gemv_part_floats(out_dim, in_dim);
+        if (dalloc(gs.part, gs.part_floats, tmp.allocs) != hipSuccess) rc = set_error(CIH_ERR_HIP, "allocation failed");
+    }
     if (!rc) {
-        hipError_t e = launch_gemm(tmp.emb, dx, in_dim, AF_F32, db, dy, out_dim, seq_len, EPI_NONE, nullptr);
+        hipError_t e = gv ? launch_gemv(tmp.emb, dx, in_dim, seq_len, db, dy, out_dim, EPI_NONE, gs, nullptr)
+                          : launch_gemm(tmp.emb, dx, in_dim, AF_F32, db, dy, out_dim, seq_len, EPI_NONE, nullptr);
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e == hipSuccess) e = hipMemcpy(out, dy, (size_t)seq_len * out_dim * 4, hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = set_error(CIH_ERR_HIP, "GEMM failed: %s", hipGetErrorString(e));

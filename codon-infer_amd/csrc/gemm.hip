@@ -25,17 +25,6 @@ namespace cih {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// erf_f32 (lib.rs:3485-3491, Abramowitz & Stegun 7.1.26) and gelu (3493-3498)
-__device__ __forceinline__ float erf_as(float x) {
-    float sign = x < 0.0f ? -1.0f : 1.0f;
-    float ax = fabsf(x);
-    float t = 1.0f / (1.0f + 0.3275911f * ax);
-    float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
-                       0.254829592f) * t * expf(-ax * ax);
-    return sign * y;
-}
-__device__ __forceinline__ float gelu_ref(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f)); }
-
 constexpr int A_LD = 36;    // floats per LDS row of the A tile (32 + 4 pad: conflict-free b128 reads)
 constexpr int F32_LD = 36;  // same for FP32 weight rows
 constexpr int Q8_LD = 48;   // bytes per LDS column of Q8 quants (32 + 16 pad)
@@ -247,7 +236,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const float *__restrict__ X, in
                 if (row < M) {
                     float v = acc[r][c][q] + bv;
                     float *dst = Y + (size_t)row * ldy + col;
-                    if constexpr (EPI == EPI_GELU) v = gelu_ref(v);
+                    if constexpr (EPI == EPI_GELU) v = gelu_as(v);
                     if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
                     *dst = v;
                 }

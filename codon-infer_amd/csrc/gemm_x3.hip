@@ -28,16 +28,6 @@ namespace cih {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ float erf_as3(float x) {
-    float sign = x < 0.0f ? -1.0f : 1.0f;
-    float ax = fabsf(x);
-    float t = 1.0f / (1.0f + 0.3275911f * ax);
-    float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
-                       0.254829592f) * t * expf(-ax * ax);
-    return sign * y;
-}
-__device__ __forceinline__ float gelu_ref3(float x) { return 0.5f * x * (1.0f + erf_as3(x * 0.70710678118654752440f)); }
-
 constexpr int XL = 40;    // bf16 per LDS column of B (32 + 8 pad): conflict-free 16-byte reads
 constexpr int AROW = 104; // bf16 per LDS row of A: 3 limbs x 32 + 8 pad (208 B, conflict-free)
 
@@ -276,10 +266,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                 if (row < M) {
                     float v = acc[r][c][q] + bv;
                     if constexpr (EPI == EPI_GELU_X3) {
-                        x3_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_ref3(v));
+                        x3_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
                     } else {
                         float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
-                        if constexpr (EPI == EPI_GELU) v = gelu_ref3(v);
+                        if constexpr (EPI == EPI_GELU) v = gelu_as(v);
                         if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
                         *dst = v;
                     }

@@ -19,6 +19,19 @@ enum WFmt { WF_F32 = 0, WF_Q8 = 1, WF_Q4 = 2 };
 // in the three-limb bf16 format of x3.h (for the next quantized GEMM).
 enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_GELU_X3 = 3 };
 
+// erf_f32 (src/lib.rs:3485-3491, Abramowitz & Stegun 7.1.26, |error| <= 1.5e-7)
+// and gelu(x) = 0.5 x (1 + erf(x / sqrt 2)) (src/lib.rs:3493-3498).
+__device__ __forceinline__ float erf_as(float x) {
+    const float sign = x < 0.0f ? -1.0f : 1.0f;
+    const float ax = fabsf(x);
+    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    const float y =
+        1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) *
+                   t * expf(-ax * ax);
+    return sign * y;
+}
+__device__ __forceinline__ float gelu_as(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f)); }
+
 struct DevMatrix {
     int fmt = WF_F32;
     int N = 0, K = 0;          // out_dim, in_dim
@@ -35,6 +48,21 @@ hipError_t launch_gemm(const DevMatrix &W, const void *X, int ldx, int a_fmt, co
 // into three bf16 limbs (FP32-equivalent products), block scale in FP32.
 hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
                           int ldy, int M, int epi, hipStream_t st);
+
+// Weight-streaming GEMV for M <= GEMV_MAX_M tokens (FP32 activations, epilogue
+// EPI_NONE / EPI_GELU / EPI_RESIDUAL).  With several k-splits the partial sums
+// go through `part` ([splits][M][N] floats) and a second kernel.
+constexpr int GEMV_MAX_M = 8;
+// 64-column groups, k-splits, k-blocks per wave (a split is 4 waves x nb blocks)
+struct GemvGrid { int cols = 0, splits = 0, nb = 0; };
+struct GemvScratch {
+    float *part = nullptr;
+    size_t part_floats = 0;
+};
+GemvGrid gemv_grid(int N, int K);
+size_t gemv_part_floats(int N, int K);  // partial-sum floats needed at M = GEMV_MAX_M
+hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const float *bias, float *Y, int ldy,
+                       int epi, const GemvScratch &s, hipStream_t st);
 
 // Dequantizes nblocks of a device matrix in k-block-major layout back to the
 // reference's row-major [N][K] FP32 (test path).

@@ -70,14 +70,18 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *xr = x + (size_t)row * d;
-    float v[PER];
+    // gamma and beta are requested with the row, so their latency overlaps the reductions
+    float v[PER], g[PER], be[PER];
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int c = lane + 64 * i;
         v[i] = c < d ? xr[c] : 0.0f;
-        s += v[i];
+        g[i] = c < d ? w[c] : 0.0f;
+        be[i] = c < d ? b[c] : 0.0f;
     }
+#pragma unroll
+    for (int i = 0; i < PER; i++) s += v[i];
     const float mean = wave_sum(s) / (float)d;
     float q = 0.0f;
 #pragma unroll
@@ -92,7 +96,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     for (int i = 0; i < PER; i++) {
         const int c = lane + 64 * i;
         if (c < d) {
-            const float y = w[c] * (v[i] - mean) * inv + b[c];
+            const float y = g[i] * (v[i] - mean) * inv + be[i];
             if constexpr (OF == AF_X3)
                 x3_store(reinterpret_cast<unsigned short *>(out), row, c, d, y);
             else

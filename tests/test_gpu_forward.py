@@ -138,13 +138,36 @@ def test_forward_preset_archs(arch, dtype, B, lo, hi):
 
 
 def test_forward_650m_q8_short():
-    """The headline architecture (650M, Q8_0) on two short sequences."""
+    """The headline architecture (650M, Q8_0) on two short sequences, then on
+    six residues alone (8 tokens: every linear layer on the GEMV path)."""
     rng = np.random.default_rng(12)
     cfg = ch.EsmConfig.esm2_650m()
     w = ch.EsmWeights.random(cfg, seed=2, bias_std=0.02).quantize_q8()
     seqs = [rand_tokens(rng, 62), rand_tokens(rng, 40)]
     print("650M Q8 short", flush=True)
     check_batch(cfg, w, seqs, ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT, nthreads=16)
+    print("650M Q8 GEMV path (T = 8)", flush=True)
+    check_batch(cfg, w, [rand_tokens(rng, 6)], ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT, nthreads=16)
+
+
+@pytest.mark.parametrize("gemv", ["on", "off"])
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_forward_few_tokens(dtype, gemv, monkeypatch):
+    """Batches of at most 8 tokens in total run every linear layer on the
+    weight-streaming GEMV (CIH_GEMV=0: on the MFMA GEMMs); all outputs, with
+    a <mask>, a sequence with no residues (BOS, EOS) and contacts."""
+    if gemv == "off":
+        monkeypatch.setenv("CIH_GEMV", "0")
+    rng = np.random.default_rng(21 + dtype)
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = quantized(ch.EsmWeights.random(cfg, seed=5 + dtype, bias_std=0.02), dtype)
+    cw = rng.standard_normal(cfg.n_layers * cfg.n_heads).astype(np.float32)
+    for lens in ([2], [1, 2], [0, 1, 1], [6]):  # at most 8 tokens per batch
+        seqs = [rand_tokens(rng, n) for n in lens]
+        if len(seqs[0]) > 3:
+            seqs[0][2] = 32
+        print(f"few tokens dtype={dtype} gemv={gemv} residues={lens}", flush=True)
+        check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(0.25)))
 
 
 def test_tied_embedding_decoder():

@@ -1,5 +1,6 @@
-"""GPU parity of the dequantizing GEMM and the device block decode against
-the oracle (oracle/cpu_ref.c: matmul_tiled_* restatement, lib.rs:4766-4961).
+"""GPU parity of the dequantizing GEMM, the weight-streaming GEMV (M <= 8
+tokens) and the device block decode against the oracle (oracle/cpu_ref.c:
+matmul_tiled_* restatement, lib.rs:4766-4961).
 
 Tolerance (FP32 accumulate, different summation order): per element
 |gpu - oracle| <= 2e-6 * sum_k |x_k w_k| + 1e-7.
@@ -31,6 +32,7 @@ def _weights(dtype, N, K, rng):
 def test_gemm_matches_oracle(dtype, N, K, path, monkeypatch):
     """Both quantized GEMM kernels: the default bf16-limb MFMA kernel (x3)
     and the FP32-MFMA kernel selected by CIH_QGEMM=fp32."""
+    monkeypatch.setenv("CIH_GEMV", "0")  # small M also through the MFMA kernels
     if path == "fp32":
         monkeypatch.setenv("CIH_QGEMM", "fp32")
     elif dtype == 0:
@@ -46,6 +48,30 @@ def test_gemm_matches_oracle(dtype, N, K, path, monkeypatch):
         scale = np.abs(x.reshape(M, K)).astype(np.float64) @ np.abs(wd.reshape(N, K)).astype(np.float64).T
         err = np.abs(got.astype(np.float64) - ref)
         assert np.all(err <= 2e-6 * scale + 1e-7), (M, N, K, float(err.max()), float((err / (scale + 1e-30)).max()))
+
+
+# (N, K) chosen to cover every GEMV grid shape: one split (K <= 128), one
+# block per wave (1280x1280), two (1280x5120), four (5120x5120), a split with
+# a partly filled last wave (K = 480), columns not a multiple of 64 (33, 1000).
+GEMV_SHAPES = [(96, 64), (33, 320), (1280, 1280), (1280, 5120), (5120, 5120), (480, 480), (1000, 480), (3840, 1280)]
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+@pytest.mark.parametrize("N,K", GEMV_SHAPES)
+def test_gemv_matches_oracle(dtype, N, K):
+    rng = np.random.default_rng(N * 3 + K + dtype)
+    w, wd = _weights(dtype, N, K, rng)
+    bias = rng.standard_normal(N, dtype=np.float32) * np.float32(0.02)
+    for M in range(1, 9):
+        x = rng.standard_normal(M * K, dtype=np.float32)
+        print(f"gemv dtype={dtype} M={M} N={N} K={K}", flush=True)
+        got = ch.matmul_tiled(dtype, x, w, bias, K, N)
+        ref = cr.matmul_tiled(dtype, x, w, bias, K, N, num_threads=8)
+        scale = np.abs(x.reshape(M, K)).astype(np.float64) @ np.abs(wd.reshape(N, K)).astype(np.float64).T
+        err = np.abs(got.astype(np.float64) - ref)
+        assert np.all(err <= 2e-6 * scale + 1e-7), (M, N, K, float(err.max()), float((err / (scale + 1e-30)).max()))
+        # repeated calls give identical bits (split-K order does not depend on scheduling)
+        assert np.array_equal(ch.matmul_tiled(dtype, x, w, bias, K, N).view(np.uint32), got.view(np.uint32))
 
 
 @pytest.mark.parametrize("dtype", [1, 2])
