@@ -1,25 +1,32 @@
-// Quantized GEMM on bf16 MFMA with exact integer weights:
+// Quantized GEMM on 16-bit MFMA with exact integer weights:
 //   Y = epi(X * W^T + b),  W in Q8_0 / Q4_0 blocks of 32.
 //
 // Same result as matmul_tiled_q8/q4_parallel (codon-infer src/lib.rs:4870,
 // 4937) to FP32 rounding, several times the FP32-MFMA rate:
-//   * The block's quants q (|q| <= 127, or -8..7 for Q4_0) are exact in bf16.
-//   * Each FP32 activation is split into three bf16 limbs
-//     x = b0 + b1 + b2 (b0 = bf16(x), b1 = bf16(x - b0), b2 = bf16(x - b0 - b1)),
-//     24 significant bits: the split is exact to below FP32 rounding.
+//   * The block's quants q (|q| <= 127, or -8..7 for Q4_0) are exact in bf16
+//     and in f16.
+//   * Each FP32 activation is split into limbs whose sum carries (nearly) all
+//     of its 24 significant bits:
+//       LIMB_F16X2 (default): x = h0 + h1, h0 = f16(x), h1 = f16(x - h0):
+//         22-23 bits; relative error <= 2^-22, absolute <= 2^-25 (f16
+//         subnormals, which the f16 MFMA keeps); |x| must stay below 65520;
+//       LIMB_BF16X3: x = b0 + b1 + b2 (b0 = bf16(x), b1 = bf16(x - b0),
+//         b2 = bf16(x - b0 - b1)): 24 bits, full FP32 range.
 //   * Every limb x q product is exact in the MFMA's FP32 accumulator, so per
-//     32-element block tmp = sum_k (b0 + b1 + b2)_k q_k is the FP32 dot product
-//     of the block, and acc += d * tmp applies the block scale in FP32.
+//     32-element block tmp = sum_k (limbs)_k q_k is the FP32 dot product of
+//     the block, and acc += d * tmp applies the block scale in FP32.
 // The reference forms w = q*d first and then sums w*x (lib.rs:4687, 4724-4741,
 // 4476-4492); this is the same sum regrouped per block, with FP32 rounding.
 //
 // Tiling: 256 threads = 4 waves (2x2), workgroup tile BM x BN, BK = 32 = one
-// block.  v_mfma_f32_32x32x16_bf16: lane (i = lane%32, half = lane/32) feeds
+// block.  v_mfma_f32_32x32x16_{f16,bf16}: lane (i = lane%32, half = lane/32) feeds
 // the 8 elements 16*kh + 8*half + e of k-half kh.  For Q4_0 that is the low
 // nibbles (kh = 0) and high nibbles (kh = 1) of bytes 8*half..8*half+7: the
 // reference's packing.  The activation split and the integer-to-bf16
 // conversion happen once per workgroup while staging into LDS; the next
 // k-block is fetched into registers during the current block's MFMAs.
+#include <string.h>
+
 #include "kernels.h"
 #include "x3.h"
 
@@ -27,9 +34,15 @@ namespace cih {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int XL = 40;    // bf16 per LDS column of B (32 + 8 pad): conflict-free 16-byte reads
-constexpr int AROW = 104; // bf16 per LDS row of A: 3 limbs x 32 + 8 pad (208 B, conflict-free)
+enum Limb { LIMB_BF16X3 = 0, LIMB_F16X2 = 1 };
+template <int LIMB> struct LimbT;
+template <> struct LimbT<LIMB_BF16X3> { using V = bf16x8; static constexpr int NL = 3, AROW = 104; };
+template <> struct LimbT<LIMB_F16X2> { using V = f16x8; static constexpr int NL = 2, AROW = 72; };
+
+constexpr int XL = 40;    // 16-bit values per LDS column of B (32 + 8 pad): conflict-free 16-byte reads
+// A rows in LDS: NL limbs x 32 + 8 pad (208 B / 144 B)
 
 __device__ __forceinline__ unsigned pack_bf16(float lo, float hi) {
     // round-to-nearest-even f32 -> bf16 for both halves
@@ -55,6 +68,31 @@ __device__ __forceinline__ void split4(float4 x, uint2 &l0, uint2 &l1, uint2 &l2
     l2.y = pack_bf16(r2, r3);
 }
 
+// two f16 (round to nearest even) packed low | high << 16
+__device__ __forceinline__ unsigned pack_f16(float lo, float hi) {
+    const _Float16 a = (_Float16)lo, b = (_Float16)hi;
+    return (unsigned)__builtin_bit_cast(unsigned short, a) | ((unsigned)__builtin_bit_cast(unsigned short, b) << 16);
+}
+__device__ __forceinline__ float f16_lo(unsigned p) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(p & 0xFFFFu));
+}
+__device__ __forceinline__ float f16_hi(unsigned p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p >> 16)); }
+
+// x0..x3 -> two f16 limbs, each as two packed dwords
+__device__ __forceinline__ void split4_f16(float4 x, uint2 &l0, uint2 &l1) {
+    l0.x = pack_f16(x.x, x.y);
+    l0.y = pack_f16(x.z, x.w);
+    l1.x = pack_f16(x.x - f16_lo(l0.x), x.y - f16_hi(l0.x));
+    l1.y = pack_f16(x.z - f16_lo(l0.y), x.w - f16_hi(l0.y));
+}
+
+// 16-bit packing of two small integers (exact in both formats)
+template <int LIMB>
+__device__ __forceinline__ unsigned pack_int(float lo, float hi) {
+    if constexpr (LIMB == LIMB_F16X2) return pack_f16(lo, hi);
+    else return pack_exact(lo, hi);
+}
+
 __device__ __forceinline__ void tile_of3(int bid, int total, int nM, int nN, int &mt, int &nt) {
     constexpr int XCD = 8, GROUP_M = 8;
     int xcd = bid % XCD, local = bid / XCD;
@@ -69,7 +107,7 @@ __device__ __forceinline__ void tile_of3(int bid, int total, int nM, int nN, int
     nt = r / gsize;
 }
 
-template <int WF, int EPI, int BM, int BN, int AF>
+template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
 __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv, int ldx,
                                                     const void *__restrict__ Wq, const float *__restrict__ Wsc,
                                                     const float *__restrict__ bias, void *__restrict__ Yv, int ldy,
@@ -80,6 +118,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     constexpr int B_ITEMS = BN * 2;                  // (column, half of the block's bytes)
     constexpr int B_LOADS = (B_ITEMS + 255) / 256;
     constexpr int QB = WF == WF_Q8 ? 32 : 16;        // quant bytes per block
+    constexpr int NL = LimbT<LIMB>::NL, AROW = LimbT<LIMB>::AROW;
+    using V8 = typename LimbT<LIMB>::V;
+    static_assert(AF == AF_F32 || LIMB == LIMB_BF16X3, "the three-limb activation format is bf16");
     __shared__ __attribute__((aligned(16))) unsigned short Al[BM * AROW];
     __shared__ __attribute__((aligned(16))) unsigned short Bl[BN * XL];
     __shared__ float Ss[BN];
@@ -145,13 +186,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                 *reinterpret_cast<uint4 *>(&Al[row * AROW + part * 8]) = a[i];
             } else {
                 const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
-                uint2 l0, l1, l2;
-                split4(make_float4(__uint_as_float(a[i].x), __uint_as_float(a[i].y), __uint_as_float(a[i].z),
-                                   __uint_as_float(a[i].w)),
-                       l0, l1, l2);
-                *reinterpret_cast<uint2 *>(&Al[row * AROW + c4 * 4]) = l0;
-                *reinterpret_cast<uint2 *>(&Al[row * AROW + 32 + c4 * 4]) = l1;
-                *reinterpret_cast<uint2 *>(&Al[row * AROW + 64 + c4 * 4]) = l2;
+                const float4 xv = make_float4(__uint_as_float(a[i].x), __uint_as_float(a[i].y),
+                                              __uint_as_float(a[i].z), __uint_as_float(a[i].w));
+                if constexpr (LIMB == LIMB_F16X2) {
+                    uint2 l0, l1;
+                    split4_f16(xv, l0, l1);
+                    *reinterpret_cast<uint2 *>(&Al[row * AROW + c4 * 4]) = l0;
+                    *reinterpret_cast<uint2 *>(&Al[row * AROW + 32 + c4 * 4]) = l1;
+                } else {
+                    uint2 l0, l1, l2;
+                    split4(xv, l0, l1, l2);
+                    *reinterpret_cast<uint2 *>(&Al[row * AROW + c4 * 4]) = l0;
+                    *reinterpret_cast<uint2 *>(&Al[row * AROW + 32 + c4 * 4]) = l1;
+                    *reinterpret_cast<uint2 *>(&Al[row * AROW + 64 + c4 * 4]) = l2;
+                }
             }
         }
 #pragma unroll
@@ -160,14 +208,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
             if (idx >= B_ITEMS) continue;
             const unsigned w[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
             if constexpr (WF == WF_Q8) {
-                // 16 int8 = elements 16*part .. 16*part+15, exact in bf16
+                // 16 int8 = elements 16*part .. 16*part+15, exact in bf16 / f16
                 unsigned o[8];
 #pragma unroll
                 for (int p = 0; p < 8; p++) {
                     const unsigned word = w[p >> 1];
                     const int sh = (p & 1) * 16;
-                    o[p] = pack_exact((float)(signed char)((word >> sh) & 0xFF),
-                                      (float)(signed char)((word >> (sh + 8)) & 0xFF));
+                    o[p] = pack_int<LIMB>((float)(signed char)((word >> sh) & 0xFF),
+                                          (float)(signed char)((word >> (sh + 8)) & 0xFF));
                 }
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16]) = make_uint4(o[0], o[1], o[2], o[3]);
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16 + 8]) = make_uint4(o[4], o[5], o[6], o[7]);
@@ -179,8 +227,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                     const unsigned word = w[p >> 1];
                     const int sh = (p & 1) * 16;
                     const unsigned b0 = (word >> sh) & 0xFF, b1 = (word >> (sh + 8)) & 0xFF;
-                    lo[p] = pack_exact((float)((int)(b0 & 0xF) - 8), (float)((int)(b1 & 0xF) - 8));
-                    hi[p] = pack_exact((float)((int)(b0 >> 4) - 8), (float)((int)(b1 >> 4) - 8));
+                    lo[p] = pack_int<LIMB>((float)((int)(b0 & 0xF) - 8), (float)((int)(b1 & 0xF) - 8));
+                    hi[p] = pack_int<LIMB>((float)((int)(b0 >> 4) - 8), (float)((int)(b1 >> 4) - 8));
                 }
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 8]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + 16 + part * 8]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -198,15 +246,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
             for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
 
     auto compute = [&]() {
-        // A operands of this wave's rows for both k-halves and all three limbs
-        bf16x8 a[2][3][MT];
+        // A operands of this wave's rows for both k-halves and all limbs
+        V8 a[2][NL][MT];
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-            for (int l = 0; l < 3; l++)
+            for (int l = 0; l < NL; l++)
 #pragma unroll
                 for (int r = 0; r < MT; r++)
-                    a[kh][l][r] = *reinterpret_cast<const bf16x8 *>(
+                    a[kh][l][r] = *reinterpret_cast<const V8 *>(
                         &Al[(wm * (BM / 2) + r * 32 + li) * AROW + l * 32 + kh * 16 + hh * 8]);
 #pragma unroll
         for (int c = 0; c < NT; c++) {
@@ -214,19 +262,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
             f32x16 tmp[MT];
 #pragma unroll
             for (int kh = 0; kh < 2; kh++) {
-                const bf16x8 b = *reinterpret_cast<const bf16x8 *>(&Bl[col * XL + kh * 16 + hh * 8]);
+                const V8 b = *reinterpret_cast<const V8 *>(&Bl[col * XL + kh * 16 + hh * 8]);
 #pragma unroll
-                for (int l = 0; l < 3; l++)
+                for (int l = 0; l < NL; l++)
 #pragma unroll
                     for (int r = 0; r < MT; r++) {
+                        f32x16 c;
                         if (kh == 0 && l == 0) {
-                            f32x16 z;
 #pragma unroll
-                            for (int q = 0; q < 16; q++) z[q] = 0.0f;
-                            tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kh][l][r], b, z, 0, 0, 0);
+                            for (int q = 0; q < 16; q++) c[q] = 0.0f;
                         } else {
-                            tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kh][l][r], b, tmp[r], 0, 0, 0);
+                            c = tmp[r];
                         }
+                        if constexpr (LIMB == LIMB_F16X2)
+                            tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kh][l][r], b, c, 0, 0, 0);
+                        else
+                            tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kh][l][r], b, c, 0, 0, 0);
                     }
             }
             const float d = Ss[col];
@@ -278,33 +329,33 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     }
 }
 
-template <int WF, int EPI, int BM, int BN, int AF>
+template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
 static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy, int M,
                               hipStream_t st) {
     const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc, bias, Y,
-                       ldy, M, W.N, W.K);
+    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF, LIMB>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc,
+                       bias, Y, ldy, M, W.N, W.K);
     return hipGetLastError();
 }
 
-template <int WF, int EPI, int AF>
+template <int WF, int EPI, int AF, int LIMB>
 static hipError_t launch_x3_shape(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
                                   int M, hipStream_t st) {
     const bool small_m = M <= 64, small_n = W.N <= 64;
-    if (small_m && small_n) return launch_x3_t<WF, EPI, 64, 64, AF>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_m) return launch_x3_t<WF, EPI, 64, 128, AF>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_n) return launch_x3_t<WF, EPI, 128, 64, AF>(W, X, ldx, bias, Y, ldy, M, st);
-    return launch_x3_t<WF, EPI, 128, 128, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_m && small_n) return launch_x3_t<WF, EPI, 64, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_m) return launch_x3_t<WF, EPI, 64, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_n) return launch_x3_t<WF, EPI, 128, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    return launch_x3_t<WF, EPI, 128, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
 }
 
-template <int WF, int AF>
+template <int WF, int AF, int LIMB>
 static hipError_t launch_x3_epi(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
                                 int M, int epi, hipStream_t st) {
     switch (epi) {
-    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF>(W, X, ldx, bias, Y, ldy, M, st);
-    case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF>(W, X, ldx, bias, Y, ldy, M, st);
-    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF>(W, X, ldx, bias, Y, ldy, M, st);
-    default: return launch_x3_shape<WF, EPI_NONE, AF>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    default: return launch_x3_shape<WF, EPI_NONE, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
     }
 }
 
@@ -313,12 +364,18 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
     if (epi == EPI_GELU_X3 && W.N % 32 != 0) return hipErrorInvalidValue;
+    // FP32 activations: f16 two-limb split unless CIH_LIMBS=bf16x3
+    const char *lv = getenv("CIH_LIMBS");
+    const bool bf16 = lv && !strcmp(lv, "bf16x3");
     if (a_fmt == AF_X3) {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    } else if (bf16) {
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
     } else {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
     }
     return hipErrorInvalidValue;
 }

@@ -26,17 +26,20 @@ def _weights(dtype, N, K, rng):
     return q, wd
 
 
-@pytest.mark.parametrize("path", ["x3", "fp32"])
+@pytest.mark.parametrize("path", ["f16x2", "bf16x3", "fp32"])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
 @pytest.mark.parametrize("N,K", SHAPES)
 def test_gemm_matches_oracle(dtype, N, K, path, monkeypatch):
-    """Both quantized GEMM kernels: the default bf16-limb MFMA kernel (x3)
-    and the FP32-MFMA kernel selected by CIH_QGEMM=fp32."""
+    """Every quantized GEMM kernel: the default 16-bit MFMA kernel with f16
+    two-limb activations, its bf16 three-limb form (CIH_LIMBS=bf16x3) and the
+    FP32-MFMA kernel (CIH_QGEMM=fp32)."""
     monkeypatch.setenv("CIH_GEMV", "0")  # small M also through the MFMA kernels
     if path == "fp32":
         monkeypatch.setenv("CIH_QGEMM", "fp32")
     elif dtype == 0:
         pytest.skip("FP32 weights always use the FP32-MFMA kernel")
+    if path == "bf16x3":
+        monkeypatch.setenv("CIH_LIMBS", "bf16x3")
     rng = np.random.default_rng(N * 7 + K + dtype)
     w, wd = _weights(dtype, N, K, rng)
     bias = rng.standard_normal(N, dtype=np.float32) * np.float32(0.02)
@@ -72,6 +75,26 @@ def test_gemv_matches_oracle(dtype, N, K):
         assert np.all(err <= 2e-6 * scale + 1e-7), (M, N, K, float(err.max()), float((err / (scale + 1e-30)).max()))
         # repeated calls give identical bits (split-K order does not depend on scheduling)
         assert np.array_equal(ch.matmul_tiled(dtype, x, w, bias, K, N).view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("path", ["f16x2", "bf16x3"])
+def test_gemm_activation_range(path, monkeypatch):
+    """Activations spanning 1e-9 .. 3e4 (f16 subnormal to near its maximum):
+    the limb split keeps the FP32-accumulate error bound."""
+    monkeypatch.setenv("CIH_GEMV", "0")
+    if path == "bf16x3":
+        monkeypatch.setenv("CIH_LIMBS", "bf16x3")
+    rng = np.random.default_rng(77)
+    N, K, M = 256, 512, 96
+    w, wd = _weights(1, N, K, rng)
+    bias = np.zeros(N, np.float32)
+    mag = np.float32(10.0) ** rng.uniform(-9, 4.5, M * K).astype(np.float32)
+    x = (mag * np.sign(rng.standard_normal(M * K))).astype(np.float32)
+    got = ch.matmul_tiled(1, x, w, bias, K, N)
+    ref = cr.matmul_tiled(1, x, w, bias, K, N, num_threads=8)
+    scale = np.abs(x.reshape(M, K)).astype(np.float64) @ np.abs(wd.reshape(N, K)).astype(np.float64).T
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= 2e-6 * scale + 1e-7), float((err / (scale + 1e-30)).max())
 
 
 @pytest.mark.parametrize("dtype", [1, 2])
