@@ -239,13 +239,14 @@ double wbytes(const DevMatrix &W) {
 // A few tokens go to the weight-streaming GEMV (CIH_GEMV=0 turns it off).
 bool use_gemv(int M, int a_fmt, int epi) {
     const char *e = getenv("CIH_GEMV");
-    return !(e && !std::strcmp(e, "0")) && M <= GEMV_MAX_M && a_fmt == AF_F32 && epi != EPI_GELU_X3;
+    return !(e && !std::strcmp(e, "0")) && M <= GEMV_MAX_M && a_fmt == AF_F32 && epi != EPI_GELU_X3 &&
+           epi != EPI_GELU_H2;
 }
 
 hipError_t gemm(cih_model *m, const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
                 int M, int epi) {
     const double flops = 2.0 * M * W.N * W.K;
-    const double in_b = a_fmt == AF_X3 ? 6.0 : 4.0, out_b = epi == EPI_GELU_X3 ? 6.0 : 4.0;
+    const double in_b = a_fmt == AF_X3 ? 6.0 : 4.0, out_b = epi == EPI_GELU_X3 ? 6.0 : 4.0;  // H2: 4 B/element
     const double bytes = wbytes(W) + in_b * M * W.K + out_b * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
     ProfScope ps(m, W.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, flops, bytes);
     if (use_gemv(M, a_fmt, epi))
@@ -527,15 +528,23 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
           *t_final = dev_io ? out->final_att : ws.o_final, *t_contacts = dev_io ? out->contacts : ws.o_contacts,
           *t_attn = dev_io ? out->attn : ws.o_attn, *t_layer = dev_io ? out->layer_hidden : ws.o_layer;
 
-    // Activations reach the quantized GEMMs as FP32 and are split into bf16
-    // limbs inside the GEMM (measured faster at the 650M B=16 L=512 shape).
-    // CIH_ACT=x3 makes LayerNorm / attention / FC1's epilogue write the
-    // pre-split three-limb form instead; CIH_QGEMM=fp32 selects the FP32-MFMA
-    // GEMM (FP32 activations).
-    const char *qpath = getenv("CIH_QGEMM"), *apath = getenv("CIH_ACT");
-    const bool x3 = m->dtype != DT_FP32 && !(qpath && !std::strcmp(qpath, "fp32")) &&
-                    (apath && !std::strcmp(apath, "x3"));
-    const int af = x3 && T > GEMV_MAX_M ? AF_X3 : AF_F32;
+    // Activations reach the quantized GEMMs already split into f16 limbs
+    // (AF_H2, written by LayerNorm / attention / FC1's epilogue: same bytes as
+    // FP32, no conversion in the GEMM).  CIH_ACT=f32 hands over FP32 (split in
+    // the GEMM), CIH_ACT=x3 the three-limb bf16 form; CIH_LIMBS=bf16x3 and
+    // CIH_QGEMM=fp32 imply FP32 hand-off.  Batches of at most GEMV_MAX_M
+    // tokens take the GEMV, which reads FP32.
+    int af = AF_F32;
+    {
+        const char *qpath = getenv("CIH_QGEMM"), *apath = getenv("CIH_ACT"), *lpath = getenv("CIH_LIMBS");
+        const bool fp32_gemm = qpath && !std::strcmp(qpath, "fp32");
+        const bool bf16 = lpath && !std::strcmp(lpath, "bf16x3");
+        if (m->dtype != DT_FP32 && !fp32_gemm && T > GEMV_MAX_M) {
+            if (apath && !std::strcmp(apath, "x3")) af = AF_X3;
+            else if (!(apath && !std::strcmp(apath, "f32")) && !bf16) af = AF_H2;
+        }
+    }
+    const int epi_fc1 = af == AF_X3 ? EPI_GELU_X3 : (af == AF_H2 ? EPI_GELU_H2 : EPI_GELU);
 
     m->prof.used = 0;
     {
@@ -582,7 +591,7 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
             HIPCHK(launch_layernorm(ws.x, ly.ln2w, ly.ln2b, ws.xb, af, T, d, st));
         }
-        HIPCHK(gemm(m, ly.w1, ws.xb, d, af, ly.b1, ws.hbuf, F, T, af == AF_X3 ? EPI_GELU_X3 : EPI_GELU));
+        HIPCHK(gemm(m, ly.w1, ws.xb, d, af, ly.b1, ws.hbuf, F, T, epi_fc1));
         HIPCHK(gemm(m, ly.w2, ws.hbuf, F, af, ly.b2, ws.x, d, T, EPI_RESIDUAL));
         if (want_layer) HIPCHK(launch_scatter_rows(ws.x, d, sm, t_layer + (size_t)l * S_max * d, (int64_t)L * S_max * d, st));
     }

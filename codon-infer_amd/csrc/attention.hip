@@ -160,6 +160,8 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
                                                  oacc[t][4 * g + 2] * inv_sum, oacc[t][4 * g + 3] * inv_sum);
                     if (out_fmt == AF_X3)
                         x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                    else if (out_fmt == AF_H2)
+                        h2_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
                     else
                         *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d +
                                                     h * HD + dd) = v;
@@ -245,6 +247,8 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
                 const float4 v = make_float4(oacc[t][4 * g], oacc[t][4 * g + 1], oacc[t][4 * g + 2], oacc[t][4 * g + 3]);
                 if (out_fmt == AF_X3)
                     x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                else if (out_fmt == AF_H2)
+                    h2_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
                 else
                     *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d + h * HD + dd) = v;
             }
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
 
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos, const float *rope_sin,
                             void *out, int out_fmt, float *P, int64_t pb, int64_t ph, hipStream_t st) {
-    if (out_fmt == AF_X3 && d % 32) return hipErrorInvalidValue;
+    if ((out_fmt == AF_X3 || out_fmt == AF_H2) && d % 32) return hipErrorInvalidValue;
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
     dim3 grid((sm.S_max + 127) / 128, H, sm.B);

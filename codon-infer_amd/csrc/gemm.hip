@@ -278,15 +278,15 @@ hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, c
                        int M, int epi, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0) return hipErrorInvalidValue;
-    // Quantized weights go to the bf16-limb MFMA kernel (FP32 or pre-split
+    // Quantized weights go to the 16-bit-limb MFMA kernel (FP32 or pre-split
     // activations) unless CIH_QGEMM=fp32 selects the FP32-MFMA kernel, which
     // gives the same results to FP32 rounding and is kept for A/B runs.
     if (W.fmt != WF_F32) {
         const char *path = getenv("CIH_QGEMM");
-        if (a_fmt == AF_X3 || !(path && !strcmp(path, "fp32")))
+        if (a_fmt != AF_F32 || !(path && !strcmp(path, "fp32")))
             return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, st);
     }
-    if (a_fmt != AF_F32 || epi == EPI_GELU_X3 || ldx % 4 != 0) return hipErrorInvalidValue;
+    if (a_fmt != AF_F32 || epi == EPI_GELU_X3 || epi == EPI_GELU_H2 || ldx % 4 != 0) return hipErrorInvalidValue;
     const float *X = reinterpret_cast<const float *>(Xv);
     float *Y = reinterpret_cast<float *>(Yv);
     if (W.fmt == WF_Q8) return launch_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);

@@ -12,6 +12,8 @@
 //         subnormals, which the f16 MFMA keeps); |x| must stay below 65520;
 //       LIMB_BF16X3: x = b0 + b1 + b2 (b0 = bf16(x), b1 = bf16(x - b0),
 //         b2 = bf16(x - b0 - b1)): 24 bits, full FP32 range.
+//   Activations arrive as FP32 (split while staging) or already split by
+//   their producer (AF_H2 for f16 limbs, AF_X3 for bf16 limbs: x3.h).
 //   * Every limb x q product is exact in the MFMA's FP32 accumulator, so per
 //     32-element block tmp = sum_k (limbs)_k q_k is the FP32 dot product of
 //     the block, and acc += d * tmp applies the block scale in FP32.
@@ -86,6 +88,15 @@ __device__ __forceinline__ void split4_f16(float4 x, uint2 &l0, uint2 &l1) {
     l1.y = pack_f16(x.z - f16_lo(l0.y), x.w - f16_hi(l0.y));
 }
 
+// packed f16 pair minus (1152, 1152) / (1032, 1032); exact for the integer-valued inputs here
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned sub_f16x2(unsigned p, _Float16 c) {
+    const f16x2 v = __builtin_bit_cast(f16x2, p) - f16x2{c, c};
+    return __builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ unsigned sub1152(unsigned p) { return sub_f16x2(p, (_Float16)1152.0f); }
+__device__ __forceinline__ unsigned sub1032(unsigned p) { return sub_f16x2(p, (_Float16)1032.0f); }
+
 // 16-bit packing of two small integers (exact in both formats)
 template <int LIMB>
 __device__ __forceinline__ unsigned pack_int(float lo, float hi) {
@@ -113,14 +124,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                                                     const float *__restrict__ bias, void *__restrict__ Yv, int ldy,
                                                     int M, int N, int K) {
     constexpr int MT = BM / 64, NT = BN / 64;
-    // A tile per k-block: FP32 -> BM*8 float4 (split here); X3 -> BM*12 16-byte chunks (copied)
+    // A tile per k-block: FP32 -> BM*8 float4 (split here); X3 -> BM*12, H2 -> BM*8 16-byte chunks (copied)
     constexpr int A_LOADS = AF == AF_X3 ? BM * 12 / 256 : BM / 32;
     constexpr int B_ITEMS = BN * 2;                  // (column, half of the block's bytes)
     constexpr int B_LOADS = (B_ITEMS + 255) / 256;
     constexpr int QB = WF == WF_Q8 ? 32 : 16;        // quant bytes per block
     constexpr int NL = LimbT<LIMB>::NL, AROW = LimbT<LIMB>::AROW;
     using V8 = typename LimbT<LIMB>::V;
-    static_assert(AF == AF_F32 || LIMB == LIMB_BF16X3, "the three-limb activation format is bf16");
+    static_assert(AF == AF_F32 || (AF == AF_X3) == (LIMB == LIMB_BF16X3), "activation format / limb type mismatch");
+    static_assert(EPI != EPI_GELU_H2 || LIMB == LIMB_F16X2, "f16-limb epilogue with f16 limbs only");
     __shared__ __attribute__((aligned(16))) unsigned short Al[BM * AROW];
     __shared__ __attribute__((aligned(16))) unsigned short Bl[BN * XL];
     __shared__ float Ss[BN];
@@ -147,6 +159,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                 const int gr = m0 + row;
                 a[i] = gr < M ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const unsigned short *>(Xv) +
                                                                  ((size_t)gr * KB + kb) * 96 + part * 8)
+                              : make_uint4(0, 0, 0, 0);
+            } else if constexpr (AF == AF_H2) {
+                const int row = (tid >> 3) + 32 * i, part = tid & 7;
+                const int gr = m0 + row;
+                a[i] = gr < M ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const unsigned short *>(Xv) +
+                                                                 ((size_t)gr * KB + kb) * 64 + part * 8)
                               : make_uint4(0, 0, 0, 0);
             } else {
                 const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
@@ -184,6 +202,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                 // chunk part p of a row = bf16 elements 8p..8p+7 of [limb0|limb1|limb2]
                 const int c = tid + 256 * i, row = c / 12, part = c % 12;
                 *reinterpret_cast<uint4 *>(&Al[row * AROW + part * 8]) = a[i];
+            } else if constexpr (AF == AF_H2) {
+                // chunk part p of a row = f16 elements 8p..8p+7 of [hi|lo]
+                const int row = (tid >> 3) + 32 * i, part = tid & 7;
+                *reinterpret_cast<uint4 *>(&Al[row * AROW + part * 8]) = a[i];
             } else {
                 const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
                 const float4 xv = make_float4(__uint_as_float(a[i].x), __uint_as_float(a[i].y),
@@ -207,8 +229,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
             const int idx = tid + 256 * i, col = idx >> 1, part = idx & 1;
             if (idx >= B_ITEMS) continue;
             const unsigned w[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
-            if constexpr (WF == WF_Q8) {
-                // 16 int8 = elements 16*part .. 16*part+15, exact in bf16 / f16
+            if constexpr (WF == WF_Q8 && LIMB == LIMB_F16X2) {
+                // 16 int8 = elements 16*part .. 16*part+15.  Biased byte u = q + 128 placed
+                // under the f16 exponent of 1024 reads as 1024 + u; subtracting 1152 leaves q.
+                unsigned o[8];
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const unsigned u = w[p] ^ 0x80808080u;
+                    o[2 * p] = sub1152(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+                    o[2 * p + 1] = sub1152(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
+                }
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16]) = make_uint4(o[0], o[1], o[2], o[3]);
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16 + 8]) = make_uint4(o[4], o[5], o[6], o[7]);
+            } else if constexpr (WF == WF_Q8) {
+                // 16 int8 = elements 16*part .. 16*part+15, exact in bf16
                 unsigned o[8];
 #pragma unroll
                 for (int p = 0; p < 8; p++) {
@@ -219,6 +253,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                 }
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16]) = make_uint4(o[0], o[1], o[2], o[3]);
                 *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16 + 8]) = make_uint4(o[4], o[5], o[6], o[7]);
+            } else if constexpr (LIMB == LIMB_F16X2) {
+                // 8 bytes = elements 8*part+e (low nibble) and 16+8*part+e (high nibble);
+                // nibble n under the f16 exponent of 1024 reads as 1024 + n, minus 1032 = n - 8
+                unsigned lo[4], hi[4];
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const unsigned nl = w[p] & 0x0F0F0F0Fu, nh = (w[p] >> 4) & 0x0F0F0F0Fu;
+                    lo[2 * p] = sub1032(__builtin_amdgcn_perm(0x64646464u, nl, 0x04010400u));
+                    lo[2 * p + 1] = sub1032(__builtin_amdgcn_perm(0x64646464u, nl, 0x04030402u));
+                    hi[2 * p] = sub1032(__builtin_amdgcn_perm(0x64646464u, nh, 0x04010400u));
+                    hi[2 * p + 1] = sub1032(__builtin_amdgcn_perm(0x64646464u, nh, 0x04030402u));
+                }
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 8]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *reinterpret_cast<uint4 *>(&Bl[col * XL + 16 + part * 8]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
             } else {
                 // 8 bytes = elements 8*part+e (low nibble) and 16+8*part+e (high nibble)
                 unsigned lo[4], hi[4];
@@ -318,6 +366,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                     float v = acc[r][c][q] + bv;
                     if constexpr (EPI == EPI_GELU_X3) {
                         x3_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
+                    } else if constexpr (EPI == EPI_GELU_H2) {
+                        h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
                     } else {
                         float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
                         if constexpr (EPI == EPI_GELU) v = gelu_as(v);
@@ -354,6 +404,9 @@ static hipError_t launch_x3_epi(const DevMatrix &W, const void *X, int ldx, cons
     switch (epi) {
     case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
     case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_GELU_H2:
+        if constexpr (LIMB == LIMB_F16X2) return launch_x3_shape<WF, EPI_GELU_H2, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+        return hipErrorInvalidValue;
     case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
     default: return launch_x3_shape<WF, EPI_NONE, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
     }
@@ -363,11 +416,14 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
                           int M, int epi, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
-    if (epi == EPI_GELU_X3 && W.N % 32 != 0) return hipErrorInvalidValue;
+    if ((epi == EPI_GELU_X3 || epi == EPI_GELU_H2) && W.N % 32 != 0) return hipErrorInvalidValue;
     // FP32 activations: f16 two-limb split unless CIH_LIMBS=bf16x3
     const char *lv = getenv("CIH_LIMBS");
     const bool bf16 = lv && !strcmp(lv, "bf16x3");
-    if (a_fmt == AF_X3) {
+    if (a_fmt == AF_H2) {
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    } else if (a_fmt == AF_X3) {
         if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
         if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
     } else if (bf16) {

@@ -15,9 +15,9 @@ namespace cih {
 //   Q4 : qs [K/32][N][16] uint8,  sc [K/32][N] float   (reference nibble order)
 enum WFmt { WF_F32 = 0, WF_Q8 = 1, WF_Q4 = 2 };
 
-// GEMM epilogue applied to v = acc + bias[n]; EPI_GELU_X3 writes gelu(v)
-// in the three-limb bf16 format of x3.h (for the next quantized GEMM).
-enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_GELU_X3 = 3 };
+// GEMM epilogue applied to v = acc + bias[n]; EPI_GELU_X3 / EPI_GELU_H2 write
+// gelu(v) in the limb formats of x3.h (for the next quantized GEMM).
+enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_GELU_X3 = 3, EPI_GELU_H2 = 4 };
 
 // erf_f32 (src/lib.rs:3485-3491, Abramowitz & Stegun 7.1.26, |error| <= 1.5e-7)
 // and gelu(x) = 0.5 x (1 + erf(x / sqrt 2)) (src/lib.rs:3493-3498).
@@ -40,7 +40,8 @@ struct DevMatrix {
 };
 
 // Y[M][N] (row stride ldy) = epi(X[M][K] * W^T + bias).  X is FP32 with row
-// stride ldx (a_fmt AF_F32) or three-limb bf16 (AF_X3, quantized W only).
+// stride ldx (a_fmt AF_F32) or in a limb format of x3.h (AF_X3 / AF_H2,
+// quantized W only).
 hipError_t launch_gemm(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
                        int ldy, int M, int epi, hipStream_t st);
 

@@ -99,6 +99,8 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
             const float y = g[i] * (v[i] - mean) * inv + be[i];
             if constexpr (OF == AF_X3)
                 x3_store(reinterpret_cast<unsigned short *>(out), row, c, d, y);
+            else if constexpr (OF == AF_H2)
+                h2_store(reinterpret_cast<unsigned short *>(out), row, c, d, y);
             else
                 reinterpret_cast<float *>(out)[(size_t)row * d + c] = y;
         }
@@ -122,6 +124,7 @@ hipError_t launch_layernorm(const float *x, const float *w, const float *b, void
                             hipStream_t st) {
     if (rows <= 0) return hipSuccess;
     if (out_fmt == AF_X3) return d % 32 ? hipErrorInvalidValue : launch_ln_t<AF_X3>(x, w, b, out, rows, d, st);
+    if (out_fmt == AF_H2) return d % 32 ? hipErrorInvalidValue : launch_ln_t<AF_H2>(x, w, b, out, rows, d, st);
     return launch_ln_t<AF_F32>(x, w, b, out, rows, d, st);
 }
 

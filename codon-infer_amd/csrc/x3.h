@@ -1,6 +1,13 @@
-// Three-limb bf16 activation format ("X3") shared by the producers
-// (LayerNorm, attention output, FC1's GELU epilogue) and the quantized GEMM.
+// Limb activation formats shared by the producers (LayerNorm, attention
+// output, FC1's GELU epilogue) and the quantized GEMM, which then stages
+// activations into LDS without converting them.
 //
+// "H2": two f16 limbs, 4 bytes/element (the size of FP32).  A row of K values
+// is K/32 chunks of 64 f16:
+//   chunk kb = [hi[32] | lo[32]]  for elements kb*32 .. kb*32+31
+// with hi = f16(x), lo = f16(x - hi) (round to nearest even).
+//
+// "X3": three bf16 limbs, 6 bytes/element:
 // A row of K FP32 values is stored as K/32 chunks of 96 bf16:
 //   chunk kb = [limb0[32] | limb1[32] | limb2[32]]  for elements kb*32 .. kb*32+31
 // with x = limb0 + limb1 + limb2, limb0 = bf16(x), limb1 = bf16(x - limb0),
@@ -11,7 +18,7 @@
 
 namespace cih {
 
-enum AFmt { AF_F32 = 0, AF_X3 = 1 };
+enum AFmt { AF_F32 = 0, AF_X3 = 1, AF_H2 = 2 };
 
 __device__ __forceinline__ unsigned short bf16_bits(float x) {
     return __builtin_bit_cast(unsigned short, (__bf16)x);
@@ -48,6 +55,37 @@ __device__ __forceinline__ void x3_store4(unsigned short *base, size_t row, int 
     const size_t i = x3_index(row, col, K, 0);
 #pragma unroll
     for (int k = 0; k < 3; k++)
+        *reinterpret_cast<uint2 *>(base + i + 32 * k) =
+            make_uint2((unsigned)l[k][0] | ((unsigned)l[k][1] << 16), (unsigned)l[k][2] | ((unsigned)l[k][3] << 16));
+}
+
+__device__ __forceinline__ unsigned short f16_bits(float x) { return __builtin_bit_cast(unsigned short, (_Float16)x); }
+__device__ __forceinline__ float f16_val(unsigned short h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// element index of (row, col) limb l in an H2 matrix with K columns
+__device__ __forceinline__ size_t h2_index(size_t row, int col, int K, int l) {
+    return (row * (size_t)(K / 32) + (col >> 5)) * 64 + l * 32 + (col & 31);
+}
+
+__device__ __forceinline__ void h2_store(unsigned short *base, size_t row, int col, int K, float x) {
+    const unsigned short a = f16_bits(x);
+    const size_t i = h2_index(row, col, K, 0);
+    base[i] = a;
+    base[i + 32] = f16_bits(x - f16_val(a));
+}
+
+// four consecutive columns col..col+3 (col % 4 == 0) as 8-byte stores per limb
+__device__ __forceinline__ void h2_store4(unsigned short *base, size_t row, int col, int K, float4 x) {
+    const float v[4] = {x.x, x.y, x.z, x.w};
+    unsigned short l[2][4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        l[0][e] = f16_bits(v[e]);
+        l[1][e] = f16_bits(v[e] - f16_val(l[0][e]));
+    }
+    const size_t i = h2_index(row, col, K, 0);
+#pragma unroll
+    for (int k = 0; k < 2; k++)
         *reinterpret_cast<uint2 *>(base + i + 32 * k) =
             make_uint2((unsigned)l[k][0] | ((unsigned)l[k][1] << 16), (unsigned)l[k][2] | ((unsigned)l[k][3] << 16));
 }

@@ -69,18 +69,19 @@ def check_batch(cfg, w, seqs, flags, contact=None, nthreads=8, margin=2e-3):
     return got
 
 
-@pytest.mark.parametrize("act", ["f32", "x3"])
+@pytest.mark.parametrize("act", ["h2", "f32", "x3"])
 @pytest.mark.parametrize("hd,H", [(16, 4), (24, 4), (32, 2), (64, 2)])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
 def test_forward_small_configs(hd, H, dtype, act, monkeypatch):
     """Every head size, every weight format, ragged batch crossing the 32-key
-    and 128-query tile edges, all outputs including contacts and maps; both
-    activation hand-offs to the quantized GEMMs (FP32, split in the GEMM; and
-    three-limb bf16 written by the producers, CIH_ACT=x3)."""
-    if act == "x3":
-        if dtype == 0:
-            pytest.skip("FP32 weights never use the three-limb hand-off")
-        monkeypatch.setenv("CIH_ACT", "x3")
+    and 128-query tile edges, all outputs including contacts and maps; every
+    activation hand-off to the quantized GEMMs (h2: two f16 limbs written by
+    the producers, the default; f32: FP32 split in the GEMM, CIH_ACT=f32;
+    x3: three bf16 limbs written by the producers, CIH_ACT=x3)."""
+    if act != "h2" and dtype == 0:
+        pytest.skip("FP32 weights always hand over FP32")
+    if act != "h2":
+        monkeypatch.setenv("CIH_ACT", act)
     rng = np.random.default_rng(hd * 10 + dtype)
     d = hd * H
     cfg = ch.EsmConfig(d, 4 * d, 2, H)
