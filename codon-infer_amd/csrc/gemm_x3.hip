@@ -25,8 +25,11 @@
 // the 8 elements 16*kh + 8*half + e of k-half kh.  For Q4_0 that is the low
 // nibbles (kh = 0) and high nibbles (kh = 1) of bytes 8*half..8*half+7: the
 // reference's packing.  The activation split and the integer-to-bf16
-// conversion happen once per workgroup while staging into LDS; the next
-// k-block is fetched into registers during the current block's MFMAs.
+// conversion happen once per workgroup while staging into LDS; two LDS stages
+// alternate (one barrier per block) and the block after next is fetched into
+// registers during the current block's MFMAs.
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "kernels.h"
@@ -133,9 +136,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     using V8 = typename LimbT<LIMB>::V;
     static_assert(AF == AF_F32 || (AF == AF_X3) == (LIMB == LIMB_BF16X3), "activation format / limb type mismatch");
     static_assert(EPI != EPI_GELU_H2 || LIMB == LIMB_F16X2, "f16-limb epilogue with f16 limbs only");
-    __shared__ __attribute__((aligned(16))) unsigned short Al[BM * AROW];
-    __shared__ __attribute__((aligned(16))) unsigned short Bl[BN * XL];
-    __shared__ float Ss[BN];
+    // two LDS stages: block kb+1 is stored while block kb is multiplied (one barrier per block)
+    __shared__ __attribute__((aligned(16))) unsigned short Al2[2][BM * AROW];
+    __shared__ __attribute__((aligned(16))) unsigned short Bl2[2][BN * XL];
+    __shared__ float Ss2[2][BN];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -195,7 +199,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         sc = (tid < BN && gc < N) ? Wsc[(size_t)kb * N + gc] : 0.0f;
     };
 
-    auto sstore = [&](const uint4 (&a)[A_LOADS], const uint4 (&b)[B_LOADS], float sc) {
+    auto sstore = [&](int stg, const uint4 (&a)[A_LOADS], const uint4 (&b)[B_LOADS], float sc) {
+        unsigned short *Al = Al2[stg], *Bl = Bl2[stg];
+        float *Ss = Ss2[stg];
 #pragma unroll
         for (int i = 0; i < A_LOADS; i++) {
             if constexpr (AF == AF_X3) {
@@ -293,7 +299,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
 
-    auto compute = [&]() {
+    auto compute = [&](int stg) {
+        const unsigned short *Al = Al2[stg], *Bl = Bl2[stg];
+        const float *Ss = Ss2[stg];
         // A operands of this wave's rows for both k-halves and all limbs
         V8 a[2][NL][MT];
 #pragma unroll
@@ -339,17 +347,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     gload(0, ra[0], rb[0], rs[0]);
     if (KB > 1) gload(1, ra[1], rb[1], rs[1]);
     for (int kb = 0; kb < KB; kb += 2) {
-        __syncthreads();  // every wave is done reading the previous block
-        sstore(ra[0], rb[0], rs[0]);
+        // Stage 0 was last read by compute(kb - 2); every wave finished that before the
+        // previous iteration's barrier, so one barrier per block suffices.
+        sstore(0, ra[0], rb[0], rs[0]);
         __syncthreads();
         if (kb + 2 < KB) gload(kb + 2, ra[0], rb[0], rs[0]);
-        compute();
+        compute(0);
         if (kb + 1 >= KB) break;
-        __syncthreads();
-        sstore(ra[1], rb[1], rs[1]);
+        sstore(1, ra[1], rb[1], rs[1]);
         __syncthreads();
         if (kb + 3 < KB) gload(kb + 3, ra[1], rb[1], rs[1]);
-        compute();
+        compute(1);
     }
 
 #pragma unroll
@@ -388,14 +396,29 @@ static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const 
     return hipGetLastError();
 }
 
+// Tile shape: the largest of 128x128, 128x64, 64x128, 64x64 that still gives
+// at least 1024 workgroups (two rounds of two per CU), else 64x64.
+// CIH_GEMM_TILE=<BM>x<BN> forces one.
+static void pick_tile(int M, int N, int &bm, int &bn) {
+    const char *e = getenv("CIH_GEMM_TILE");
+    if (e && sscanf(e, "%dx%d", &bm, &bn) == 2 && (bm == 64 || bm == 128) && (bn == 64 || bn == 128)) return;
+    auto wgs = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
+    const long target = 1024;
+    if (M > 64 && N > 64 && wgs(128, 128) >= target) bm = 128, bn = 128;
+    else if (M > 64 && wgs(128, 64) >= target) bm = 128, bn = 64;
+    else if (N > 64 && wgs(64, 128) >= target) bm = 64, bn = 128;
+    else bm = 64, bn = 64;
+}
+
 template <int WF, int EPI, int AF, int LIMB>
 static hipError_t launch_x3_shape(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
                                   int M, hipStream_t st) {
-    const bool small_m = M <= 64, small_n = W.N <= 64;
-    if (small_m && small_n) return launch_x3_t<WF, EPI, 64, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_m) return launch_x3_t<WF, EPI, 64, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_n) return launch_x3_t<WF, EPI, 128, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    return launch_x3_t<WF, EPI, 128, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    int bm, bn;
+    pick_tile(M, W.N, bm, bn);
+    if (bm == 128 && bn == 128) return launch_x3_t<WF, EPI, 128, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    if (bm == 128) return launch_x3_t<WF, EPI, 128, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    if (bn == 128) return launch_x3_t<WF, EPI, 64, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    return launch_x3_t<WF, EPI, 64, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
 }
 
 template <int WF, int AF, int LIMB>

@@ -151,6 +151,31 @@ def test_forward_650m_q8_short():
     check_batch(cfg, w, [rand_tokens(rng, 6)], ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT, nthreads=16)
 
 
+def test_forward_headline_shape():
+    """The benchmark workload itself (650M Q8_0, B=16, L=512: the largest GEMM
+    tiles and the f16-limb hand-off at full size).  One sequence of the batch
+    against the oracle, another bit-identical alone and inside the batch."""
+    rng = np.random.default_rng(650)
+    cfg = ch.EsmConfig.esm2_650m()
+    w = ch.EsmWeights.random(cfg, seed=650, bias_std=0.02).quantize_q8()
+    seqs = [rand_tokens(rng, 510) for _ in range(16)]
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN
+    m = ch.GpuModel(cfg, w, max_batch=16, max_len=512, outputs=flags)
+    print("650M Q8 B=16 L=512", flush=True)
+    got = m.forward(seqs, flags)
+    ref = cr.forward(cfg, w, seqs[0], 16, final_att=False)
+    for name in ("logits", "hidden"):
+        e = float(np.abs(got[name][0].astype(np.float64) - ref[name]).max())
+        print(name, f"{e:.2e}", flush=True)
+        assert e <= TOL[name], (name, e)
+    top2 = np.sort(ref["logits"], axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 2e-3
+    assert np.array_equal(got["logits"][0].argmax(1)[clear], ref["logits"].argmax(1)[clear])
+    alone = m.forward([seqs[5]], flags)
+    assert np.array_equal(alone["logits"][0], got["logits"][5])
+    m.close()
+
+
 @pytest.mark.parametrize("gemv", ["on", "off"])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
 def test_forward_few_tokens(dtype, gemv, monkeypatch):

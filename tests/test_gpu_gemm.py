@@ -77,6 +77,27 @@ def test_gemv_matches_oracle(dtype, N, K):
         assert np.array_equal(ch.matmul_tiled(dtype, x, w, bias, K, N).view(np.uint32), got.view(np.uint32))
 
 
+@pytest.mark.parametrize("tile", ["128x128", "128x64", "64x128", "64x64"])
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_gemm_tile_shapes(tile, dtype, monkeypatch):
+    """Every workgroup tile of the 16-bit-limb kernel (CIH_GEMM_TILE forces
+    one), with row and column counts that end inside a tile."""
+    monkeypatch.setenv("CIH_GEMV", "0")
+    monkeypatch.setenv("CIH_GEMM_TILE", tile)
+    rng = np.random.default_rng(31 + dtype)
+    for N, K in [(1280, 1280), (200, 96), (33, 320)]:
+        w, wd = _weights(dtype, N, K, rng)
+        bias = rng.standard_normal(N, dtype=np.float32) * np.float32(0.02)
+        for M in (130, 512, 9):
+            x = rng.standard_normal(M * K, dtype=np.float32)
+            print(f"tile {tile} dtype={dtype} M={M} N={N} K={K}", flush=True)
+            got = ch.matmul_tiled(dtype, x, w, bias, K, N)
+            ref = cr.matmul_tiled(dtype, x, w, bias, K, N, num_threads=8)
+            scale = np.abs(x.reshape(M, K)).astype(np.float64) @ np.abs(wd.reshape(N, K)).astype(np.float64).T
+            err = np.abs(got.astype(np.float64) - ref)
+            assert np.all(err <= 2e-6 * scale + 1e-7), (M, N, K, float(err.max()))
+
+
 @pytest.mark.parametrize("path", ["f16x2", "bf16x3"])
 def test_gemm_activation_range(path, monkeypatch):
     """Activations spanning 1e-9 .. 3e4 (f16 subnormal to near its maximum):
