@@ -52,7 +52,7 @@ struct Workspace {
     float *rope_c = nullptr, *rope_s = nullptr;
     float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
     float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
-    GemvScratch gemv;                                   // split-K partial sums of the GEMV path
+    PartialBuf part;                                    // partial sums of k-split GEMMs / GEMVs
     // device staging of outputs for host-pointer calls (padded layouts)
     float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
           *o_layer = nullptr;
@@ -250,8 +250,8 @@ hipError_t gemm(cih_model *m, const DevMatrix &W, const void *X, int ldx, int a_
     const double bytes = wbytes(W) + in_b * M * W.K + out_b * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
     ProfScope ps(m, W.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, flops, bytes);
     if (use_gemv(M, a_fmt, epi))
-        return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, m->ws.gemv, m->stream);
-    return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, m->stream);
+        return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, m->ws.part, m->stream);
+    return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, &m->ws.part, m->stream);
 }
 
 }  // namespace
@@ -434,8 +434,8 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
             mats.insert(mats.end(), {&ly.wqkv, &ly.wo, &ly.w1, &ly.w2});
         }
         for (const DevMatrix *w : mats) pf = std::max(pf, gemv_part_floats(w->N, w->K));
-        ws.gemv.part_floats = pf;
-        good = ok(dalloc(ws.gemv.part, pf, dl));
+        ws.part.floats = std::max(pf, SPLITK_PART_FLOATS);
+        good = ok(dalloc(ws.part.part, ws.part.floats, dl));
     }
     const bool need_P = flags & (CIH_OUT_CONTACTS | CIH_OUT_FINAL_ATT | CIH_OUT_ATTN);
     if (good && need_P) good = ok(dalloc(ws.P, B * H * S * S, dl));
@@ -697,15 +697,13 @@ int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w, c
     if (!rc) rc = upload(&tmp, db, bias, (size_t)out_dim);
     if (!rc && dalloc(dy, (size_t)seq_len * out_dim, tmp.allocs) != hipSuccess)
         rc = set_error(CIH_ERR_HIP, "allocation failed");
-    GemvScratch gs;
+    PartialBuf gs;
     const bool gv = use_gemv(seq_len, AF_F32, EPI_NONE);
-    if (!rc && gv) {
-        gs.part_floats = gemv_part_floats(out_dim, in_dim);
-        if (dalloc(gs.part, gs.part_floats, tmp.allocs) != hipSuccess) rc = set_error(CIH_ERR_HIP, "allocation failed");
-    }
+    gs.floats = std::max(gemv_part_floats(out_dim, in_dim), SPLITK_PART_FLOATS);
+    if (!rc && dalloc(gs.part, gs.floats, tmp.allocs) != hipSuccess) rc = set_error(CIH_ERR_HIP, "allocation failed");
     if (!rc) {
         hipError_t e = gv ? launch_gemv(tmp.emb, dx, in_dim, seq_len, db, dy, out_dim, EPI_NONE, gs, nullptr)
-                          : launch_gemm(tmp.emb, dx, in_dim, AF_F32, db, dy, out_dim, seq_len, EPI_NONE, nullptr);
+                          : launch_gemm(tmp.emb, dx, in_dim, AF_F32, db, dy, out_dim, seq_len, EPI_NONE, &gs, nullptr);
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e == hipSuccess) e = hipMemcpy(out, dy, (size_t)seq_len * out_dim * 4, hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = set_error(CIH_ERR_HIP, "GEMM failed: %s", hipGetErrorString(e));

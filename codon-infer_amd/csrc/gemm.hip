@@ -275,7 +275,7 @@ static hipError_t launch_epi(const DevMatrix &W, const float *X, int ldx, const 
 }
 
 hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, const float *bias, void *Yv, int ldy,
-                       int M, int epi, hipStream_t st) {
+                       int M, int epi, const PartialBuf *pb, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0) return hipErrorInvalidValue;
     // Quantized weights go to the 16-bit-limb MFMA kernel (FP32 or pre-split
@@ -284,7 +284,7 @@ hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, c
     if (W.fmt != WF_F32) {
         const char *path = getenv("CIH_QGEMM");
         if (a_fmt != AF_F32 || !(path && !strcmp(path, "fp32")))
-            return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, st);
+            return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st);
     }
     if (a_fmt != AF_F32 || epi == EPI_GELU_X3 || epi == EPI_GELU_H2 || ldx % 4 != 0) return hipErrorInvalidValue;
     const float *X = reinterpret_cast<const float *>(Xv);

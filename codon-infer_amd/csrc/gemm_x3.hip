@@ -28,6 +28,7 @@
 // conversion happen once per workgroup while staging into LDS; two LDS stages
 // alternate (one barrier per block) and the block after next is fetched into
 // registers during the current block's MFMAs.
+#include <algorithm>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -125,7 +126,7 @@ template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
 __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv, int ldx,
                                                     const void *__restrict__ Wq, const float *__restrict__ Wsc,
                                                     const float *__restrict__ bias, void *__restrict__ Yv, int ldy,
-                                                    int M, int N, int K) {
+                                                    int M, int N, int K, int kps, float *__restrict__ part) {
     constexpr int MT = BM / 64, NT = BN / 64;
     // A tile per k-block: FP32 -> BM*8 float4 (split here); X3 -> BM*12, H2 -> BM*8 16-byte chunks (copied)
     constexpr int A_LOADS = AF == AF_X3 ? BM * 12 / 256 : BM / 32;
@@ -344,20 +345,38 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         }
     };
 
-    gload(0, ra[0], rb[0], rs[0]);
-    if (KB > 1) gload(1, ra[1], rb[1], rs[1]);
-    for (int kb = 0; kb < KB; kb += 2) {
+    // k-blocks [kb0, kend) of this split (all of K without split-K)
+    const int kb0 = blockIdx.y * kps, kend = min(KB, kb0 + kps);
+    gload(kb0, ra[0], rb[0], rs[0]);
+    if (kb0 + 1 < kend) gload(kb0 + 1, ra[1], rb[1], rs[1]);
+    for (int kb = kb0; kb < kend; kb += 2) {
         // Stage 0 was last read by compute(kb - 2); every wave finished that before the
         // previous iteration's barrier, so one barrier per block suffices.
         sstore(0, ra[0], rb[0], rs[0]);
         __syncthreads();
-        if (kb + 2 < KB) gload(kb + 2, ra[0], rb[0], rs[0]);
+        if (kb + 2 < kend) gload(kb + 2, ra[0], rb[0], rs[0]);
         compute(0);
-        if (kb + 1 >= KB) break;
+        if (kb + 1 >= kend) break;
         sstore(1, ra[1], rb[1], rs[1]);
         __syncthreads();
-        if (kb + 3 < KB) gload(kb + 3, ra[1], rb[1], rs[1]);
+        if (kb + 3 < kend) gload(kb + 3, ra[1], rb[1], rs[1]);
         compute(1);
+    }
+
+    if (part) {  // split-K: raw partial sums, bias and epilogue in k_splitk_reduce
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const int col = n0 + wn * (BN / 2) + c * 32 + li;
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    if (row < M) part[((size_t)blockIdx.y * M + row) * N + col] = acc[r][c][q];
+                }
+        }
+        return;
     }
 
 #pragma unroll
@@ -387,12 +406,52 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     }
 }
 
+// Y = epi(sum over splits of part[s] + bias), splits in order
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ part, int S, int M, int N,
+                                                       const float *__restrict__ bias, void *__restrict__ Yv, int ldy,
+                                                       int epi) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= M * N) return;
+    const int row = i / N, col = i - row * N;
+    const size_t MN = (size_t)M * N;
+    float v = part[i];
+    for (int s = 1; s < S; s++) v += part[s * MN + i];
+    v += bias ? bias[col] : 0.0f;
+    if (epi == EPI_GELU_X3) {
+        x3_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
+    } else if (epi == EPI_GELU_H2) {
+        h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
+    } else {
+        float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
+        if (epi == EPI_GELU) v = gelu_as(v);
+        if (epi == EPI_RESIDUAL) v += *dst;
+        *dst = v;
+    }
+}
+
 template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
 static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy, int M,
-                              hipStream_t st) {
-    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF, LIMB>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc,
-                       bias, Y, ldy, M, W.N, W.K);
+                              const PartialBuf *pb, hipStream_t st) {
+    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN, KB = W.K / 32;
+    // Split K when the tiles alone leave the GPU mostly idle: up to ~1024
+    // workgroups, at least 4 k-blocks per split, partials within pb.
+    int S = 1, kps = KB;
+    const char *e = getenv("CIH_SPLITK");
+    const long wgs = (long)nM * nN;
+    if (pb && pb->part && !(e && !strcmp(e, "0")) && wgs < 512 && KB >= 8) {
+        S = (int)std::min<long>(1024 / wgs, KB / 4);
+        while (S > 1 && (size_t)S * M * W.N > pb->floats) S--;
+        if (S > 1) {
+            kps = (KB + S - 1) / S;
+            S = (KB + kps - 1) / kps;
+        }
+    }
+    float *part = S > 1 ? pb->part : nullptr;
+    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF, LIMB>), dim3(nM * nN, S), dim3(256), 0, st, X, ldx, W.q, W.sc,
+                       bias, Y, ldy, M, W.N, W.K, kps, part);
+    if (S > 1)
+        hipLaunchKernelGGL(k_splitk_reduce, dim3((M * W.N + 255) / 256), dim3(256), 0, st, part, S, M, W.N, bias, Y,
+                           ldy, EPI);
     return hipGetLastError();
 }
 
@@ -412,31 +471,31 @@ static void pick_tile(int M, int N, int &bm, int &bn) {
 
 template <int WF, int EPI, int AF, int LIMB>
 static hipError_t launch_x3_shape(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
-                                  int M, hipStream_t st) {
+                                  int M, const PartialBuf *pb, hipStream_t st) {
     int bm, bn;
     pick_tile(M, W.N, bm, bn);
-    if (bm == 128 && bn == 128) return launch_x3_t<WF, EPI, 128, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    if (bm == 128) return launch_x3_t<WF, EPI, 128, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    if (bn == 128) return launch_x3_t<WF, EPI, 64, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    return launch_x3_t<WF, EPI, 64, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    if (bm == 128 && bn == 128) return launch_x3_t<WF, EPI, 128, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    if (bm == 128) return launch_x3_t<WF, EPI, 128, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    if (bn == 128) return launch_x3_t<WF, EPI, 64, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    return launch_x3_t<WF, EPI, 64, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
 }
 
 template <int WF, int AF, int LIMB>
 static hipError_t launch_x3_epi(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
-                                int M, int epi, hipStream_t st) {
+                                int M, int epi, const PartialBuf *pb, hipStream_t st) {
     switch (epi) {
-    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
     case EPI_GELU_H2:
-        if constexpr (LIMB == LIMB_F16X2) return launch_x3_shape<WF, EPI_GELU_H2, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+        if constexpr (LIMB == LIMB_F16X2) return launch_x3_shape<WF, EPI_GELU_H2, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
         return hipErrorInvalidValue;
-    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
-    default: return launch_x3_shape<WF, EPI_NONE, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    default: return launch_x3_shape<WF, EPI_NONE, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
     }
 }
 
 hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
-                          int M, int epi, hipStream_t st) {
+                          int M, int epi, const PartialBuf *pb, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
     if ((epi == EPI_GELU_X3 || epi == EPI_GELU_H2) && W.N % 32 != 0) return hipErrorInvalidValue;
@@ -444,17 +503,17 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     const char *lv = getenv("CIH_LIMBS");
     const bool bf16 = lv && !strcmp(lv, "bf16x3");
     if (a_fmt == AF_H2) {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
     } else if (a_fmt == AF_X3) {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
     } else if (bf16) {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
     } else {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
     }
     return hipErrorInvalidValue;
 }

@@ -216,13 +216,13 @@ static void launch_fmt(const DevMatrix &W, const float *X, int ldx, int M, const
 }
 
 hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const float *bias, float *Y, int ldy,
-                       int epi, const GemvScratch &s, hipStream_t st) {
+                       int epi, const PartialBuf &s, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     if (M > GEMV_MAX_M || W.K % 32 || ldx < W.K || ldx % 4 || ldy < W.N ||
         (epi != EPI_NONE && epi != EPI_GELU && epi != EPI_RESIDUAL))
         return hipErrorInvalidValue;
     const GemvGrid g = gemv_grid(W.N, W.K);
-    if (g.splits > 1 && (!s.part || s.part_floats < (size_t)g.splits * M * W.N)) return hipErrorInvalidValue;
+    if (g.splits > 1 && (!s.part || s.floats < (size_t)g.splits * M * W.N)) return hipErrorInvalidValue;
     if (W.fmt == WF_Q8) launch_fmt<WF_Q8>(W, X, ldx, M, bias, Y, ldy, epi, s.part, g, st);
     else if (W.fmt == WF_Q4) launch_fmt<WF_Q4>(W, X, ldx, M, bias, Y, ldy, epi, s.part, g, st);
     else launch_fmt<WF_F32>(W, X, ldx, M, bias, Y, ldy, epi, s.part, g, st);

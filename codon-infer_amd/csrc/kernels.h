@@ -39,31 +39,36 @@ struct DevMatrix {
     const float *sc = nullptr; // per-block scales (quantized formats)
 };
 
+// Device buffer for partial sums of k-split GEMMs and GEMVs (one stream uses
+// it at a time).  A split-K GEMM needs at most SPLITK_PART_FLOATS floats.
+struct PartialBuf {
+    float *part = nullptr;
+    size_t floats = 0;
+};
+constexpr size_t SPLITK_PART_FLOATS = (size_t)1024 * 64 * 64;
+
 // Y[M][N] (row stride ldy) = epi(X[M][K] * W^T + bias).  X is FP32 with row
 // stride ldx (a_fmt AF_F32) or in a limb format of x3.h (AF_X3 / AF_H2,
-// quantized W only).
+// quantized W only).  With pb, a GEMM too small to fill the GPU splits K
+// (CIH_SPLITK=0 disables).
 hipError_t launch_gemm(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
-                       int ldy, int M, int epi, hipStream_t st);
+                       int ldy, int M, int epi, const PartialBuf *pb, hipStream_t st);
 
 // Q8_0/Q4_0 GEMM on bf16 MFMA: exact integer weights, activations split
 // into three bf16 limbs (FP32-equivalent products), block scale in FP32.
 hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
-                          int ldy, int M, int epi, hipStream_t st);
+                          int ldy, int M, int epi, const PartialBuf *pb, hipStream_t st);
 
 // Weight-streaming GEMV for M <= GEMV_MAX_M tokens (FP32 activations, epilogue
 // EPI_NONE / EPI_GELU / EPI_RESIDUAL).  With several k-splits the partial sums
-// go through `part` ([splits][M][N] floats) and a second kernel.
+// go through pb ([splits][M][N] floats) and a second kernel.
 constexpr int GEMV_MAX_M = 8;
 // 64-column groups, k-splits, k-blocks per wave (a split is 4 waves x nb blocks)
 struct GemvGrid { int cols = 0, splits = 0, nb = 0; };
-struct GemvScratch {
-    float *part = nullptr;
-    size_t part_floats = 0;
-};
 GemvGrid gemv_grid(int N, int K);
 size_t gemv_part_floats(int N, int K);  // partial-sum floats needed at M = GEMV_MAX_M
 hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const float *bias, float *Y, int ldy,
-                       int epi, const GemvScratch &s, hipStream_t st);
+                       int epi, const PartialBuf &pb, hipStream_t st);
 
 // Dequantizes nblocks of a device matrix in k-block-major layout back to the
 // reference's row-major [N][K] FP32 (test path).

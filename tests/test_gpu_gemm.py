@@ -26,14 +26,17 @@ def _weights(dtype, N, K, rng):
     return q, wd
 
 
-@pytest.mark.parametrize("path", ["f16x2", "bf16x3", "fp32"])
+@pytest.mark.parametrize("path", ["f16x2", "f16x2-unsplit", "bf16x3", "fp32"])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
 @pytest.mark.parametrize("N,K", SHAPES)
 def test_gemm_matches_oracle(dtype, N, K, path, monkeypatch):
     """Every quantized GEMM kernel: the default 16-bit MFMA kernel with f16
-    two-limb activations, its bf16 three-limb form (CIH_LIMBS=bf16x3) and the
-    FP32-MFMA kernel (CIH_QGEMM=fp32)."""
+    two-limb activations (split-K where the tiles alone would not fill the
+    GPU; CIH_SPLITK=0 never splits), its bf16 three-limb form
+    (CIH_LIMBS=bf16x3) and the FP32-MFMA kernel (CIH_QGEMM=fp32)."""
     monkeypatch.setenv("CIH_GEMV", "0")  # small M also through the MFMA kernels
+    if path == "f16x2-unsplit":
+        monkeypatch.setenv("CIH_SPLITK", "0")
     if path == "fp32":
         monkeypatch.setenv("CIH_QGEMM", "fp32")
     elif dtype == 0:
