@@ -31,9 +31,10 @@ PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 PEAK_HBM_GBS = 8000.0
 TIMING = "HIP event pair around every launch on the library stream, over an instrumented second pass of the same steps"
 GEMV_MAX_TOKENS = 8             # batches of at most this many tokens use the weight-streaming GEMV
-# The default quantized GEMM issues 3 bf16 MFMA MACs per algorithmic MAC
-# (activation split into three bf16 limbs); CIH_QGEMM=fp32 selects the
-# FP32-MFMA kernel (1 MAC per MAC).
+PEAK_F16_MFMA_TFLOPS = 2500.0   # MI355X dense f16 matrix peak
+# The default quantized GEMM issues 2 f16 MFMA MACs per algorithmic MAC
+# (activation split into two f16 limbs); CIH_LIMBS=bf16x3 issues 3 bf16 MACs,
+# CIH_QGEMM=fp32 selects the FP32-MFMA kernel (1 MAC per MAC).
 
 
 class Hip:
@@ -185,8 +186,10 @@ def main():
         achieved = q["flops"] / (q["total_ms"] * 1e-3) / 1e12 if q["total_ms"] > 0 else 0.0
         if fp32_path:
             kname, peak, limbs = "k_gemm<Q8_0> FP32 MFMA (QKV, Wo, FC1, FC2)", PEAK_FP32_MFMA_TFLOPS, 1
-        else:
+        elif os.environ.get("CIH_LIMBS") == "bf16x3":
             kname, peak, limbs = "k_gemm_x3<Q8_0> bf16 MFMA, 3 limbs (QKV, Wo, FC1, FC2)", PEAK_BF16_MFMA_TFLOPS, 3
+        else:
+            kname, peak, limbs = "k_gemm_x3<Q8_0> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)", PEAK_F16_MFMA_TFLOPS, 2
     kernels = {k: {"launches": v["launches"] // max(1, args.steps),
                    "ms_per_step": v["total_ms"] / max(1, args.steps),
                    "tflops": (v["flops"] / (v["total_ms"] * 1e-3) / 1e12) if v["total_ms"] > 0 and v["flops"] else None}

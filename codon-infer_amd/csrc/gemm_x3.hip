@@ -122,7 +122,7 @@ __device__ __forceinline__ void tile_of3(int bid, int total, int nM, int nN, int
     nt = r / gsize;
 }
 
-template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
+template <int WF, int EPI, int BM, int BN, int AF, int LIMB, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv, int ldx,
                                                     const void *__restrict__ Wq, const float *__restrict__ Wsc,
                                                     const float *__restrict__ bias, void *__restrict__ Yv, int ldy,
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     };
 
     // k-blocks [kb0, kend) of this split (all of K without split-K)
-    const int kb0 = blockIdx.y * kps, kend = min(KB, kb0 + kps);
+    const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kend = SPLIT ? min(KB, kb0 + kps) : KB;
     gload(kb0, ra[0], rb[0], rs[0]);
     if (kb0 + 1 < kend) gload(kb0 + 1, ra[1], rb[1], rs[1]);
     for (int kb = kb0; kb < kend; kb += 2) {
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         compute(1);
     }
 
-    if (part) {  // split-K: raw partial sums, bias and epilogue in k_splitk_reduce
+    if (SPLIT && part) {  // split-K: raw partial sums, bias and epilogue in k_splitk_reduce
 #pragma unroll
         for (int c = 0; c < NT; c++) {
             const int col = n0 + wn * (BN / 2) + c * 32 + li;
@@ -434,11 +434,13 @@ static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const 
                               const PartialBuf *pb, hipStream_t st) {
     const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN, KB = W.K / 32;
     // Split K when the tiles alone leave the GPU mostly idle: up to ~1024
-    // workgroups, at least 4 k-blocks per split, partials within pb.
+    // workgroups, at least 4 k-blocks per split, partials within pb.  Only
+    // the 64x64 tile (the one chosen for small problems) is built with it.
+    constexpr bool SPLIT = BM == 64 && BN == 64;
     int S = 1, kps = KB;
     const char *e = getenv("CIH_SPLITK");
     const long wgs = (long)nM * nN;
-    if (pb && pb->part && !(e && !strcmp(e, "0")) && wgs < 512 && KB >= 8) {
+    if (SPLIT && pb && pb->part && !(e && !strcmp(e, "0")) && wgs < 512 && KB >= 8) {
         S = (int)std::min<long>(1024 / wgs, KB / 4);
         while (S > 1 && (size_t)S * M * W.N > pb->floats) S--;
         if (S > 1) {
@@ -447,7 +449,7 @@ static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const 
         }
     }
     float *part = S > 1 ? pb->part : nullptr;
-    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF, LIMB>), dim3(nM * nN, S), dim3(256), 0, st, X, ldx, W.q, W.sc,
+    hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF, LIMB, SPLIT>), dim3(nM * nN, S), dim3(256), 0, st, X, ldx, W.q, W.sc,
                        bias, Y, ldy, M, W.N, W.K, kps, part);
     if (S > 1)
         hipLaunchKernelGGL(k_splitk_reduce, dim3((M * W.N + 255) / 256), dim3(256), 0, st, part, S, M, W.N, bias, Y,
