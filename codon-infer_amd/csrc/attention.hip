@@ -25,11 +25,27 @@
 // an online softmax (P.V accumulated unnormalised, divided by the sum once).
 // RoPE is applied while staging K into LDS and Q into registers, from the
 // host-built cos/sin tables (the reference's f32 powf/cos/sin values).
+//
+// Two kernels share this structure:
+//   k_attention   : FP32 MFMA (v_mfma_f32_32x32x2_f32), CIH_ATT=fp32;
+//   k_attention_h : f16 MFMA (v_mfma_f32_32x32x16_f16) on two-limb operands
+//                   (x = hi + lo, hi = f16(x), lo = f16(x - hi)); each product
+//                   is taken as hi*hi + hi*lo + lo*hi (the dropped lo*lo term
+//                   and the split are ~2^-22 relative), accumulated in FP32.
+//                   The 16-wide k-chunks of the MFMA need the probabilities'
+//                   key order permuted: register 8c + e of a lane in half h
+//                   holds key 16c + 8(e/4) + 4h + e%4, and V is read from LDS
+//                   in that order.  The default.
+#include <stdlib.h>
+#include <string.h>
+
 #include "kernels.h"
 
 namespace cih {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 template <int HD, bool ONEPASS>
 __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
@@ -255,19 +271,274 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
     }
 }
 
+__device__ __forceinline__ f16x8 cat4(f16x4 a, f16x4 b) {
+    return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// hi/lo f16 limbs of 8 floats
+__device__ __forceinline__ void split8(const float *v, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        hi[e] = (_Float16)v[e];
+        lo[e] = (_Float16)(v[e] - (float)hi[e]);
+    }
+}
+
+template <int HD, bool ONEPASS>
+__global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
+                                                     const int *__restrict__ lens, int S_max,
+                                                     const float *__restrict__ rc, const float *__restrict__ rsn,
+                                                     void *__restrict__ out, int out_fmt, float *__restrict__ P,
+                                                     long long pb, long long ph, float inv_scale) {
+    constexpr int HALF = HD / 2;
+    constexpr int HDP = (HD + 15) / 16 * 16;  // dims padded to whole 16-wide k-chunks
+    constexpr int NC = HDP / 16;
+    constexpr int VW = HD < 32 ? 32 : HD;     // output tile rows (dims), zero padded for small heads
+    constexpr int DT = VW / 32;
+    constexpr int K_LD = HDP + 8;             // f16 per LDS key row (16-byte aligned, padded)
+    constexpr int V_LD = 32 + 8;              // f16 per LDS dim row of the transposed V tile
+    __shared__ __attribute__((aligned(16))) _Float16 Kh[32 * K_LD], Kl[32 * K_LD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vh[VW * V_LD], Vl[VW * V_LD];
+
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int len = lens[b], base = cu[b];
+    const int qblk = blockIdx.x * 128;
+    if (qblk >= len) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, hh = lane >> 5;
+    const size_t ld = (size_t)3 * d;
+    const float *Qg = qkv + h * HD;
+    const float *Kg = qkv + d + h * HD;
+    const float *Vg = qkv + 2 * d + h * HD;
+
+    // padding dims (HD..HDP of K, HD..VW of V) stay zero for every tile
+    if constexpr (HDP > HD)
+        for (int idx = tid; idx < 32 * (HDP - HD); idx += 256) {
+            const int key = idx / (HDP - HD), c = HD + idx % (HDP - HD);
+            Kh[key * K_LD + c] = (_Float16)0.0f;
+            Kl[key * K_LD + c] = (_Float16)0.0f;
+        }
+    if constexpr (VW > HD)
+        for (int idx = tid; idx < (VW - HD) * 32; idx += 256) {
+            const int c = HD + idx / 32, key = idx % 32;
+            Vh[c * V_LD + key] = (_Float16)0.0f;
+            Vl[c * V_LD + key] = (_Float16)0.0f;
+        }
+
+    // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs
+    const int qi = qblk + wave * 32 + li;
+    const int qc = min(qi, len - 1);
+    f16x8 qh[NC], ql[NC];
+    {
+        const float *qrow = Qg + (size_t)(base + qc) * ld;
+        const float *cs = rc + (size_t)qc * HALF, *sn = rsn + (size_t)qc * HALF;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int dim = 16 * c + 8 * hh + e;
+                float r = 0.0f;
+                if (dim < HALF) r = qrow[dim] * cs[dim] - qrow[dim + HALF] * sn[dim];
+                else if (dim < HD) r = qrow[dim] * cs[dim - HALF] + qrow[dim - HALF] * sn[dim - HALF];
+                v[e] = r;
+            }
+            split8(v, qh[c], ql[c]);
+        }
+    }
+
+    auto load_k = [&](int kt0) {
+        for (int idx = tid; idx < 32 * HALF; idx += 256) {
+            const int key = idx / HALF, c = idx % HALF;
+            const int kk = min(kt0 + key, len - 1);
+            const float *krow = Kg + (size_t)(base + kk) * ld;
+            const float k0 = krow[c], k1 = krow[c + HALF];
+            const float cs = rc[(size_t)kk * HALF + c], sn = rsn[(size_t)kk * HALF + c];
+            const float r0 = k0 * cs - k1 * sn, r1 = k1 * cs + k0 * sn;
+            const _Float16 h0 = (_Float16)r0, h1 = (_Float16)r1;
+            Kh[key * K_LD + c] = h0;
+            Kl[key * K_LD + c] = (_Float16)(r0 - (float)h0);
+            Kh[key * K_LD + c + HALF] = h1;
+            Kl[key * K_LD + c + HALF] = (_Float16)(r1 - (float)h1);
+        }
+    };
+    auto load_v = [&](int kt0) {
+        for (int idx = tid; idx < 32 * HD; idx += 256) {
+            const int key = idx / HD, c = idx % HD;
+            const int kk = min(kt0 + key, len - 1);
+            const float v = Vg[(size_t)(base + kk) * ld + c];
+            const _Float16 hv = (_Float16)v;
+            Vh[c * V_LD + key] = hv;
+            Vl[c * V_LD + key] = (_Float16)(v - (float)hv);
+        }
+    };
+    // S^T tile (32 keys x 32 queries): A = K rows (keys), B = Q columns (queries)
+    auto scores = [&](f32x16 &acc) {
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[q] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const f16x8 kh = *reinterpret_cast<const f16x8 *>(&Kh[li * K_LD + 16 * c + 8 * hh]);
+            const f16x8 kl = *reinterpret_cast<const f16x8 *>(&Kl[li * K_LD + 16 * c + 8 * hh]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[c], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[c], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[c], acc, 0, 0, 0);
+        }
+    };
+    // O^T += V^T P^T over the tile's 32 keys: B = this lane's 16 probabilities
+    // (register 8c + e = key 16c + 8(e/4) + 4hh + e%4), A = V^T read in that key order
+    auto pv = [&](f32x16 (&oacc)[DT], const float (&p)[16]) {
+        f16x8 phi[2], plo[2];
+        split8(p, phi[0], plo[0]);
+        split8(p + 8, phi[1], plo[1]);
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            const int row = (t * 32 + li) * V_LD;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const f16x8 vh = cat4(*reinterpret_cast<const f16x4 *>(&Vh[row + 16 * c + 4 * hh]),
+                                      *reinterpret_cast<const f16x4 *>(&Vh[row + 16 * c + 8 + 4 * hh]));
+                const f16x8 vl = cat4(*reinterpret_cast<const f16x4 *>(&Vl[row + 16 * c + 4 * hh]),
+                                      *reinterpret_cast<const f16x4 *>(&Vl[row + 16 * c + 8 + 4 * hh]));
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, phi[c], oacc[t], 0, 0, 0);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, plo[c], oacc[t], 0, 0, 0);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, phi[c], oacc[t], 0, 0, 0);
+            }
+        }
+    };
+
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
+    float out_scale;
+    if constexpr (ONEPASS) {
+        // one pass, online softmax (see k_attention)
+        float m = -INFINITY, l = 0.0f;
+        for (int kt0 = 0; kt0 < len; kt0 += 32) {
+            __syncthreads();
+            load_k(kt0);
+            load_v(kt0);
+            __syncthreads();
+            f32x16 acc;
+            scores(acc);
+            float sv[16];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                sv[q] = key < len ? acc[q] * inv_scale : -INFINITY;
+                tmax = fmaxf(tmax, sv[q]);
+            }
+            // key kt0 (< len) sits in half 0, so the combined tile max is finite
+            const float mn = fmaxf(m, fmaxf(tmax, __shfl_xor(tmax, 32)));
+            const float corr = expf(m - mn);
+            float p[16], sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                p[q] = expf(sv[q] - mn);
+                sum += p[q];
+            }
+            l = l * corr + sum;
+            m = mn;
+#pragma unroll
+            for (int t = 0; t < DT; t++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
+            pv(oacc, p);
+        }
+        out_scale = 1.0f / (l + __shfl_xor(l, 32));
+    } else {
+        // pass 1: running max / sum of exp per lane
+        float m = -INFINITY, l = 0.0f;
+        for (int kt0 = 0; kt0 < len; kt0 += 32) {
+            __syncthreads();
+            load_k(kt0);
+            __syncthreads();
+            f32x16 acc;
+            scores(acc);
+            float sv[16];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                sv[q] = key < len ? acc[q] * inv_scale : -INFINITY;
+                tmax = fmaxf(tmax, sv[q]);
+            }
+            const float mn = fmaxf(m, tmax);
+            if (mn != -INFINITY) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) sum += expf(sv[q] - mn);
+                l = l * expf(m - mn) + sum;
+                m = mn;
+            }
+        }
+        const float mo = __shfl_xor(m, 32), lo = __shfl_xor(l, 32);
+        const float mx = fmaxf(m, mo);
+        const float inv_sum = 1.0f / (l * expf(m - mx) + lo * expf(mo - mx));
+        // pass 2: normalized probabilities, optional export, P.V
+        float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+        for (int kt0 = 0; kt0 < len; kt0 += 32) {
+            __syncthreads();
+            load_k(kt0);
+            load_v(kt0);
+            __syncthreads();
+            f32x16 acc;
+            scores(acc);
+            float p[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                p[q] = key < len ? expf(acc[q] * inv_scale - mx) * inv_sum : 0.0f;
+            }
+            if (Prow) {
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    if (key < len) Prow[key] = p[q];
+                }
+            }
+            pv(oacc, p);
+        }
+        out_scale = 1.0f;
+    }
+    if (qi < len) {
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int dd = t * 32 + 8 * g + 4 * hh;
+                if (dd >= HD) continue;
+                const float4 v = make_float4(oacc[t][4 * g] * out_scale, oacc[t][4 * g + 1] * out_scale,
+                                             oacc[t][4 * g + 2] * out_scale, oacc[t][4 * g + 3] * out_scale);
+                if (out_fmt == AF_X3)
+                    x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                else if (out_fmt == AF_H2)
+                    h2_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                else
+                    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d + h * HD +
+                                                dd) = v;
+            }
+    }
+}
+
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos, const float *rope_sin,
                             void *out, int out_fmt, float *P, int64_t pb, int64_t ph, hipStream_t st) {
     if ((out_fmt == AF_X3 || out_fmt == AF_H2) && d % 32) return hipErrorInvalidValue;
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
     dim3 grid((sm.S_max + 127) / 128, H, sm.B);
-#define CIH_ATT(HDV)                                                                                          \
-    if (P)                                                                                                     \
-        hipLaunchKernelGGL((k_attention<HDV, false>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, \
-                           rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);       \
-    else                                                                                                       \
-        hipLaunchKernelGGL((k_attention<HDV, true>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max,  \
-                           rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale);
+    const char *e = getenv("CIH_ATT");
+    const bool fp32 = e && !strcmp(e, "fp32");
+#define CIH_ATT_K(KER, HDV, ONE)                                                                                \
+    hipLaunchKernelGGL((KER<HDV, ONE>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,     \
+                       rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale)
+#define CIH_ATT(HDV)                                                                                           \
+    if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                          \
+    else if (fp32) CIH_ATT_K(k_attention, HDV, true);                                                           \
+    else if (P) CIH_ATT_K(k_attention_h, HDV, false);                                                           \
+    else CIH_ATT_K(k_attention_h, HDV, true);
     switch (hd) {
     case 16: CIH_ATT(16) break;
     case 24: CIH_ATT(24) break;
@@ -276,6 +547,7 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     default: return hipErrorInvalidValue;
     }
 #undef CIH_ATT
+#undef CIH_ATT_K
     return hipGetLastError();
 }
 

@@ -94,6 +94,20 @@ def test_forward_small_configs(hd, H, dtype, act, monkeypatch):
     check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(-0.5)))
 
 
+@pytest.mark.parametrize("hd,H", [(16, 4), (24, 4), (32, 2), (64, 2)])
+def test_forward_fp32_attention_kernel(hd, H, monkeypatch):
+    """The FP32-MFMA attention kernel (CIH_ATT=fp32), kept for A/B runs, on
+    the same ragged batch and outputs as the default f16-limb kernel."""
+    monkeypatch.setenv("CIH_ATT", "fp32")
+    rng = np.random.default_rng(hd * 10 + 7)
+    d = hd * H
+    cfg = ch.EsmConfig(d, 4 * d, 2, H)
+    w = ch.EsmWeights.random(cfg, seed=hd + 7, bias_std=0.02).quantize_q8()
+    cw = rng.standard_normal(cfg.n_layers * H).astype(np.float32)
+    seqs = [rand_tokens(rng, n) for n in (3, 35, 70, 128, 1)]
+    check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(-0.5)))
+
+
 def test_forward_8m_peptide(w8m_path):
     """Shipped 8M weights: every format reproduces the published prediction
     (docs/benchmarks_v1.6.0.md:61-62) and matches the oracle within tolerance."""
