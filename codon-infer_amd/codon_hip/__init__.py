@@ -5,11 +5,12 @@ attention-map API.  All compute runs in libcodon_hip.so (HIP kernels);
 importing fails if the library has not been built.
 """
 from . import _lib
-from ._lib import (CihError, DTYPE_FP32, DTYPE_Q4_0, DTYPE_Q8_0, IO_DEVICE, KC_ATTENTION, KC_GEMM_FP32,
+from ._lib import (CihError, DMS_MASKED_MARGINAL, DMS_WILDTYPE_MARGINAL, DTYPE_FP32, DTYPE_Q4_0, DTYPE_Q8_0,
+                   IO_DEVICE, KC_ATTENTION, KC_GEMM_FP32,
                    KC_GEMM_QUANT, KC_OTHER, OUT_ATTN, OUT_CONTACTS, OUT_FINAL_ATT, OUT_HIDDEN, OUT_LAYER_HIDDEN,
                    OUT_LOGITS)
-from .model import (BidirectionalRunState, EsmConfig, EsmWeights, EsmWeightsQ4, EsmWeightsQ8, GpuModel, Tokenizer,
-                    dequantize_blocks, dequantize_on_device, forward_bidirectional, forward_bidirectional_gpu,
+from .model import (CANONICAL_AAS, BidirectionalRunState, DmsPositionRow, EsmConfig, EsmWeights, EsmWeightsQ4,
+                    EsmWeightsQ8, GpuModel, Tokenizer, dequantize_blocks, run_pipeline_dms, dequantize_on_device, forward_bidirectional, forward_bidirectional_gpu,
                     forward_bidirectional_q4, forward_bidirectional_q8, log_softmax_canonical, matmul_tiled,
                     quantize_slice_to_q4, quantize_slice_to_q8)
 

@@ -343,6 +343,19 @@ class GpuModel:
         C.check(C.lib().cih_forward(self._h, ctypes.c_void_p(tokens_ptr), lens.ctypes.data, lens.size, S_max,
                                     outputs | C.IO_DEVICE, ctypes.byref(o)))
 
+    def dms(self, residues, window=0, stride=0, mode=C.DMS_MASKED_MARGINAL, chunk=0):
+        """In-silico deep mutational scan of one protein (cih_dms; the
+        reference's run_pipeline_dms_with_mode, pipeline.rs:76-280).
+        residues: token ids of the residues (no BOS/EOS).  Returns
+        (deltas [n][20] in CANONICAL_AAS order, entropy [n])."""
+        res = np.ascontiguousarray(residues, np.int32)
+        n = res.size
+        deltas = np.zeros((n, 20), np.float32)
+        ent = np.zeros(n, np.float32)
+        C.check(C.lib().cih_dms(self._h, res.ctypes.data, n, window, stride, mode, chunk, deltas.ctypes.data,
+                                ent.ctypes.data))
+        return deltas, ent
+
     def profile(self, enable=True):
         C.check(C.lib().cih_profile_enable(self._h, int(enable)))
 
@@ -402,3 +415,37 @@ def forward_bidirectional_q8(tokens, config, model, state, num_threads=1):
 
 def forward_bidirectional_q4(tokens, config, model, state, num_threads=1):
     forward_bidirectional_gpu(tokens, config, model, state)
+
+
+CANONICAL_AAS = "ACDEFGHIKLMNPQRSTVWY"  # benchmark.rs:702-707 column order
+
+
+class DmsPositionRow:
+    """One scanned position (export.rs DmsPositionRow::new): mean of the 19
+    non-zero deltas and the tolerance category."""
+
+    def __init__(self, pos, wt, deltas, entropy):
+        self.pos, self.wt = pos, wt
+        self.deltas = np.asarray(deltas, np.float32)
+        nz = self.deltas[self.deltas != 0.0]
+        self.mean_delta_logp = np.float32(np.float32(nz.sum(dtype=np.float32)) / np.float32(19.0))
+        self.entropy = float(entropy)
+        if self.mean_delta_logp <= -3.8:
+            self.category = "Catalytic / Strictly Intolerant"
+        elif self.mean_delta_logp <= -2.2:
+            self.category = "Conserved Structural Core"
+        else:
+            self.category = "Tolerated Variable"
+
+
+def run_pipeline_dms(sequence, model, window_size=0, stride=0, mode=C.DMS_MASKED_MARGINAL, chunk=0):
+    """run_pipeline_dms_with_mode (pipeline.rs:76-315) on the GPU model:
+    returns the rows and mutations per second."""
+    import time
+    toks = Tokenizer.encode(sequence)[1:-1]
+    t0 = time.perf_counter()
+    deltas, ent = model.dms(toks, window_size, stride, mode, chunk)
+    el = time.perf_counter() - t0
+    rows = [DmsPositionRow(p + 1, sequence[p], deltas[p], ent[p]) for p in range(len(sequence))]
+    return rows, (len(sequence) * 20 / el if el > 0 else 0.0)
+

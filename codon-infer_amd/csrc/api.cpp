@@ -53,6 +53,8 @@ struct Workspace {
     float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
     float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
     PartialBuf part;                                    // partial sums of k-split GEMMs / GEMVs
+    int *dms_meta = nullptr;                            // [max(maxB, maxS)][2] scored row, wild type
+    float *dms_out = nullptr;                           // [max(maxB, maxS)][21] deltas, entropy
     // device staging of outputs for host-pointer calls (padded layouts)
     float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
           *o_layer = nullptr;
@@ -435,7 +437,9 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
         }
         for (const DevMatrix *w : mats) pf = std::max(pf, gemv_part_floats(w->N, w->K));
         ws.part.floats = std::max(pf, SPLITK_PART_FLOATS);
-        good = ok(dalloc(ws.part.part, ws.part.floats, dl));
+        const size_t nd = std::max(B, S);
+        good = ok(dalloc(ws.part.part, ws.part.floats, dl)) && ok(dalloc(ws.dms_meta, nd * 2, dl)) &&
+               ok(dalloc(ws.dms_out, nd * 21, dl));
     }
     const bool need_P = flags & (CIH_OUT_CONTACTS | CIH_OUT_FINAL_ATT | CIH_OUT_ATTN);
     if (good && need_P) good = ok(dalloc(ws.P, B * H * S * S, dl));
@@ -474,8 +478,15 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
     return CIH_OK;
 }
 
-int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B, int32_t S_max, uint32_t flags,
-                const cih_outputs *out) {
+}  // extern "C"
+
+namespace {
+
+// The forward behind cih_forward.  keep_logits: compute the LM head into the
+// workspace's packed logits ws.logits [T][V] (rows cu[b] + pos) even when no
+// logits output is requested (the DMS driver scores them on the device).
+int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B, int32_t S_max, uint32_t flags,
+                 const cih_outputs *out, bool keep_logits) {
     if (!m || !tokens || !lens || !out) return set_error(CIH_ERR_ARG, "null argument");
     Workspace &ws = m->ws;
     if (ws.maxB == 0) return set_error(CIH_ERR_CAPACITY, "cih_model_reserve has not been called");
@@ -605,7 +616,7 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
         HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, AF_F32, T, d, st));
     }
     if (want_hidden) HIPCHK(launch_scatter_rows(ws.ao, d, sm, t_hidden, (int64_t)S_max * d, st));
-    if (want_logits) {
+    if (want_logits || keep_logits) {
         if (m->has_head) {
             HIPCHK(gemm(m, m->dense, ws.ao, d, AF_F32, m->dense_b, ws.hbuf, d, T, EPI_GELU));
             {
@@ -616,7 +627,7 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
         } else {
             HIPCHK(gemm(m, m->emb, ws.ao, d, AF_F32, nullptr, ws.logits, V, T, EPI_NONE));
         }
-        HIPCHK(launch_scatter_rows(ws.logits, V, sm, t_logits, (int64_t)S_max * V, st));
+        if (want_logits) HIPCHK(launch_scatter_rows(ws.logits, V, sm, t_logits, (int64_t)S_max * V, st));
     }
     HIPCHK(hipStreamSynchronize(st));
 
@@ -662,6 +673,111 @@ int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_
             s.flops += m->prof.flops[i];
             s.bytes += m->prof.bytes[i];
         }
+    }
+    return CIH_OK;
+}
+
+// Scores `count` positions whose logits are rows meta[2i] of ws.logits and
+// copies deltas / entropy to dst_d[idx[i]][20], dst_e[idx[i]].
+int dms_score_rows(cih_model *m, const std::vector<int> &meta, const std::vector<int> &idx, float *dst_d,
+                   float *dst_e) {
+    Workspace &ws = m->ws;
+    const int count = (int)idx.size();
+    if (count == 0) return CIH_OK;
+    std::vector<float> h((size_t)count * 21);
+    HIPCHK(hipMemcpyAsync(ws.dms_meta, meta.data(), (size_t)count * 2 * sizeof(int), hipMemcpyHostToDevice, m->stream));
+    HIPCHK(launch_dms_score(ws.logits, m->cfg.vocab_size, ws.dms_meta, count, ws.dms_out, m->stream));
+    HIPCHK(hipMemcpyAsync(h.data(), ws.dms_out, h.size() * sizeof(float), hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    for (int i = 0; i < count; i++) {
+        std::memcpy(dst_d + (size_t)idx[i] * 20, &h[(size_t)i * 21], 20 * sizeof(float));
+        dst_e[idx[i]] = h[(size_t)i * 21 + 20];
+    }
+    return CIH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B, int32_t S_max, uint32_t flags,
+                const cih_outputs *out) {
+    return forward_impl(m, tokens, lens, B, S_max, flags, out, false);
+}
+
+int cih_dms(cih_model *m, const int32_t *residues, int32_t n, int32_t window, int32_t stride, int32_t mode,
+            int32_t chunk, float *deltas, float *entropy) {
+    if (!m || !residues || !deltas || !entropy) return set_error(CIH_ERR_ARG, "null argument");
+    if (n < 1) return set_error(CIH_ERR_ARG, "the sequence is empty");
+    if (mode != CIH_DMS_MASKED_MARGINAL && mode != CIH_DMS_WILDTYPE_MARGINAL) return set_error(CIH_ERR_ARG, "bad mode");
+    Workspace &ws = m->ws;
+    if (ws.maxB == 0) return set_error(CIH_ERR_CAPACITY, "cih_model_reserve has not been called");
+    const int V = m->cfg.vocab_size;
+    for (int i = 0; i < n; i++)
+        if (residues[i] < 0 || residues[i] >= V)
+            return set_error(CIH_ERR_TOKEN, "residue token %d at %d outside [0, %d)", residues[i], i, V);
+    // window of the scan (pipeline.rs:87-91)
+    const int max_len = m->cfg.max_seq_len;
+    const int aw = (n <= window || window == 0) ? std::min(n, max_len) : std::min(window, max_len);
+    if (aw + 2 > ws.maxS)
+        return set_error(CIH_ERR_CAPACITY, "the scan's windows need max_seq_len >= %d (reserved %d)", aw + 2, ws.maxS);
+    const int S = aw + 2;
+    const cih_outputs none{};
+    std::vector<int32_t> toks, lens;
+    std::vector<int> meta, idx;
+    if (mode == CIH_DMS_MASKED_MARGINAL) {
+        // one masked copy per position, window centred on it (pipeline.rs:111-122)
+        const int cb = (chunk <= 0 || chunk > ws.maxB) ? ws.maxB : chunk, half = aw / 2;
+        for (int p0 = 0; p0 < n; p0 += cb) {
+            const int B = std::min(cb, n - p0);
+            toks.assign((size_t)B * S, 0);
+            lens.assign(B, 0);
+            meta.clear();
+            idx.clear();
+            int row0 = 0;
+            for (int b = 0; b < B; b++) {
+                const int p = p0 + b;
+                const int w0 = p < half ? 0 : (p + half > n ? std::max(n - aw, 0) : p - half);
+                const int w1 = std::min(w0 + aw, n);
+                int32_t *t = &toks[(size_t)b * S];
+                t[0] = 0;
+                for (int i = w0; i < w1; i++) t[1 + i - w0] = residues[i];
+                t[1 + w1 - w0] = 2;
+                lens[b] = w1 - w0 + 2;
+                const int tp = p - w0 + 1;
+                meta.push_back(row0 + tp);
+                meta.push_back(t[tp]);
+                idx.push_back(p);
+                t[tp] = 32;  // <mask>
+                row0 += lens[b];
+            }
+            if (int rc = forward_impl(m, toks.data(), lens.data(), B, S, 0, &none, true)) return rc;
+            if (int rc = dms_score_rows(m, meta, idx, deltas, entropy)) return rc;
+        }
+        return CIH_OK;
+    }
+    // wild-type marginal: one unmasked forward per window (pipeline.rs:196-265)
+    const int step = (stride > 0 && stride <= aw) ? stride : std::max(aw / 2, 1);
+    int covered = 0, w0 = 0;
+    while (covered < n) {
+        const int w1 = std::min(w0 + aw, n);
+        toks.assign(S, 0);
+        toks[0] = 0;
+        for (int i = w0; i < w1; i++) toks[1 + i - w0] = residues[i];
+        toks[1 + w1 - w0] = 2;
+        lens.assign(1, w1 - w0 + 2);
+        meta.clear();
+        idx.clear();
+        for (int p = covered; p < w1; p++) {
+            meta.push_back(p - w0 + 1);
+            meta.push_back(residues[p]);
+            idx.push_back(p);
+        }
+        if (int rc = forward_impl(m, toks.data(), lens.data(), 1, S, 0, &none, true)) return rc;
+        if (int rc = dms_score_rows(m, meta, idx, deltas, entropy)) return rc;
+        covered = w1;
+        if (w1 >= n) break;
+        w0 = std::min(w0 + step, std::max(n - aw, 0));
     }
     return CIH_OK;
 }

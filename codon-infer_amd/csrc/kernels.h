@@ -110,6 +110,11 @@ hipError_t launch_apc_layer(const float *P, int64_t pb, int64_t ph, int H, int l
 hipError_t launch_apc_finalize(const float *M, const float *r, float *coef, const float *w_dev, int LH, SeqMeta sm,
                                float bias, float *contacts, int n_stride, hipStream_t st);
 
+// DMS rows (pipeline.rs:152-172): for entry i, logits row meta[2i] of the
+// packed [T][V] logits and wild-type token meta[2i+1] give out[i][0..19] =
+// deltas in CANONICAL_AAS order and out[i][20] = entropy.
+hipError_t launch_dms_score(const float *logits, int V, const int *meta, int count, float *out, hipStream_t st);
+
 // Copies packed rows [T][width] into padded [B][S_max][width] (valid rows only).
 hipError_t launch_scatter_rows(const float *src, int width, SeqMeta sm, float *dst, int64_t dst_b_stride,
                                hipStream_t st);

@@ -282,4 +282,39 @@ hipError_t launch_scatter_rows(const float *src, int width, SeqMeta sm, float *d
     return hipGetLastError();
 }
 
+// One thread per scored position: log_softmax_canonical (lib.rs:4426-4441),
+// Shannon entropy over ids 4..=23 with p = exp(lp) counted when p > 1e-12,
+// deltas lp[aa] - lp[wt] in CANONICAL_AAS order (benchmark.rs:702-707),
+// 0 for the wild-type column (pipeline.rs:152-172).
+__global__ __launch_bounds__(64) void k_dms_score(const float *__restrict__ logits, int V, const int *__restrict__ meta,
+                                                  int count, float *__restrict__ out) {
+    const int i = blockIdx.x * 64 + threadIdx.x;
+    if (i >= count) return;
+    const float *lg = logits + (size_t)meta[2 * i] * V;
+    const int wt = meta[2 * i + 1];
+    float m = -INFINITY;
+    for (int t = 4; t <= 23; t++) m = fmaxf(m, lg[t]);
+    float s = 0.0f;
+    for (int t = 4; t <= 23; t++) s += expf(lg[t] - m);
+    const float lse = m + logf(s);
+    float h = 0.0f;
+    for (int t = 4; t <= 23; t++) {
+        const float lp = lg[t] - lse;
+        const float p = expf(lp);
+        if (p > 1e-12f) h -= p * lp;
+    }
+    constexpr int tok[20] = {5, 23, 13, 9, 18, 6, 21, 12, 15, 4, 20, 17, 14, 16, 10, 8, 11, 7, 22, 19};
+    // lp of a non-canonical wild-type token is -inf in the reference's table
+    const float lw = (wt >= 4 && wt <= 23) ? lg[wt] - lse : -INFINITY;
+    float *o = out + (size_t)i * 21;
+    for (int c = 0; c < 20; c++) o[c] = tok[c] == wt ? 0.0f : (lg[tok[c]] - lse) - lw;
+    o[20] = h;
+}
+
+hipError_t launch_dms_score(const float *logits, int V, const int *meta, int count, float *out, hipStream_t st) {
+    if (count <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_dms_score, dim3((count + 63) / 64), dim3(64), 0, st, logits, V, meta, count, out);
+    return hipGetLastError();
+}
+
 }  // namespace cih

@@ -136,6 +136,25 @@ int cih_model_destroy(cih_model *m);
 int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B,
                 int32_t S_max, uint32_t flags, const cih_outputs *out);
 
+/* ---- in-silico deep mutational scan -------------------------------------- */
+
+enum cih_dms_mode { CIH_DMS_MASKED_MARGINAL = 0, CIH_DMS_WILDTYPE_MARGINAL = 1 };
+
+/* Replaces run_pipeline_dms_with_mode (pipeline.rs:76-280) for one protein.
+ * residues: the n token ids between BOS and EOS (Tokenizer::encode of the
+ * sequence without its first and last entries).  window / stride as the
+ * reference (0 = the whole protein, capped at the model's max_seq_len).
+ * Masked marginal: one forward per position with that position set to
+ * <mask> (32), run as batches of `chunk` masked copies (0 or > reserved
+ * max_batch = max_batch); wild-type marginal: one unmasked forward per
+ * window.  Scoring (canonical log-softmax, entropy, deltas) runs on the GPU;
+ * outputs are host arrays: deltas [n][20] in CANONICAL_AAS order
+ * (A C D E F G H I K L M N P Q R S T V W Y, benchmark.rs:702-707; exactly 0
+ * in the wild-type column) and entropy [n].  Needs a workspace reserved for
+ * max_seq_len >= window + 2; allocates nothing. */
+int cih_dms(cih_model *m, const int32_t *residues, int32_t n, int32_t window, int32_t stride, int32_t mode,
+            int32_t chunk, float *deltas, float *entropy);
+
 /* ---- kernel-level entry points (host pointers; each call stages through
  * freshly allocated device memory — for tests, not for the hot loop) ------ */
 

@@ -233,6 +233,27 @@ void cr_log_softmax_canonical(const float *logits, float *out) {
     for (int i = 4; i <= 23; i++) out[i] = logits[i] - lse;
 }
 
+/* One DMS row from the logits at the scored position, pipeline.rs:152-172
+ * (masked marginal; the wild-type marginal rows, 201-220, are the same
+ * arithmetic): canonical log-softmax, Shannon entropy over ids 4..=23 in
+ * ascending id order with p = exp(lp) counted when p > 1e-12, and
+ * deltas[c] = lp[aa_c] - lp[wt] in CANONICAL_AAS order (benchmark.rs:702-707),
+ * exactly 0 for the wild-type column. */
+static const int32_t CR_CANONICAL_TOK[20] = {5, 23, 13, 9, 18, 6, 21, 12, 15, 4, 20, 17, 14, 16, 10, 8, 11, 7, 22, 19};
+
+void cr_dms_score(const float *logits, int32_t wt_tok, float *deltas20, float *entropy) {
+    float lp[33];
+    cr_log_softmax_canonical(logits, lp);
+    float h = 0.0f;
+    for (int i = 4; i <= 23; i++) {
+        float p = expf(lp[i]);
+        if (p > 1e-12f) h -= p * lp[i];
+    }
+    *entropy = h;
+    for (int c = 0; c < 20; c++)
+        deltas20[c] = CR_CANONICAL_TOK[c] == wt_tok ? 0.0f : lp[CR_CANONICAL_TOK[c]] - lp[wt_tok];
+}
+
 /* accumulate_head_apc, lib.rs:5036-5076 */
 void cr_accumulate_head_apc(const float *A, float *cl, int32_t S, int32_t n, float w) {
     if (n == 0 || w == 0.0f) return;

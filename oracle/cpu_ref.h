@@ -78,6 +78,7 @@ void cr_rope_tables(int32_t max_len, int32_t head_dim, float *cos_t, float *sin_
 void cr_apply_rope(float *q, float *k, const float *cos_t, const float *sin_t,
                    int32_t pos, int32_t dim, int32_t n_heads);
 void cr_log_softmax_canonical(const float *logits, float *out33);
+void cr_dms_score(const float *logits33, int32_t wt_tok, float *deltas20, float *entropy);
 void cr_accumulate_head_apc(const float *head_att, float *contact_logits,
                             int32_t seq_len, int32_t n_res, float w_lh);
 

@@ -81,6 +81,7 @@ def lib():
         L.cr_rope_tables.argtypes = [ctypes.c_int32, ctypes.c_int32, _f32p, _f32p]
         L.cr_apply_rope.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
         L.cr_log_softmax_canonical.argtypes = [_f32p, _f32p]
+        L.cr_dms_score.argtypes = [_f32p, ctypes.c_int32, _f32p, _f32p]
         L.cr_accumulate_head_apc.argtypes = [_f32p, _f32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_float]
         L.cr_matmul_tiled.argtypes = [ctypes.c_int32, _f32p, _f32p, ctypes.c_void_p, _f32p,
                                       ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
@@ -188,6 +189,79 @@ def log_softmax_canonical(logits):
     out = np.empty(33, np.float32)
     lib().cr_log_softmax_canonical(_f(logits), _f(out))
     return out
+
+
+CANONICAL_AAS = "ACDEFGHIKLMNPQRSTVWY"  # benchmark.rs:702-707 column order
+
+
+def dms_score(logits33, wt_tok):
+    """(deltas[20], entropy) of one DMS row from 33 logits (pipeline.rs:152-172)."""
+    logits33 = np.ascontiguousarray(logits33, np.float32)
+    deltas = np.empty(20, np.float32)
+    ent = np.empty(1, np.float32)
+    lib().cr_dms_score(_f(logits33), int(wt_tok), _f(deltas), _f(ent))
+    return deltas, float(ent[0])
+
+
+def dms_windows(n, window, max_seq_len):
+    """Window of every position for the masked-marginal scan (pipeline.rs:87-122):
+    returns actual_window and a list of (w_start, w_end) per position."""
+    aw = min(n, max_seq_len) if (n <= window or window == 0) else min(window, max_seq_len)
+    half = aw // 2
+    out = []
+    for p in range(n):
+        if p < half:
+            ws = 0
+        elif p + half > n:
+            ws = max(n - aw, 0)
+        else:
+            ws = p - half
+        out.append((ws, min(ws + aw, n)))
+    return aw, out
+
+
+def dms_wt_windows(n, window, stride, max_seq_len):
+    """Forwards of the wild-type-marginal scan (pipeline.rs:196-265): a list of
+    (w_start, w_end, first_scored, end_scored)."""
+    aw = min(n, max_seq_len) if (n <= window or window == 0) else min(window, max_seq_len)
+    if n <= aw:
+        return [(0, n, 0, n)]
+    step = stride if 0 < stride <= aw else max(aw // 2, 1)
+    out, covered, ws = [], 0, 0
+    while covered < n:
+        we = min(ws + aw, n)
+        out.append((ws, we, covered, we))
+        covered = we
+        if we >= n:
+            break
+        ws = min(ws + step, max(n - aw, 0))
+    return out
+
+
+def dms(cfg, weights, residue_tokens, window=0, stride=0, mode="masked", num_threads=1, max_seq_len=1024):
+    """run_pipeline_dms_with_mode (pipeline.rs:76-280) on one protein given as
+    residue token ids: returns deltas [n][20] and entropy [n]."""
+    res = np.asarray(residue_tokens, np.int32)
+    n = res.size
+    deltas = np.zeros((n, 20), np.float32)
+    ent = np.zeros(n, np.float32)
+    if mode == "masked":
+        _, wins = dms_windows(n, window, max_seq_len)
+        for p, (ws, we) in enumerate(wins):
+            toks = np.concatenate([[0], res[ws:we], [2]]).astype(np.int32)
+            tp = p - ws + 1
+            wt = int(toks[tp])
+            toks[tp] = 32
+            logits = forward(cfg, weights, toks, num_threads, final_att=False, hidden=False)["logits"]
+            deltas[p], ent[p] = dms_score(logits[tp], wt)
+    else:
+        for ws, we, c0, c1 in dms_wt_windows(n, window, stride, max_seq_len):
+            toks = np.concatenate([[0], res[ws:we], [2]]).astype(np.int32)
+            logits = forward(cfg, weights, toks, num_threads, final_att=False, hidden=False)["logits"]
+            for p in range(c0, c1):
+                tp = p - ws + 1
+                deltas[p], ent[p] = dms_score(logits[tp], int(toks[tp]))
+    return deltas, ent
 
 
 def accumulate_head_apc(head_att, contact_logits, seq_len, n_res, w_lh):
