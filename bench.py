@@ -94,25 +94,36 @@ def physical_cores():
     return os.cpu_count() or 1
 
 
-def cpu_baseline(cfg, w, tokens, budget_s):
+def cpu_baseline(cfg, w, tokens, budget_s, contacts=None):
     """The oracle (the reference's CPU algorithm: row-partitioned 4-token FMA
     GEMMs on a thread pool, serial attention) over whole sequences of the same
-    workload, one after another, until budget_s has elapsed."""
+    workload, one after another, until budget_s has elapsed.  A sequence whose
+    single forward would far exceed the budget (3B at L=2048) is cut to its
+    first 256 tokens + EOS, which the sample string states.  With contacts
+    the oracle computes them as the reference does, from each head's map in
+    turn (no map export)."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import cpu_ref as cr
 
     threads = max(1, min(16, physical_cores(), os.cpu_count() or 1))
+    # ~ 2 * 12 d^2 flops per token at ~0.15 TFLOP/s on 16 host cores
+    est = 24.0 * cfg.dim * cfg.dim * cfg.n_layers * len(tokens[0]) / 1.5e11
+    cut = est > budget_s
     done, res = 0, 0
     t0 = time.perf_counter()
     while True:
-        cr.forward(cfg, w, tokens[done % len(tokens)], threads, final_att=False, hidden=False)
+        t = tokens[done % len(tokens)]
+        if cut:
+            t = np.concatenate([t[:256], [2]]).astype(np.int32)
+        cr.forward(cfg, w, t, threads, contacts=contacts, final_att=False, hidden=False)
         done += 1
-        res += len(tokens[0]) - 2
+        res += len(t) - 2
         el = time.perf_counter() - t0
         if el >= budget_s or done >= len(tokens):
             break
+    what = f"first 256 residues of {done} sequence(s)" if cut else f"{done} sequence(s)"
     return {"value": res / el, "unit": "residues/s", "cores": threads, "kind": "port",
-            "sample": f"{done} sequence(s) of the same workload (650M Q8_0, L={len(tokens[0])}) run serially with "
+            "sample": f"{what} of the same workload (L={len(tokens[0])}) run serially with "
                       f"{threads} threads in {el:.1f} s"}
 
 
@@ -190,6 +201,12 @@ def main():
                     help="tokens per sequence; --batch 1 --seq-len 8 or less measures the weight-streaming GEMV")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--model", choices=["8M", "35M", "150M", "650M", "3B"], default="650M")
+    ap.add_argument("--dtype", choices=["fp32", "q8", "q4"], default="q8")
+    ap.add_argument("--ragged", type=int, nargs=2, metavar=("LO", "HI"),
+                    help="residues per sequence uniform in [LO, HI] (padded to --seq-len)")
+    ap.add_argument("--outputs", choices=["logits", "contacts", "maps", "maps+contacts"], default="logits",
+                    help="contacts: + contact probabilities; maps: + every layer's attention maps")
     ap.add_argument("--workload", choices=["forward", "dms"], default="forward",
                     help="forward: batched forward (the headline); dms: in-silico deep mutational scan of a "
                          "400-residue protein (400 masked copies, L=402, chunks of 32)")
@@ -207,23 +224,43 @@ def main():
     if args.workload == "dms":
         return dms_bench(args, ch)
     B, S = args.batch, args.seq_len
-    cfg = ch.EsmConfig.esm2_650m()
+    cfg = ch.EsmConfig.by_name(args.model)
+    headline = (args.model, args.dtype, args.ragged, args.outputs) == ("650M", "q8", None, "logits")
+    seeds = {"8M": 8, "35M": 35, "150M": 150, "650M": 650, "3B": 3000}
     t0 = time.perf_counter()
-    w = ch.EsmWeights.random(cfg, seed=650, bias_std=0.0).quantize_q8()
+    w = ch.EsmWeights.random(cfg, seed=seeds[args.model], bias_std=0.0)
+    w = w.quantize_q8() if args.dtype == "q8" else (w.quantize_q4() if args.dtype == "q4" else w)
     print(f"[bench] weights ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
     rng = np.random.default_rng(16)
+    if args.ragged:
+        lens = (rng.integers(args.ragged[0], args.ragged[1] + 1, B) + 2).astype(np.int32)
+        assert lens.max() <= S, "--ragged HI + 2 must fit in --seq-len"
+    else:
+        lens = np.full(B, S, np.int32)
     toks = np.zeros((B, S), np.int32)
-    toks[:, 0], toks[:, -1] = 0, 2
-    toks[:, 1:-1] = 4 + rng.integers(0, 20, (B, S - 2))
-    lens = np.full(B, S, np.int32)
+    for b in range(B):
+        toks[b, 0], toks[b, lens[b] - 1] = 0, 2
+        toks[b, 1:lens[b] - 1] = 4 + rng.integers(0, 20, lens[b] - 2)
 
     flags = ch.OUT_LOGITS
-    model = ch.GpuModel(cfg, w, max_batch=B, max_len=S, outputs=flags | ch.IO_DEVICE)
+    if "contacts" in args.outputs:
+        flags |= ch.OUT_CONTACTS
+    if "maps" in args.outputs:
+        flags |= ch.OUT_ATTN
+    contact = cfg.contact_head_weights() if flags & ch.OUT_CONTACTS else None
+    model = ch.GpuModel(cfg, w, contact_head=contact, max_batch=B, max_len=S, outputs=flags | ch.IO_DEVICE)
     hip = Hip()
     d_tok = hip.malloc(toks.nbytes)
     d_log = hip.malloc(B * S * cfg.vocab_size * 4)
     hip.h2d(d_tok, toks)
     outs = {"logits": d_log}
+    extra = []
+    if flags & ch.OUT_CONTACTS:
+        outs["contacts"] = hip.malloc(B * (S - 2) * (S - 2) * 4)
+        extra.append(outs["contacts"])
+    if flags & ch.OUT_ATTN:
+        outs["attn"] = hip.malloc(B * cfg.n_layers * cfg.n_heads * S * S * 4)
+        extra.append(outs["attn"])
     if args.copy_probe_mb:
         nbytes = args.copy_probe_mb << 20
         src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
@@ -260,27 +297,30 @@ def main():
     ks = {name: model.profile_read(kc) for name, kc in
           (("gemm_q8", ch.KC_GEMM_QUANT), ("gemm_fp32", ch.KC_GEMM_FP32), ("attention", ch.KC_ATTENTION),
            ("other", ch.KC_OTHER))}
-    q = ks["gemm_q8"]
-    gemv = B * S <= GEMV_MAX_TOKENS and os.environ.get("CIH_GEMV") != "0"
+    T = int(lens.sum())
+    fp32_model = args.dtype == "fp32"
+    q = ks["gemm_fp32"] if fp32_model else ks["gemm_q8"]
+    gemv = T <= GEMV_MAX_TOKENS and os.environ.get("CIH_GEMV") != "0"
     fp32_path = os.environ.get("CIH_QGEMM") == "fp32"
+    wname = {"q8": "Q8_0", "q4": "Q4_0", "fp32": "FP32"}[args.dtype]
     if gemv:
         # weight-streaming GEMV: algorithmic bytes = Q8_0 weights + activations in/out
         achieved = q["bytes"] / (q["total_ms"] * 1e-3) / 1e9 if q["total_ms"] > 0 else 0.0
-        kname, peak, limbs = "k_gemv<Q8_0> weight streaming (QKV, Wo, FC1, FC2)", PEAK_HBM_GBS, None
+        kname, peak, limbs = f"k_gemv<{wname}> weight streaming (QKV, Wo, FC1, FC2)", PEAK_HBM_GBS, None
     else:
         achieved = q["flops"] / (q["total_ms"] * 1e-3) / 1e12 if q["total_ms"] > 0 else 0.0
-        if fp32_path:
-            kname, peak, limbs = "k_gemm<Q8_0> FP32 MFMA (QKV, Wo, FC1, FC2)", PEAK_FP32_MFMA_TFLOPS, 1
+        if fp32_path or fp32_model:
+            kname, peak, limbs = f"k_gemm<{wname}> FP32 MFMA (QKV, Wo, FC1, FC2, LM head)", PEAK_FP32_MFMA_TFLOPS, 1
         elif os.environ.get("CIH_LIMBS") == "bf16x3":
-            kname, peak, limbs = "k_gemm_x3<Q8_0> bf16 MFMA, 3 limbs (QKV, Wo, FC1, FC2)", PEAK_BF16_MFMA_TFLOPS, 3
+            kname, peak, limbs = f"k_gemm_x3<{wname}> bf16 MFMA, 3 limbs (QKV, Wo, FC1, FC2)", PEAK_BF16_MFMA_TFLOPS, 3
         else:
-            kname, peak, limbs = "k_gemm_x3<Q8_0> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)", PEAK_F16_MFMA_TFLOPS, 2
+            kname, peak, limbs = f"k_gemm_x3<{wname}> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)", PEAK_F16_MFMA_TFLOPS, 2
     # traffic from the committed PMC summary, for the workloads it was measured on
     overrides = any(k.startswith("CIH_") for k in os.environ)
     prof = None
-    if not overrides and (B, S) == (16, 512):
+    if not overrides and headline and (B, S) == (16, 512):
         prof = "gemm_q8_650m_b16_l512.md"
-    elif not overrides and (B, S) == (1, 8):
+    elif not overrides and headline and (B, S) == (1, 8):
         prof = "gemv_q8_650m_b1_l8.md"
     traffic, traffic_src = measured_traffic(prof) if prof else (None, None)
     kernels = {k: {"launches": v["launches"] // max(1, args.steps),
@@ -294,10 +334,16 @@ def main():
     hip.d2h(logits, d_log)
     assert np.isfinite(logits).all()
 
-    residues = B * (S - 2)
+    residues = int((lens - 2).sum())
     value = residues * args.steps / el
+    outs_desc = {"logits": "logits", "contacts": "logits + contacts", "maps": "logits + every layer's attention maps",
+                 "maps+contacts": "logits + every layer's attention maps + contacts"}[args.outputs]
+    lens_desc = (f"{args.ragged[0]}-{args.ragged[1]} residues (uniform), padded to L={S}" if args.ragged
+                 else f"L={S} (BOS+{S - 2}+EOS)")
+    metric = METRIC if headline and (B, S) == (16, 512) else \
+        f"residues/sec ESM-2 {args.model} {wname} B={B} {lens_desc}, {outs_desc}"
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 1),
         "unit": "residues/s",
         "n_gpus": 1,
@@ -310,8 +356,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"ESM-2 650M Q8_0 bidirectional forward, B={B}, L={S} (BOS+{S - 2}+EOS), "
-                               "seeded N(0,0.02) weights quantized in-tree, uniform 20-AA tokens, logits to HBM",
+        "config": {"workload": f"ESM-2 {args.model} {wname} bidirectional forward, B={B}, {lens_desc}, "
+                               f"seeded N(0,0.02) weights{' quantized in-tree' if args.dtype != 'fp32' else ''}, "
+                               f"uniform 20-AA tokens, {outs_desc} to HBM",
                    "batch": B, "seq_len": S, "residues_per_step": residues, "parallelism": "single GPU"},
         "roofline": ({"bound": "hbm", "kernel": kname,
                       "achieved": round(achieved, 1), "peak": peak, "unit": "GB/s",
@@ -327,10 +374,13 @@ def main():
     }
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline (oracle) ...", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(cfg, w, [toks[b] for b in range(B)], args.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline(cfg, w, [toks[b, :lens[b]] for b in range(B)], args.cpu_budget,
+                                            contact if "contacts" in args.outputs else None)
     model.close()
     hip.free(d_tok)
     hip.free(d_log)
+    for p in extra:
+        hip.free(p)
     print(json.dumps(line), flush=True)
 
 

@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void k_apc_final(const float *__restrict__ M, 
             const float c = coef[(size_t)lh * B + b];
             if (c != 0.0f) {
                 const float *rr = r + ((size_t)lh * B + b) * n_max;
-                corr += c * rr[i] * rr[j];
+                corr = fmaf(c, rr[i] * rr[j], corr);  // r_i r_j first: (i, j) and (j, i) round alike
             }
         }
         const float logit = Mb[(size_t)i * n_max + j] + Mb[(size_t)j * n_max + i] - corr;
