@@ -52,6 +52,7 @@ struct Workspace {
     float *rope_c = nullptr, *rope_s = nullptr;
     float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
     float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
+    float *rowsum = nullptr, *colpart = nullptr;        // contacts: map row sums, column partial sums
     PartialBuf part;                                    // partial sums of k-split GEMMs / GEMVs
     int *dms_meta = nullptr;                            // [max(maxB, maxS)][2] scored row, wild type
     float *dms_out = nullptr;                           // [max(maxB, maxS)][21] deltas, entropy
@@ -445,7 +446,8 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
     if (good && need_P) good = ok(dalloc(ws.P, B * H * S * S, dl));
     if (good && (flags & CIH_OUT_CONTACTS))
         good = ok(dalloc(ws.M, B * n * n, dl)) && ok(dalloc(ws.r, L * H * B * n, dl)) &&
-               ok(dalloc(ws.coef, L * H * B, dl));
+               ok(dalloc(ws.coef, L * H * B, dl)) && ok(dalloc(ws.rowsum, B * H * S, dl)) &&
+               ok(dalloc(ws.colpart, B * H * ((n + 31) / 32) * n, dl));
     if (good && !(flags & CIH_IO_DEVICE)) {
         if (flags & CIH_OUT_LOGITS) good = good && ok(dalloc(ws.o_logits, T * V, dl));
         if (flags & CIH_OUT_HIDDEN) good = good && ok(dalloc(ws.o_hidden, T * d, dl));
@@ -586,12 +588,13 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             double fl = 0;
             for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
             ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
-            HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, af, P, pb, ph, st));
+            HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, af, P, pb, ph,
+                                    want_contacts && m->nz[l] > 0 ? ws.rowsum : nullptr, st));
         }
         if (want_contacts && m->nz[l] > 0) {
             ProfScope ps(m, CIH_KC_OTHER, 0, 0);
-            HIPCHK(launch_apc_layer(P, pb, ph, H, l, m->d_contact_w, m->d_heads + (size_t)l * H, m->nz[l], sm, ws.M,
-                                    ws.r, st));
+            HIPCHK(launch_apc_layer(P, pb, ph, H, l, m->d_contact_w, m->d_heads + (size_t)l * H, m->nz[l], sm,
+                                    ws.rowsum, ws.colpart, ws.M, ws.r, st));
         }
         if (want_final && l == L - 1) {
             ProfScope ps(m, CIH_KC_OTHER, 0, 0);

@@ -47,12 +47,49 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
+// Stores a lane's 16 probabilities (keys k0 + 8g + e, g = 0..3, e = 0..3) of
+// one query row: 16-byte stores where a group is whole and aligned.
+__device__ __forceinline__ void store_p(float *Prow, const float (&p)[16], int k0, int len) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int key = k0 + 8 * g;
+        float *dst = Prow + key;
+        if (key + 3 < len && ((uintptr_t)dst & 15) == 0) {
+            *reinterpret_cast<float4 *>(dst) = make_float4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (key + e < len) dst[e] = p[4 * g + e];
+        }
+    }
+}
+
+// Sum of the lane's probabilities whose keys are residues (1 <= key <= len - 2).
+__device__ __forceinline__ float residue_sum(const float (&p)[16], int k0, int len) {
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        const int key = k0 + 8 * (q >> 2) + (q & 3);
+        if (key >= 1 && key <= len - 2) s += p[q];
+    }
+    return s;
+}
+
+// rowsum[b][h][qi] for residue queries: the two lane halves hold disjoint keys.
+__device__ __forceinline__ void write_rowsum(float *rowsum, float rs, int b, int h, int H, int S_max, int qi, int len,
+                                             int hh) {
+    if (!rowsum) return;
+    rs += __shfl_xor(rs, 32);
+    if (hh == 0 && qi >= 1 && qi <= len - 2) rowsum[((size_t)b * H + h) * S_max + qi] = rs;
+}
+
 template <int HD, bool ONEPASS>
 __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
                                                    const int *__restrict__ lens, int S_max,
                                                    const float *__restrict__ rc, const float *__restrict__ rsn,
                                                    void *__restrict__ out, int out_fmt, float *__restrict__ P,
-                                                   long long pb, long long ph, float inv_scale) {
+                                                   long long pb, long long ph, float inv_scale,
+                                                   float *__restrict__ rowsum) {
     constexpr int HALF = HD / 2;
     constexpr int VW = HD < 32 ? 32 : HD;  // V tile width, zero padded for small heads
     constexpr int DT = VW / 32;            // 32-wide output tiles
@@ -223,6 +260,7 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
 #pragma unroll
         for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
     float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+    float rs = 0.0f;  // sum of this query's probabilities over residue keys (contacts)
     for (int kt0 = 0; kt0 < len; kt0 += 32) {
         __syncthreads();
         load_k(kt0);
@@ -236,13 +274,8 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
             const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
             p[q] = key < len ? expf(acc[q] * inv_scale - mx) * inv_sum : 0.0f;
         }
-        if (Prow) {
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                if (key < len) Prow[key] = p[q];
-            }
-        }
+        if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
+        if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
 #pragma unroll
         for (int t = 0; t < DT; t++) {
 #pragma unroll
@@ -252,6 +285,7 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
             }
         }
     }
+    write_rowsum(rowsum, rs, b, h, gridDim.y, S_max, qi, len, hh);
     if (qi < len) {
         // lane holds output dims dd = t*32 + 8*(q/4) + 4*half + q%4: groups of 4
 #pragma unroll
@@ -289,7 +323,8 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
                                                      const int *__restrict__ lens, int S_max,
                                                      const float *__restrict__ rc, const float *__restrict__ rsn,
                                                      void *__restrict__ out, int out_fmt, float *__restrict__ P,
-                                                     long long pb, long long ph, float inv_scale) {
+                                                     long long pb, long long ph, float inv_scale,
+                                                     float *__restrict__ rowsum) {
     constexpr int HALF = HD / 2;
     constexpr int HDP = (HD + 15) / 16 * 16;  // dims padded to whole 16-wide k-chunks
     constexpr int NC = HDP / 16;
@@ -479,6 +514,7 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
         const float inv_sum = 1.0f / (l * expf(m - mx) + lo * expf(mo - mx));
         // pass 2: normalized probabilities, optional export, P.V
         float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+        float rs = 0.0f;  // sum of this query's probabilities over residue keys (contacts)
         for (int kt0 = 0; kt0 < len; kt0 += 32) {
             __syncthreads();
             load_k(kt0);
@@ -492,15 +528,11 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
                 p[q] = key < len ? expf(acc[q] * inv_scale - mx) * inv_sum : 0.0f;
             }
-            if (Prow) {
-#pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                    if (key < len) Prow[key] = p[q];
-                }
-            }
+            if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
+            if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
             pv(oacc, p);
         }
+        write_rowsum(rowsum, rs, b, h, gridDim.y, S_max, qi, len, hh);
         out_scale = 1.0f;
     }
     if (qi < len) {
@@ -524,7 +556,8 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
 }
 
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos, const float *rope_sin,
-                            void *out, int out_fmt, float *P, int64_t pb, int64_t ph, hipStream_t st) {
+                            void *out, int out_fmt, float *P, int64_t pb, int64_t ph, float *rowsum, hipStream_t st) {
+    if (rowsum && !P) return hipErrorInvalidValue;
     if ((out_fmt == AF_X3 || out_fmt == AF_H2) && d % 32) return hipErrorInvalidValue;
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
@@ -533,7 +566,7 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     const bool fp32 = e && !strcmp(e, "fp32");
 #define CIH_ATT_K(KER, HDV, ONE)                                                                                \
     hipLaunchKernelGGL((KER<HDV, ONE>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,     \
-                       rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale)
+                       rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum)
 #define CIH_ATT(HDV)                                                                                           \
     if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                          \
     else if (fp32) CIH_ATT_K(k_attention, HDV, true);                                                           \

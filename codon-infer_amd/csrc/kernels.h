@@ -89,22 +89,25 @@ hipError_t launch_layernorm(const float *x, const float *w, const float *b, void
                             int d, hipStream_t st);
 
 // Bidirectional rotary attention over packed Q|K|V rows.  When P != nullptr
-// every softmax row is stored at P[b*pb + h*ph + q*S_max + k].
-// out: [T][d] FP32 (out_fmt AF_F32) or three-limb bf16 (AF_X3).
+// every softmax row is stored at P[b*pb + h*ph + q*S_max + k]; rowsum (with
+// P) receives rowsum[b][h][q] = sum of row q over the residue keys 1..len-2,
+// for residue queries.
+// out: [T][d] FP32 (out_fmt AF_F32) or a limb format (AF_X3 / AF_H2).
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos,
                             const float *rope_sin, void *out, int out_fmt, float *P, int64_t pb, int64_t ph,
-                            hipStream_t st);
+                            float *rowsum, hipStream_t st);
 
 // final_att[b][p][t] = sum_h P_h[p][t] * (1/H), h ascending
 hipError_t launch_head_mean(const float *P, int64_t pb, int64_t ph, int H, SeqMeta sm, float *final_att,
                             hipStream_t st);
 
-// Contacts (APC).  For layer l, heads with w != 0:
-//   M[b][i][j]   += sum_h w_lh * P_lh[i+1][j+1]
-//   r[l][h][b][i] = sum_j P_lh[i+1][j+1] + P_lh[j+1][i+1]   (residues only)
+// Contacts (APC).  For layer l, heads with w != 0, one read of the maps:
+//   M[b][i][j] += sum_h w_lh * P_lh[i+1][j+1]
+//   r[l][h][b][i] = rowsum[b][h][i+1] + sum_j P_lh[j+1][i+1]   (residues only)
+// rowsum comes from launch_attention; colpart: [B][H][ceil(n_max/32)][n_max] scratch.
 hipError_t launch_apc_layer(const float *P, int64_t pb, int64_t ph, int H, int l, const float *w_dev,
-                            const int *heads_dev, int n_heads_nz, SeqMeta sm, float *M, float *r,
-                            hipStream_t st);
+                            const int *heads_dev, int n_heads_nz, SeqMeta sm, const float *rowsum, float *colpart,
+                            float *M, float *r, hipStream_t st);
 // contacts[b][i][j] = sigmoid(M_ij + M_ji - sum_lh (w_lh / T_lh) r_i r_j + bias)
 // coef: [L*H][B] scratch for w_lh / T_lh.
 hipError_t launch_apc_finalize(const float *M, const float *r, float *coef, const float *w_dev, int LH, SeqMeta sm,

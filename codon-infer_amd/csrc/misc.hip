@@ -156,61 +156,72 @@ hipError_t launch_head_mean(const float *P, int64_t pb, int64_t ph, int H, SeqMe
 //   s_ij = A_ij + A_ji, r_i = sum_j s_ij, T = sum_i r_i,
 //   logit_ij += w * (s_ij - (r_i / T) * r_j)
 // Summed over heads: logit = M + M^T - sum_h (w_h / T_h) r_h r_h^T with
-// M = sum_h w_h A_h.  Row sums of A go with M's accumulation (one workgroup
-// per residue row), column sums are a separate coalesced pass.
-// M: [B][n_max][n_max], r: [L*H][B][n_max], n_max = S_max - 2.
-__global__ __launch_bounds__(256) void k_apc_rows(const float *__restrict__ P, long long pb, long long ph, int H, int l,
-                                                  const float *__restrict__ w, const int *__restrict__ heads, int nz,
-                                                  const int *__restrict__ lens, int S_max, float *__restrict__ M,
-                                                  float *__restrict__ r, int B) {
-    const int i = blockIdx.x, b = blockIdx.y;
-    const int n = lens[b] - 2, n_max = S_max - 2;
-    if (i >= n) return;
-    __shared__ float red[4];
-    float *Mrow = M + ((size_t)b * n_max + i) * n_max;
-    // row sums per head
-    for (int k = 0; k < nz; k++) {
-        const int h = heads[k];
-        const float *A = P + b * pb + h * ph + (size_t)(i + 1) * S_max + 1;
-        float s = 0.0f;
-        for (int j = threadIdx.x; j < n; j += 256) s += A[j];
-        s = wave_sum(s);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-        __syncthreads();
-        if (threadIdx.x == 0) r[((size_t)(l * H + h) * B + b) * n_max + i] = red[0] + red[1] + red[2] + red[3];
-        __syncthreads();
-    }
-    for (int j = threadIdx.x; j < n; j += 256) {
-        float acc = Mrow[j];
-        for (int k = 0; k < nz; k++) {
-            const int h = heads[k];
-            acc += w[l * H + h] * P[b * pb + h * ph + (size_t)(i + 1) * S_max + 1 + j];
+// M = sum_h w_h A_h, and r_i = (row sum of A)_i + (column sum of A)_i.  The
+// attention kernel supplies the row sums; k_apc_tile reads each map once,
+// accumulating M and per-32-row column partial sums, which k_apc_r adds in
+// order.  M: [B][n_max][n_max], r: [L*H][B][n_max], n_max = S_max - 2.
+constexpr int APC_ROWS = 32;  // map rows per workgroup of k_apc_tile
+constexpr int APC_HMAX = 40;  // most heads of any preset (3B)
+
+__global__ __launch_bounds__(256) void k_apc_tile(const float *__restrict__ P, long long pb, long long ph, int H,
+                                                  int l, const float *__restrict__ w, const int *__restrict__ heads,
+                                                  int nz, const int *__restrict__ lens, int S_max,
+                                                  float *__restrict__ M, float *__restrict__ colpart, int B) {
+    const int tile = blockIdx.x, b = blockIdx.z;
+    const int n = lens[b] - 2, n_max = S_max - 2, ntiles = (n_max + APC_ROWS - 1) / APC_ROWS;
+    const int j = blockIdx.y * 256 + threadIdx.x;  // residue column
+    const int i0 = tile * APC_ROWS;
+    if (j >= n || i0 >= n) return;
+    const int i1 = min(i0 + APC_ROWS, n);
+    float cs[APC_HMAX];
+#pragma unroll
+    for (int k = 0; k < APC_HMAX; k++) cs[k] = 0.0f;
+    for (int i = i0; i < i1; i++) {
+        float *Mij = M + ((size_t)b * n_max + i) * n_max + j;
+        float acc = *Mij;
+        const float *row = P + b * pb + (size_t)(i + 1) * S_max + 1 + j;
+#pragma unroll
+        for (int k = 0; k < APC_HMAX; k++) {
+            if (k < nz) {
+                const int h = heads[k];
+                const float a = row[h * ph];
+                acc += w[l * H + h] * a;
+                cs[k] += a;
+            }
         }
-        Mrow[j] = acc;
+        *Mij = acc;
     }
+#pragma unroll
+    for (int k = 0; k < APC_HMAX; k++)
+        if (k < nz) colpart[(((size_t)b * H + heads[k]) * ntiles + tile) * n_max + j] = cs[k];
 }
 
-__global__ __launch_bounds__(256) void k_apc_cols(const float *__restrict__ P, long long pb, long long ph, int H, int l,
-                                                  const int *__restrict__ heads, const int *__restrict__ lens,
-                                                  int S_max, float *__restrict__ r, int B) {
-    const int b = blockIdx.y, h = heads[blockIdx.z];
-    const int n = lens[b] - 2, n_max = S_max - 2;
-    const int i = blockIdx.x * 256 + threadIdx.x;  // column (residue) index
+// r[l*H + h][b][i] = rowsum[b][h][i+1] + column partials of i in tile order
+__global__ __launch_bounds__(256) void k_apc_r(const float *__restrict__ rowsum, const float *__restrict__ colpart,
+                                               int H, int l, const int *__restrict__ heads,
+                                               const int *__restrict__ lens, int S_max, float *__restrict__ r,
+                                               int B) {
+    const int b = blockIdx.z, h = heads[blockIdx.y];
+    const int n = lens[b] - 2, n_max = S_max - 2, ntiles = (n_max + APC_ROWS - 1) / APC_ROWS;
+    const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float *A = P + b * pb + h * ph + S_max + 1 + i;
-    float s = 0.0f;
-    for (int j = 0; j < n; j++) s += A[(size_t)j * S_max];
-    r[((size_t)(l * H + h) * B + b) * n_max + i] += s;
+    float c = 0.0f;
+    const int nt = (n + APC_ROWS - 1) / APC_ROWS;
+    for (int t = 0; t < nt; t++) c += colpart[(((size_t)b * H + h) * ntiles + t) * n_max + i];
+    r[((size_t)(l * H + h) * B + b) * n_max + i] = rowsum[((size_t)b * H + h) * S_max + i + 1] + c;
 }
 
 hipError_t launch_apc_layer(const float *P, int64_t pb, int64_t ph, int H, int l, const float *w_dev,
-                            const int *heads_dev, int n_heads_nz, SeqMeta sm, float *M, float *r, hipStream_t st) {
+                            const int *heads_dev, int n_heads_nz, SeqMeta sm, const float *rowsum, float *colpart,
+                            float *M, float *r, hipStream_t st) {
     if (n_heads_nz <= 0 || sm.S_max < 3) return hipSuccess;
+    if (n_heads_nz > APC_HMAX || H > APC_HMAX) return hipErrorInvalidValue;
     const int n_max = sm.S_max - 2;
-    hipLaunchKernelGGL(k_apc_rows, dim3(n_max, sm.B), dim3(256), 0, st, P, (long long)pb, (long long)ph, H, l, w_dev,
-                       heads_dev, n_heads_nz, sm.lens, sm.S_max, M, r, sm.B);
-    hipLaunchKernelGGL(k_apc_cols, dim3((n_max + 255) / 256, sm.B, n_heads_nz), dim3(256), 0, st, P, (long long)pb,
-                       (long long)ph, H, l, heads_dev, sm.lens, sm.S_max, r, sm.B);
+    hipLaunchKernelGGL(k_apc_tile, dim3((n_max + APC_ROWS - 1) / APC_ROWS, (n_max + 255) / 256, sm.B), dim3(256), 0,
+                       st, P, (long long)pb, (long long)ph, H, l, w_dev, heads_dev, n_heads_nz, sm.lens, sm.S_max, M,
+                       colpart, sm.B);
+    hipLaunchKernelGGL(k_apc_r, dim3((n_max + 255) / 256, n_heads_nz, sm.B), dim3(256), 0, st, rowsum, colpart, H, l,
+                       heads_dev, sm.lens, sm.S_max, r, sm.B);
     return hipGetLastError();
 }
 
