@@ -39,6 +39,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace cih {
@@ -381,29 +383,49 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
         }
     }
 
+    // K tile: a thread rotates 4 consecutive pair-dims (c..c+3 with c+HALF..) of one key
     auto load_k = [&](int kt0) {
-        for (int idx = tid; idx < 32 * HALF; idx += 256) {
-            const int key = idx / HALF, c = idx % HALF;
+        constexpr int G = HALF / 4;
+        for (int idx = tid; idx < 32 * G; idx += 256) {
+            const int key = idx / G, c = 4 * (idx % G);
             const int kk = min(kt0 + key, len - 1);
             const float *krow = Kg + (size_t)(base + kk) * ld;
-            const float k0 = krow[c], k1 = krow[c + HALF];
-            const float cs = rc[(size_t)kk * HALF + c], sn = rsn[(size_t)kk * HALF + c];
-            const float r0 = k0 * cs - k1 * sn, r1 = k1 * cs + k0 * sn;
-            const _Float16 h0 = (_Float16)r0, h1 = (_Float16)r1;
-            Kh[key * K_LD + c] = h0;
-            Kl[key * K_LD + c] = (_Float16)(r0 - (float)h0);
-            Kh[key * K_LD + c + HALF] = h1;
-            Kl[key * K_LD + c + HALF] = (_Float16)(r1 - (float)h1);
+            const float4 k0 = *reinterpret_cast<const float4 *>(krow + c);
+            const float4 k1 = *reinterpret_cast<const float4 *>(krow + c + HALF);
+            const float4 cs = *reinterpret_cast<const float4 *>(rc + (size_t)kk * HALF + c);
+            const float4 sn = *reinterpret_cast<const float4 *>(rsn + (size_t)kk * HALF + c);
+            const float r0[4] = {k0.x * cs.x - k1.x * sn.x, k0.y * cs.y - k1.y * sn.y, k0.z * cs.z - k1.z * sn.z,
+                                 k0.w * cs.w - k1.w * sn.w};
+            const float r1[4] = {k1.x * cs.x + k0.x * sn.x, k1.y * cs.y + k0.y * sn.y, k1.z * cs.z + k0.z * sn.z,
+                                 k1.w * cs.w + k0.w * sn.w};
+            f16x4 h0, l0, h1, l1;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                h0[e] = (_Float16)r0[e];
+                l0[e] = (_Float16)(r0[e] - (float)h0[e]);
+                h1[e] = (_Float16)r1[e];
+                l1[e] = (_Float16)(r1[e] - (float)h1[e]);
+            }
+            *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c]) = h0;
+            *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c]) = l0;
+            *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c + HALF]) = h1;
+            *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c + HALF]) = l1;
         }
     };
+    // V tile, transposed: a thread takes 4 consecutive keys of one dim (coalesced over dims)
     auto load_v = [&](int kt0) {
-        for (int idx = tid; idx < 32 * HD; idx += 256) {
-            const int key = idx / HD, c = idx % HD;
-            const int kk = min(kt0 + key, len - 1);
-            const float v = Vg[(size_t)(base + kk) * ld + c];
-            const _Float16 hv = (_Float16)v;
-            Vh[c * V_LD + key] = hv;
-            Vl[c * V_LD + key] = (_Float16)(v - (float)hv);
+        for (int idx = tid; idx < 8 * HD; idx += 256) {
+            const int c = idx % HD, kg = 4 * (idx / HD);
+            f16x4 hv, lv;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int kk = min(kt0 + kg + e, len - 1);
+                const float v = Vg[(size_t)(base + kk) * ld + c];
+                hv[e] = (_Float16)v;
+                lv[e] = (_Float16)(v - (float)hv[e]);
+            }
+            *reinterpret_cast<f16x4 *>(&Vh[c * V_LD + kg]) = hv;
+            *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + kg]) = lv;
         }
     };
     // S^T tile (32 keys x 32 queries): A = K rows (keys), B = Q columns (queries)
@@ -448,9 +470,13 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
         for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
     float out_scale;
     if constexpr (ONEPASS) {
-        // one pass, online softmax (see k_attention)
+        // One pass, online softmax (see k_attention) in base 2: scores are
+        // pre-scaled by log2(e) / sqrt(hd) so every exponential is one
+        // v_exp_f32.  Whole tiles skip the key mask; the output accumulators
+        // are rescaled only when some lane's running max moved.
+        const float sl2 = inv_scale * 1.44269504088896340736f;
         float m = -INFINITY, l = 0.0f;
-        for (int kt0 = 0; kt0 < len; kt0 += 32) {
+        auto tile = [&](int kt0, auto masked) {
             __syncthreads();
             load_k(kt0);
             load_v(kt0);
@@ -461,27 +487,36 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
             float tmax = -INFINITY;
 #pragma unroll
             for (int q = 0; q < 16; q++) {
-                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                sv[q] = key < len ? acc[q] * inv_scale : -INFINITY;
-                tmax = fmaxf(tmax, sv[q]);
+                float v = acc[q] * sl2;
+                if constexpr (decltype(masked)::value) {
+                    const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    v = key < len ? v : -INFINITY;
+                }
+                sv[q] = v;
+                tmax = fmaxf(tmax, v);
             }
             // key kt0 (< len) sits in half 0, so the combined tile max is finite
             const float mn = fmaxf(m, fmaxf(tmax, __shfl_xor(tmax, 32)));
-            const float corr = expf(m - mn);
+            const float corr = __builtin_amdgcn_exp2f(m - mn);
             float p[16], sum = 0.0f;
 #pragma unroll
             for (int q = 0; q < 16; q++) {
-                p[q] = expf(sv[q] - mn);
+                p[q] = __builtin_amdgcn_exp2f(sv[q] - mn);
                 sum += p[q];
             }
             l = l * corr + sum;
             m = mn;
+            if (__ballot(corr != 1.0f)) {
 #pragma unroll
-            for (int t = 0; t < DT; t++)
+                for (int t = 0; t < DT; t++)
 #pragma unroll
-                for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
+                    for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
+            }
             pv(oacc, p);
-        }
+        };
+        int kt0 = 0;
+        for (; kt0 + 32 <= len; kt0 += 32) tile(kt0, std::false_type{});
+        if (kt0 < len) tile(kt0, std::true_type{});
         out_scale = 1.0f / (l + __shfl_xor(l, 32));
     } else {
         // pass 1: running max / sum of exp per lane
