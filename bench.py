@@ -127,6 +127,44 @@ def cpu_baseline(cfg, w, tokens, budget_s, contacts=None):
                       f"{threads} threads in {el:.1f} s"}
 
 
+def load_bench(args, ch):
+    """Model load: a CODQ file of --model / --dtype (seeded weights) written to
+    the temp directory, then cih_model_create_from_file timed (median of
+    --steps, page cache warm), i.e. file -> device-resident model.  With
+    --dtype fp32 the FP32 file is also loaded with quantize_to = Q8_0."""
+    import statistics
+    import tempfile
+    cfg = ch.EsmConfig.by_name(args.model)
+    seeds = {"8M": 8, "35M": 35, "150M": 150, "650M": 650, "3B": 3000}
+    w = ch.EsmWeights.random(cfg, seed=seeds[args.model], bias_std=0.02)
+    w = w.quantize_q8() if args.dtype == "q8" else (w.quantize_q4() if args.dtype == "q4" else w)
+    path = os.path.join(tempfile.gettempdir(), f"bench_{args.model}_{args.dtype}.codq")
+    ch.save_codq(path, cfg, w)
+    size = os.path.getsize(path)
+    lib = ch._lib.lib()
+
+    def timed(quantize_to):
+        ts = []
+        for i in range(args.warmup + args.steps):
+            h = ctypes.c_void_p()
+            t0 = time.perf_counter()
+            ch._lib.check(lib.cih_model_create_from_file(path.encode(), quantize_to, None, 0.0, ctypes.byref(h)))
+            dt = time.perf_counter() - t0
+            lib.cih_model_destroy(h)
+            if i >= args.warmup:
+                ts.append(dt)
+        return statistics.median(ts)
+
+    t = timed(-1)
+    line = {"metric": f"model load ms, ESM-2 {args.model} {args.dtype} CODQ file -> device", "value": round(t * 1e3, 1),
+            "unit": "ms", "higher_is_better": False, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "file_bytes": size, "GB_per_s": round(size / t / 1e9, 2)}
+    if args.dtype == "fp32":
+        line["quantize_to_q8_ms"] = round(timed(1) * 1e3, 1)
+    os.remove(path)
+    print(json.dumps(line), flush=True)
+
+
 def dms_bench(args, ch):
     """ESM-2 650M Q8_0 in-silico DMS: a seeded 400-residue protein, every
     position masked in turn (400 copies of L=402) in chunks of 32, scored on
@@ -207,7 +245,7 @@ def main():
                     help="residues per sequence uniform in [LO, HI] (padded to --seq-len)")
     ap.add_argument("--outputs", choices=["logits", "contacts", "maps", "maps+contacts"], default="logits",
                     help="contacts: + contact probabilities; maps: + every layer's attention maps")
-    ap.add_argument("--workload", choices=["forward", "dms"], default="forward",
+    ap.add_argument("--workload", choices=["forward", "dms", "load"], default="forward",
                     help="forward: batched forward (the headline); dms: in-silico deep mutational scan of a "
                          "400-residue protein (400 masked copies, L=402, chunks of 32)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -223,6 +261,8 @@ def main():
 
     if args.workload == "dms":
         return dms_bench(args, ch)
+    if args.workload == "load":
+        return load_bench(args, ch)
     B, S = args.batch, args.seq_len
     cfg = ch.EsmConfig.by_name(args.model)
     headline = (args.model, args.dtype, args.ragged, args.outputs) == ("650M", "q8", None, "logits")

@@ -12,7 +12,7 @@ from ._lib import (CihError, DMS_MASKED_MARGINAL, DMS_WILDTYPE_MARGINAL, DTYPE_F
 from .model import (CANONICAL_AAS, BidirectionalRunState, DmsPositionRow, EsmConfig, EsmWeights, EsmWeightsQ4,
                     EsmWeightsQ8, GpuModel, Tokenizer, dequantize_blocks, run_pipeline_dms, dequantize_on_device, forward_bidirectional, forward_bidirectional_gpu,
                     forward_bidirectional_q4, forward_bidirectional_q8, log_softmax_canonical, matmul_tiled,
-                    quantize_slice_to_q4, quantize_slice_to_q8)
+                    quantize_slice_to_q4, quantize_slice_to_q8, save_codq)
 
 _lib.lib()  # load now: no silent fallback
 

@@ -89,6 +89,20 @@ FIELDS = ["token_embedding_table", "ln_1_weight", "ln_1_bias", "wq", "bq", "wk",
 MATRICES = ["wq", "wk", "wv", "wo", "fc1_weight", "fc2_weight"]
 
 
+def save_codq(path, cfg, weights):
+    """EsmWeights{Q8,Q4}::save_to_file_with_header (lib.rs:716-742,
+    1128-1154): the 64-byte CODQ header (magic, version 1, dtype, arch id,
+    n_layers, dim, hidden_dim, vocab_size, 32 zero bytes), then every field in
+    EsmWeights order (FP32 floats or the packed 36/20-byte blocks)."""
+    import struct
+    hdr = b"CODQ" + struct.pack("<7I", 1, weights.dtype, ARCH_IDS[cfg.arch], cfg.n_layers, cfg.dim, cfg.hidden_dim,
+                                cfg.vocab_size) + bytes(32)
+    with open(path, "wb") as f:
+        f.write(hdr)
+        for k in FIELDS:
+            f.write(np.ascontiguousarray(getattr(weights, k)).tobytes())
+
+
 def quantize_slice_to_q8(src):
     """quantize_slice_to_q8 (lib.rs:670-673): packed 36-byte blocks as uint8."""
     src = np.ascontiguousarray(src, np.float32).ravel()
