@@ -10,7 +10,7 @@ from ._lib import (CihError, DMS_MASKED_MARGINAL, DMS_WILDTYPE_MARGINAL, DTYPE_F
                    KC_GEMM_QUANT, KC_OTHER, OUT_ATTN, OUT_CONTACTS, OUT_FINAL_ATT, OUT_HIDDEN, OUT_LAYER_HIDDEN,
                    OUT_LOGITS)
 from .model import (CANONICAL_AAS, BidirectionalRunState, DmsPositionRow, EsmConfig, EsmWeights, EsmWeightsQ4,
-                    EsmWeightsQ8, GpuModel, Tokenizer, dequantize_blocks, run_pipeline_dms, dequantize_on_device, forward_bidirectional, forward_bidirectional_gpu,
+                    EsmWeightsQ8, GpuModel, Tokenizer, dequantize_blocks, run_pipeline_dms, dequantize_on_device, quantize_on_device, forward_bidirectional, forward_bidirectional_gpu,
                     forward_bidirectional_q4, forward_bidirectional_q8, log_softmax_canonical, matmul_tiled,
                     quantize_slice_to_q4, quantize_slice_to_q8, save_codq)
 

@@ -28,7 +28,7 @@ KC_GEMM_QUANT, KC_GEMM_FP32, KC_ATTENTION, KC_OTHER = 0, 1, 2, 3
 
 EXPORTED = [
     "cih_model_create", "cih_model_create_from_file", "cih_model_reserve", "cih_model_config",
-    "cih_model_destroy", "cih_forward", "cih_matmul_tiled", "cih_dequantize_device", "cih_quantize_q8",
+    "cih_model_destroy", "cih_forward", "cih_matmul_tiled", "cih_dequantize_device", "cih_quantize_device", "cih_quantize_q8",
     "cih_quantize_q4", "cih_dequantize_q8", "cih_dequantize_q4", "cih_tokenize", "cih_log_softmax_canonical",
     "cih_profile_enable", "cih_profile_read", "cih_last_error", "cih_abi_version", "cih_dms",
 ]
@@ -93,6 +93,7 @@ def lib():
         "cih_dms": [vp, vp, i32, i32, i32, i32, i32, vp, vp],
         "cih_matmul_tiled": [i32, vp, vp, vp, vp, i32, i32, i32],
         "cih_dequantize_device": [i32, vp, i64, vp],
+        "cih_quantize_device": [i32, vp, i64, vp],
         "cih_quantize_q8": [vp, i64, vp],
         "cih_quantize_q4": [vp, i64, vp],
         "cih_dequantize_q8": [vp, i64, vp],

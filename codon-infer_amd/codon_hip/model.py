@@ -274,6 +274,15 @@ def dequantize_on_device(dtype, blocks):
     return out
 
 
+def quantize_on_device(dtype, src):
+    """quantize_slice_to_q8 / _q4 (lib.rs:670-673, 1085-1088) run by the
+    loader's GPU kernel: packed blocks as uint8."""
+    src = np.ascontiguousarray(src, np.float32).ravel()
+    out = np.empty(src.size // 32 * (36 if dtype == C.DTYPE_Q8_0 else 20), np.uint8)
+    C.check(C.lib().cih_quantize_device(dtype, src.ctypes.data, src.size, out.ctypes.data))
+    return out
+
+
 class GpuModel:
     """Device-resident ESM-2 (one HIP stream).  Replaces the reference's
     weights + BidirectionalRunState pair for the GPU path."""

@@ -29,167 +29,13 @@ int set_error(int code, const char *fmt, ...) {
 }
 }  // namespace cih
 
-#define HIPCHK(expr)                                                                                     \
-    do {                                                                                                 \
-        hipError_t e_ = (expr);                                                                          \
-        if (e_ != hipSuccess) return set_error(CIH_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
-    } while (0)
+#include "model.h"
 
-namespace {
-
-struct Layer {
-    DevMatrix wqkv, wo, w1, w2;
-    float *bqkv = nullptr, *bo = nullptr, *b1 = nullptr, *b2 = nullptr;
-    float *ln1w = nullptr, *ln1b = nullptr, *ln2w = nullptr, *ln2b = nullptr;
-};
-
-struct Workspace {
-    int maxB = 0, maxS = 0;
-    uint32_t flags = 0;
-    int *tokens = nullptr, *cu = nullptr, *lens = nullptr;
-    int *h_meta = nullptr;  // pinned: cu[maxB] | lens[maxB]
-    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *ao = nullptr, *hbuf = nullptr, *logits = nullptr;
-    float *rope_c = nullptr, *rope_s = nullptr;
-    float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
-    float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
-    float *rowsum = nullptr, *colpart = nullptr;        // contacts: map row sums, column partial sums
-    PartialBuf part;                                    // partial sums of k-split GEMMs / GEMVs
-    int *dms_meta = nullptr;                            // [max(maxB, maxS)][2] scored row, wild type
-    float *dms_out = nullptr;                           // [max(maxB, maxS)][21] deltas, entropy
-    // device staging of outputs for host-pointer calls (padded layouts)
-    float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
-          *o_layer = nullptr;
-    std::vector<void *> dev, host;
-};
-
-struct Prof {
-    bool on = false;
-    std::vector<hipEvent_t> ev;  // pairs
-    std::vector<int> cls;
-    std::vector<double> flops, bytes;
-    size_t used = 0;
-    cih_kernel_stats st[CIH_KC_COUNT] = {};
-};
-
-}  // namespace
-
-struct cih_model {
-    cih_config cfg{};
-    int dtype = 0, hd = 0;
-    int device = 0;
-    hipStream_t stream = nullptr;
-    std::vector<void *> allocs;
-    DevMatrix emb;
-    std::vector<Layer> layers;
-    float *lnfw = nullptr, *lnfb = nullptr;
-    bool has_head = false;
-    DevMatrix dense, dec;
-    float *dense_b = nullptr, *lm_lnw = nullptr, *lm_lnb = nullptr, *dec_b = nullptr;
-    std::vector<float> contact_w;
-    float contact_b = 0.0f;
-    bool has_contacts = false;
-    float *d_contact_w = nullptr;
-    int *d_heads = nullptr;  // [L][H] per-layer list of heads with nonzero weight
-    std::vector<int> nz;
-    Workspace ws;
-    Prof prof;
-};
-
-namespace {
-
-template <class T>
-hipError_t dalloc(T *&p, size_t n, std::vector<void *> &list) {
-    p = nullptr;
-    if (n == 0) return hipSuccess;
-    void *v = nullptr;
-    hipError_t e = hipMalloc(&v, n * sizeof(T));
-    if (e != hipSuccess) return e;
-    list.push_back(v);
-    p = (T *)v;
-    return hipSuccess;
-}
-
-template <class T>
-int upload(cih_model *m, T *&dst, const T *src, size_t n) {
-    HIPCHK(dalloc(dst, n, m->allocs));
-    if (n) HIPCHK(hipMemcpy(dst, src, n * sizeof(T), hipMemcpyHostToDevice));
-    return 0;
-}
-
-// One [N][K] source matrix (FP32 values or reference row-major blocks) that
-// becomes rows [n_off, n_off + N) of a device matrix.
-struct Part {
-    const void *src;
-    int N;
-};
-
-// Repacks parts into the k-block-major device layout (see kernels.h) and
-// uploads.  Quantized blocks keep their exact bytes and scales.
-int upload_matrix(cih_model *m, int dtype, int K, const std::vector<Part> &parts, DevMatrix &out) {
-    int Ntot = 0;
-    for (auto &p : parts) Ntot += p.N;
-    const int KB = K / 32;
-    out.N = Ntot;
-    out.K = K;
-    out.fmt = dtype == DT_Q8 ? WF_Q8 : (dtype == DT_Q4 ? WF_Q4 : WF_F32);
-    if (dtype == DT_FP32) {
-        std::vector<float> h((size_t)KB * Ntot * 32);
-        int off = 0;
-        for (auto &p : parts) {
-            const float *src = (const float *)p.src;
-            parallel_for(p.N, [&](int64_t a, int64_t b) {
-                for (int64_t n = a; n < b; n++)
-                    for (int kb = 0; kb < KB; kb++)
-                        std::memcpy(&h[((size_t)kb * Ntot + off + n) * 32], src + (size_t)n * K + kb * 32, 128);
-            });
-            off += p.N;
-        }
-        float *d;
-        if (int rc = upload(m, d, h.data(), h.size())) return rc;
-        out.q = d;
-        out.sc = nullptr;
-        return 0;
-    }
-    const int bb = block_bytes(dtype), qb = bb - 4;
-    std::vector<uint8_t> hq((size_t)KB * Ntot * qb);
-    std::vector<float> hs((size_t)KB * Ntot);
-    int off = 0;
-    for (auto &p : parts) {
-        const uint8_t *src = (const uint8_t *)p.src;
-        parallel_for(p.N, [&](int64_t a, int64_t b) {
-            for (int64_t n = a; n < b; n++)
-                for (int kb = 0; kb < KB; kb++) {
-                    const uint8_t *blk = src + ((size_t)n * KB + kb) * bb;
-                    std::memcpy(&hs[(size_t)kb * Ntot + off + n], blk, 4);
-                    std::memcpy(&hq[((size_t)kb * Ntot + off + n) * qb], blk + 4, qb);
-                }
-        });
-        off += p.N;
-    }
-    uint8_t *dq;
-    float *ds;
-    if (int rc = upload(m, dq, hq.data(), hq.size())) return rc;
-    if (int rc = upload(m, ds, hs.data(), hs.size())) return rc;
-    out.q = dq;
-    out.sc = ds;
-    return 0;
-}
-
-const void *mat_ptr(const void *base, int dtype, int64_t elems) {
-    if (dtype == DT_FP32) return (const float *)base + elems;
-    return (const uint8_t *)base + elems / 32 * block_bytes(dtype);
-}
+namespace cih {
 
 void free_list(std::vector<void *> &l) {
     for (void *p : l) hipFree(p);
     l.clear();
-}
-
-void free_workspace(Workspace &ws) {
-    free_list(ws.dev);
-    for (void *p : ws.host) hipHostFree(p);
-    ws.host.clear();
-    ws = Workspace();
 }
 
 int check_config(const cih_config *c) {
@@ -206,6 +52,17 @@ int check_config(const cih_config *c) {
     if (c->dim > 2560) return set_error(CIH_ERR_SHAPE, "dim %d above the LayerNorm kernel's 2560", c->dim);
     if (c->vocab_size <= 32) return set_error(CIH_ERR_SHAPE, "vocab_size must be > 32 (<mask> is id 32)");
     return 0;
+}
+
+}  // namespace cih
+
+namespace {
+
+void free_workspace(Workspace &ws) {
+    free_list(ws.dev);
+    for (void *p : ws.host) hipHostFree(p);
+    ws.host.clear();
+    ws = Workspace();
 }
 
 struct ProfScope {
@@ -265,123 +122,6 @@ extern "C" {
 
 const char *cih_last_error(void) { return g_err.c_str(); }
 int cih_abi_version(void) { return CIH_ABI_VERSION; }
-
-int cih_model_create(const cih_config *cfg, int32_t dtype, const cih_host_weights *w, const float *contact_w,
-                     float contact_b, cih_model **out) {
-    if (!out || !w) return set_error(CIH_ERR_ARG, "null argument");
-    *out = nullptr;
-    if (int rc = check_config(cfg)) return rc;
-    if (dtype != DT_FP32 && dtype != DT_Q8 && dtype != DT_Q4) return set_error(CIH_ERR_ARG, "bad dtype %d", dtype);
-    const void *need[] = {w->token_embedding_table, w->ln_1_weight, w->ln_1_bias, w->wq, w->bq, w->wk, w->bk, w->wv,
-                          w->bv, w->wo, w->bo, w->ln_2_weight, w->ln_2_bias, w->fc1_weight, w->fc1_bias,
-                          w->fc2_weight, w->fc2_bias, w->ln_f_weight, w->ln_f_bias};
-    for (const void *p : need)
-        if (!p) return set_error(CIH_ERR_ARG, "null weight tensor");
-    int dev_count = 0;
-    if (hipGetDeviceCount(&dev_count) != hipSuccess || dev_count == 0)
-        return set_error(CIH_ERR_HIP, "no HIP device available");
-
-    cih_model *m = new cih_model();
-    m->cfg = *cfg;
-    m->dtype = dtype;
-    m->hd = cfg->dim / cfg->n_heads;
-    const int64_t d = cfg->dim, F = cfg->hidden_dim, L = cfg->n_layers, V = cfg->vocab_size, H = cfg->n_heads;
-    auto fail = [&](int rc) {
-        cih_model_destroy(m);
-        return rc;
-    };
-    if (hipGetDevice(&m->device) != hipSuccess || hipStreamCreate(&m->stream) != hipSuccess)
-        return fail(set_error(CIH_ERR_HIP, "stream creation failed"));
-
-    // token embedding [V][d]: Q8 blocks for Q8 models, FP32 otherwise (lib.rs:675-687 vs 1113-1125)
-    const int emb_dt = dtype == DT_Q8 ? DT_Q8 : DT_FP32;
-    if (int rc = upload_matrix(m, emb_dt, (int)d, {{w->token_embedding_table, (int)V}}, m->emb)) return fail(rc);
-
-    m->layers.resize(L);
-    for (int64_t l = 0; l < L; l++) {
-        Layer &ly = m->layers[l];
-        const int64_t dd = l * d * d;
-        int rc = upload_matrix(m, dtype, (int)d,
-                               {{mat_ptr(w->wq, dtype, dd), (int)d}, {mat_ptr(w->wk, dtype, dd), (int)d},
-                                {mat_ptr(w->wv, dtype, dd), (int)d}},
-                               ly.wqkv);
-        if (!rc) rc = upload_matrix(m, dtype, (int)d, {{mat_ptr(w->wo, dtype, dd), (int)d}}, ly.wo);
-        if (!rc) rc = upload_matrix(m, dtype, (int)d, {{mat_ptr(w->fc1_weight, dtype, l * F * d), (int)F}}, ly.w1);
-        if (!rc) rc = upload_matrix(m, dtype, (int)F, {{mat_ptr(w->fc2_weight, dtype, l * d * F), (int)d}}, ly.w2);
-        if (rc) return fail(rc);
-        std::vector<float> bqkv(3 * d);
-        std::memcpy(bqkv.data(), w->bq + l * d, d * 4);
-        std::memcpy(bqkv.data() + d, w->bk + l * d, d * 4);
-        std::memcpy(bqkv.data() + 2 * d, w->bv + l * d, d * 4);
-        if ((rc = upload(m, ly.bqkv, bqkv.data(), bqkv.size())) || (rc = upload(m, ly.bo, w->bo + l * d, d)) ||
-            (rc = upload(m, ly.b1, w->fc1_bias + l * F, F)) || (rc = upload(m, ly.b2, w->fc2_bias + l * d, d)) ||
-            (rc = upload(m, ly.ln1w, w->ln_1_weight + l * d, d)) || (rc = upload(m, ly.ln1b, w->ln_1_bias + l * d, d)) ||
-            (rc = upload(m, ly.ln2w, w->ln_2_weight + l * d, d)) || (rc = upload(m, ly.ln2b, w->ln_2_bias + l * d, d)))
-            return fail(rc);
-    }
-    if (int rc = upload(m, m->lnfw, w->ln_f_weight, d)) return fail(rc);
-    if (int rc = upload(m, m->lnfb, w->ln_f_bias, d)) return fail(rc);
-
-    // LM head (lib.rs:5379-5439): classifier = [ln_w, ln_b, dense_w, dense_b, dec_w, dec_b]
-    const int64_t req = 3 * d + d * d + V * d + V;
-    m->has_head = w->classifier_weights && w->classifier_len >= req;
-    if (m->has_head) {
-        const float *c = w->classifier_weights;
-        int rc = upload(m, m->lm_lnw, c, d);
-        if (!rc) rc = upload(m, m->lm_lnb, c + d, d);
-        if (!rc) rc = upload_matrix(m, DT_FP32, (int)d, {{c + 2 * d, (int)d}}, m->dense);
-        if (!rc) rc = upload(m, m->dense_b, c + 2 * d + d * d, d);
-        if (!rc) rc = upload_matrix(m, DT_FP32, (int)d, {{c + 3 * d + d * d, (int)V}}, m->dec);
-        if (!rc) rc = upload(m, m->dec_b, c + 3 * d + d * d + V * d, V);
-        if (rc) return fail(rc);
-    }
-
-    // contact regression weights (EsmConfig::contact_head_weights, lib.rs:154-177)
-    m->has_contacts = contact_w != nullptr;
-    m->contact_b = contact_b;
-    m->nz.assign(L, 0);
-    if (m->has_contacts) {
-        m->contact_w.assign(contact_w, contact_w + L * H);
-        std::vector<int> heads(L * H, 0);
-        for (int64_t l = 0; l < L; l++)
-            for (int64_t h = 0; h < H; h++)
-                if (m->contact_w[l * H + h] != 0.0f) heads[l * H + m->nz[l]++] = (int)h;
-        int rc = upload(m, m->d_contact_w, m->contact_w.data(), m->contact_w.size());
-        if (!rc) rc = upload(m, m->d_heads, heads.data(), heads.size());
-        if (rc) return fail(rc);
-    }
-    *out = m;
-    return CIH_OK;
-}
-
-int cih_model_create_from_file(const char *path, int32_t quantize_to, const float *contact_w, float contact_b,
-                               cih_model **out) {
-    if (!path || !out) return set_error(CIH_ERR_ARG, "null argument");
-    HostModel hm;
-    if (int rc = load_file(path, hm)) return rc;
-    if (quantize_to == DT_Q8 || quantize_to == DT_Q4) {
-        if (hm.dtype != DT_FP32 && hm.dtype != quantize_to)
-            return set_error(CIH_ERR_ARG, "cannot requantize a dtype %d file to %d", hm.dtype, quantize_to);
-        if (hm.dtype == DT_FP32) quantize_host_model(hm, quantize_to);
-    } else if (quantize_to != -1 && quantize_to != hm.dtype) {
-        return set_error(CIH_ERR_ARG, "bad quantize_to %d", quantize_to);
-    }
-    cih_host_weights w{};
-    const bool q = hm.dtype != DT_FP32;
-    w.token_embedding_table = hm.dtype == DT_Q8 ? (const void *)hm.q.emb.data() : (const void *)hm.f.emb.data();
-    w.ln_1_weight = hm.f.ln1w.data(); w.ln_1_bias = hm.f.ln1b.data();
-    w.wq = q ? (const void *)hm.q.wq.data() : hm.f.wq.data(); w.bq = hm.f.bq.data();
-    w.wk = q ? (const void *)hm.q.wk.data() : hm.f.wk.data(); w.bk = hm.f.bk.data();
-    w.wv = q ? (const void *)hm.q.wv.data() : hm.f.wv.data(); w.bv = hm.f.bv.data();
-    w.wo = q ? (const void *)hm.q.wo.data() : hm.f.wo.data(); w.bo = hm.f.bo.data();
-    w.ln_2_weight = hm.f.ln2w.data(); w.ln_2_bias = hm.f.ln2b.data();
-    w.fc1_weight = q ? (const void *)hm.q.fc1.data() : hm.f.fc1.data(); w.fc1_bias = hm.f.fc1b.data();
-    w.fc2_weight = q ? (const void *)hm.q.fc2.data() : hm.f.fc2.data(); w.fc2_bias = hm.f.fc2b.data();
-    w.ln_f_weight = hm.f.lnfw.data(); w.ln_f_bias = hm.f.lnfb.data();
-    w.classifier_weights = hm.f.cls.data();
-    w.classifier_len = (int64_t)hm.f.cls.size();
-    return cih_model_create(&hm.cfg, hm.dtype, &w, contact_w, contact_b, out);
-}
 
 int cih_model_config(const cih_model *m, cih_config *cfg, int32_t *dtype) {
     if (!m) return set_error(CIH_ERR_ARG, "null model");
@@ -810,7 +550,7 @@ int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w, c
     if (dtype != DT_FP32 && dtype != DT_Q8 && dtype != DT_Q4) return set_error(CIH_ERR_ARG, "bad dtype");
     if (seq_len == 0) return CIH_OK;
     cih_model tmp;  // owns the temporary allocations
-    int rc = upload_matrix(&tmp, dtype, in_dim, {{w, out_dim}}, tmp.emb);
+    int rc = upload_matrix(&tmp, dtype, dtype, in_dim, {{w, out_dim}}, tmp.emb);
     float *dx = nullptr, *db = nullptr, *dy = nullptr;
     if (!rc) rc = upload(&tmp, dx, x, (size_t)seq_len * in_dim);
     if (!rc) rc = upload(&tmp, db, bias, (size_t)out_dim);
@@ -835,10 +575,10 @@ int cih_dequantize_device(int32_t dtype, const void *blocks, int64_t nblocks, fl
     if (!blocks || !out || nblocks < 0) return set_error(CIH_ERR_ARG, "bad argument");
     if (dtype != DT_Q8 && dtype != DT_Q4) return set_error(CIH_ERR_ARG, "dtype must be Q8_0 or Q4_0");
     if (nblocks == 0) return CIH_OK;
-    if (nblocks > (int64_t)1 << 30) return set_error(CIH_ERR_SHAPE, "too many blocks");
+    if (nblocks > INT32_MAX / 32) return set_error(CIH_ERR_SHAPE, "too many blocks");
     // one row of nblocks blocks: K = 32 * nblocks, N = 1
     cih_model tmp;
-    int rc = upload_matrix(&tmp, dtype, (int)(nblocks * 32), {{blocks, 1}}, tmp.emb);
+    int rc = upload_matrix(&tmp, dtype, dtype, (int)(nblocks * 32), {{blocks, 1}}, tmp.emb);
     float *dy = nullptr;
     if (!rc && dalloc(dy, (size_t)nblocks * 32, tmp.allocs) != hipSuccess) rc = set_error(CIH_ERR_HIP, "alloc failed");
     if (!rc) {
@@ -849,6 +589,32 @@ int cih_dequantize_device(int32_t dtype, const void *blocks, int64_t nblocks, fl
     }
     free_list(tmp.allocs);
     return rc;
+}
+
+int cih_quantize_device(int32_t dtype, const float *src, int64_t n, void *dst) {
+    if (!src || !dst || n < 0 || n % 32) return set_error(CIH_ERR_ARG, "n must be a non-negative multiple of 32");
+    if (dtype != DT_Q8 && dtype != DT_Q4) return set_error(CIH_ERR_ARG, "dtype must be Q8_0 or Q4_0");
+    if (n == 0) return CIH_OK;
+    if (n > INT32_MAX / 32 * 32) return set_error(CIH_ERR_SHAPE, "too many values");
+    // one row of n values quantized by the loader's kernel: qs [n/32][1][qb], sc [n/32]
+    cih_model tmp;
+    int rc = upload_matrix(&tmp, DT_FP32, dtype, (int)n, {{src, 1}}, tmp.emb);
+    const int64_t nb = n / 32, qb = block_bytes(dtype) - 4;
+    std::vector<uint8_t> qs(nb * qb);
+    std::vector<float> sc(nb);
+    if (!rc) {
+        hipError_t e = hipMemcpy(qs.data(), tmp.emb.q, qs.size(), hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(sc.data(), tmp.emb.sc, nb * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = set_error(CIH_ERR_HIP, "quantize failed: %s", hipGetErrorString(e));
+    }
+    free_list(tmp.allocs);
+    if (rc) return rc;
+    uint8_t *o = (uint8_t *)dst;
+    for (int64_t b = 0; b < nb; b++) {
+        std::memcpy(o + b * (qb + 4), &sc[b], 4);
+        std::memcpy(o + b * (qb + 4) + 4, &qs[b * qb], qb);
+    }
+    return CIH_OK;
 }
 
 // ---- host helpers ----------------------------------------------------------------

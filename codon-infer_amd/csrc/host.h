@@ -36,21 +36,6 @@ void parallel_for(int64_t n, F fn) {
     for (auto &t : th) t.join();
 }
 
-// Owned host copy of a model read from a file (the reference's EsmWeights*
-// structs).  FP32 tensors live in `f`; quantized matrices (and the Q8
-// embedding) in `q` as packed blocks.
-struct HostModel {
-    cih_config cfg{};
-    int dtype = DT_FP32;
-    struct {
-        std::vector<float> emb, ln1w, ln1b, wq, bq, wk, bk, wv, bv, wo, bo, ln2w, ln2b, fc1, fc1b, fc2, fc2b, lnfw,
-            lnfb, cls;
-    } f;
-    struct {
-        std::vector<uint8_t> emb, wq, wk, wv, wo, fc1, fc2;
-    } q;
-};
-
 void quantize_q8_block(const float *x, uint8_t *blk);
 void quantize_q4_block(const float *x, uint8_t *blk);
 void dequantize_q8_block(const uint8_t *blk, float *out);
@@ -58,7 +43,5 @@ void dequantize_q4_block(const uint8_t *blk, float *out);
 void quantize_matrix(int dtype, const float *src, int64_t n, uint8_t *dst);
 int tokenize(const char *text, int32_t *out, int32_t cap);
 void log_softmax_canonical(const float *logits, float *out33);
-int load_file(const char *path, HostModel &hm);
-void quantize_host_model(HostModel &hm, int dtype);
 
 }  // namespace cih

@@ -74,6 +74,21 @@ hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const
 // reference's row-major [N][K] FP32 (test path).
 hipError_t launch_dequant(const DevMatrix &W, float *out, hipStream_t st);
 
+// Weight residency.  src: a [N][K] matrix in the reference's row-major
+// layout (FP32 values, or packed 36-byte Q8_0 / 20-byte Q4_0 blocks; src_fmt
+// a WFmt) in device memory, 4-byte aligned.  Writes rows [n_off, n_off + N)
+// of dst (k-block-major, dst.K = K).  src_fmt == dst.fmt repacks the bytes
+// unchanged; FP32 into Q8_0 / Q4_0 quantizes (bit-exact with the reference's
+// quantizers).
+hipError_t launch_load_matrix(const uint8_t *src, int src_fmt, int N, const DevMatrix &dst, int n_off, hipStream_t st);
+
+// n floats from src + src_bytes to dst + dst_bytes, one workgroup per segment
+// (segs in device memory).
+struct CopySeg {
+    int64_t src, dst, n;
+};
+hipError_t launch_copy_segments(const uint8_t *src, uint8_t *dst, const CopySeg *segs, int count, hipStream_t st);
+
 struct SeqMeta {
     const int *cu;    // [B] first packed row of each sequence
     const int *lens;  // [B] tokens per sequence

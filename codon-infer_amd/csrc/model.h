@@ -1,0 +1,115 @@
+// Device-resident model and workspace (shared by the forward, the loader and
+// the utility entry points).  Internal, not part of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "host.h"
+#include "kernels.h"
+
+#define HIPCHK(expr)                                                                                     \
+    do {                                                                                                 \
+        hipError_t e_ = (expr);                                                                          \
+        if (e_ != hipSuccess) return set_error(CIH_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+namespace cih {
+
+struct Layer {
+    DevMatrix wqkv, wo, w1, w2;
+    float *bqkv = nullptr, *bo = nullptr, *b1 = nullptr, *b2 = nullptr;
+    float *ln1w = nullptr, *ln1b = nullptr, *ln2w = nullptr, *ln2b = nullptr;
+};
+
+struct Workspace {
+    int maxB = 0, maxS = 0;
+    uint32_t flags = 0;
+    int *tokens = nullptr, *cu = nullptr, *lens = nullptr;
+    int *h_meta = nullptr;  // pinned: cu[maxB] | lens[maxB]
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *ao = nullptr, *hbuf = nullptr, *logits = nullptr;
+    float *rope_c = nullptr, *rope_s = nullptr;
+    float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
+    float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
+    float *rowsum = nullptr, *colpart = nullptr;        // contacts: map row sums, column partial sums
+    PartialBuf part;                                    // partial sums of k-split GEMMs / GEMVs
+    int *dms_meta = nullptr;                            // [max(maxB, maxS)][2] scored row, wild type
+    float *dms_out = nullptr;                           // [max(maxB, maxS)][21] deltas, entropy
+    // device staging of outputs for host-pointer calls (padded layouts)
+    float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
+          *o_layer = nullptr;
+    std::vector<void *> dev, host;
+};
+
+struct Prof {
+    bool on = false;
+    std::vector<hipEvent_t> ev;  // pairs
+    std::vector<int> cls;
+    std::vector<double> flops, bytes;
+    size_t used = 0;
+    cih_kernel_stats st[CIH_KC_COUNT] = {};
+};
+
+}  // namespace cih
+
+struct cih_model {
+    cih_config cfg{};
+    int dtype = 0, hd = 0;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void *> allocs;
+    cih::DevMatrix emb;
+    std::vector<cih::Layer> layers;
+    float *lnfw = nullptr, *lnfb = nullptr;
+    bool has_head = false;
+    cih::DevMatrix dense, dec;
+    float *dense_b = nullptr, *lm_lnw = nullptr, *lm_lnb = nullptr, *dec_b = nullptr;
+    std::vector<float> contact_w;
+    float contact_b = 0.0f;
+    bool has_contacts = false;
+    float *d_contact_w = nullptr;
+    int *d_heads = nullptr;  // [L][H] per-layer list of heads with nonzero weight
+    std::vector<int> nz;
+    cih::Workspace ws;
+    cih::Prof prof;
+};
+
+namespace cih {
+
+template <class T>
+hipError_t dalloc(T *&p, size_t n, std::vector<void *> &list) {
+    p = nullptr;
+    if (n == 0) return hipSuccess;
+    void *v = nullptr;
+    hipError_t e = hipMalloc(&v, n * sizeof(T));
+    if (e != hipSuccess) return e;
+    list.push_back(v);
+    p = (T *)v;
+    return hipSuccess;
+}
+
+template <class T>
+int upload(cih_model *m, T *&dst, const T *src, size_t n) {
+    HIPCHK(dalloc(dst, n, m->allocs));
+    if (n) HIPCHK(hipMemcpy(dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+    return 0;
+}
+
+void free_list(std::vector<void *> &l);
+int check_config(const cih_config *c);
+
+// One [N][K] host matrix (FP32 values or reference row-major blocks) that
+// becomes rows [n_off, n_off + N) of a device matrix.
+struct Part {
+    const void *src;
+    int N;
+};
+
+// Builds a device matrix in the k-block-major layout from host parts of
+// dtype src_dt (one H2D copy, repack on the GPU), stored as dst_dt: equal to
+// src_dt, or Q8_0 / Q4_0 quantized on the GPU from FP32.  Buffers go to
+// m->allocs.
+int upload_matrix(cih_model *m, int src_dt, int dst_dt, int K, const std::vector<Part> &parts, DevMatrix &out);
+
+}  // namespace cih

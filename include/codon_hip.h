@@ -113,7 +113,10 @@ int cih_model_create(const cih_config *cfg, int32_t dtype, const cih_host_weight
  * (lib.rs:277-296): reads a CODQ (FP32/Q8_0/Q4_0) or headerless
  * grouped_canonical_v1 / sequential_hf FP32 file.  quantize_to: -1 keeps the
  * file's dtype; CIH_DTYPE_Q8_0 / CIH_DTYPE_Q4_0 quantize an FP32 file in
- * memory (lib.rs:559-607).  Contact weights as in cih_model_create. */
+ * memory (lib.rs:559-607).  Contact weights as in cih_model_create.
+ * The file body goes to the GPU as is (parallel reads into pinned staging
+ * buffers, asynchronous copies); the repack and any quantization run there.
+ * CIH_LOAD_THREADS / CIH_LOAD_CHUNK_MB size the staging (default 8 x 8 MiB). */
 int cih_model_create_from_file(const char *path, int32_t quantize_to, const float *contact_w,
                                float contact_b, cih_model **out);
 
@@ -167,6 +170,12 @@ int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w,
 /* Dequantizes nblocks blocks on the GPU with the decode routine the GEMMs
  * use (BlockQ8_0/BlockQ4_0::dequantize_to, lib.rs:663-667, 1074-1082). */
 int cih_dequantize_device(int32_t dtype, const void *blocks, int64_t nblocks, float *out);
+
+/* quantize_slice_to_q8 / quantize_slice_to_q4 (lib.rs:670-673, 1085-1088)
+ * on the GPU, with the kernel that cih_model_create_from_file(quantize_to)
+ * runs on FP32 weights; bit-identical to cih_quantize_q8 / cih_quantize_q4.
+ * n must be a multiple of 32; dst holds n/32 blocks. */
+int cih_quantize_device(int32_t dtype, const float *src, int64_t n, void *dst);
 
 /* ---- host helpers (no GPU) ---------------------------------------------- */
 
