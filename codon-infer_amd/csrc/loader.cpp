@@ -261,7 +261,7 @@ int stage(int device, int fd, const std::vector<Region> &regs, uint8_t *img) {
             chunks.push_back({r.host ? r.host + o : nullptr, r.file_off + o, r.img_off + o, std::min(chunk, r.bytes - o)});
     if (chunks.empty()) return 0;
     const int hw = (int)std::max(1u, std::thread::hardware_concurrency());
-    const int nt = (int)std::min<int64_t>((int64_t)chunks.size(), env_int("CIH_LOAD_THREADS", std::min(8, hw), 1, 64));
+    const int nt = (int)std::min<int64_t>((int64_t)chunks.size(), env_int("CIH_LOAD_THREADS", std::min(2, hw), 1, 64));
     std::atomic<size_t> next{0};
     std::atomic<bool> failed{false};
     std::mutex mu;

@@ -116,7 +116,7 @@ int cih_model_create(const cih_config *cfg, int32_t dtype, const cih_host_weight
  * memory (lib.rs:559-607).  Contact weights as in cih_model_create.
  * The file body goes to the GPU as is (parallel reads into pinned staging
  * buffers, asynchronous copies); the repack and any quantization run there.
- * CIH_LOAD_THREADS / CIH_LOAD_CHUNK_MB size the staging (default 8 x 8 MiB). */
+ * CIH_LOAD_THREADS / CIH_LOAD_CHUNK_MB size the staging (default 2 x 8 MiB). */
 int cih_model_create_from_file(const char *path, int32_t quantize_to, const float *contact_w,
                                float contact_b, cih_model **out);
 
