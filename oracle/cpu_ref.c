@@ -1,6 +1,7 @@
 /*
  * cpu_ref.c — CPU restatement of the codon-infer ESM-2 bidirectional forward
- * (FP32 / Q8_0 / Q4_0).  TEST INFRASTRUCTURE: the oracle for the HIP path and
+ * (FP32 / Q8_0 / Q4_0), and of its autoregressive one-token forward with a
+ * KV cache, sampler and generation loop.  TEST INFRASTRUCTURE: the oracle for the HIP path and
  * the timed CPU baseline.  The product never links or calls this file.
  *
  * Numerics follow the reference routine by routine (file:line cited at each
@@ -620,6 +621,278 @@ int32_t cr_forward(const cr_config *cfg, const cr_weights *w, const int32_t *tok
     free(x); free(xb); free(q); free(k); free(v); free(oa); free(hb); free(hb2); free(att);
     free(head_att); free(final_att); free(rc); free(rsn); free(cl);
     return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* The autoregressive path: forward_parallel (FP32, lib.rs:3558-3739),        */
+/* forward_q8 (3741-3930), forward_q4 (4016-4201), one token at a position   */
+/* against a KV cache, and generate_sequence* (6538-6827).                   */
+/* ------------------------------------------------------------------------ */
+
+/* matmul_avx2_fma, lib.rs:2577-2596: four 8-wide FMA accumulators over
+ * 32-wide chunks, hsum((a0 + a1) + (a2 + a3)), + bias. */
+__attribute__((target("avx2,fma")))
+static void matvec_f32(float *out, const float *x, const float *w, const float *bias, int in_dim, int r0, int r1) {
+    int chunks = in_dim / 32, rem = chunks * 32;
+    for (int i = r0; i < r1; i++) {
+        const float *wr = w + (int64_t)i * in_dim;
+        __m256 a0 = _mm256_setzero_ps(), a1 = _mm256_setzero_ps(), a2 = _mm256_setzero_ps(), a3 = _mm256_setzero_ps();
+        for (int c = 0; c < chunks; c++) {
+            int o = c * 32;
+            a0 = _mm256_fmadd_ps(_mm256_loadu_ps(wr + o), _mm256_loadu_ps(x + o), a0);
+            a1 = _mm256_fmadd_ps(_mm256_loadu_ps(wr + o + 8), _mm256_loadu_ps(x + o + 8), a1);
+            a2 = _mm256_fmadd_ps(_mm256_loadu_ps(wr + o + 16), _mm256_loadu_ps(x + o + 16), a2);
+            a3 = _mm256_fmadd_ps(_mm256_loadu_ps(wr + o + 24), _mm256_loadu_ps(x + o + 24), a3);
+        }
+        float v = hsum256(_mm256_add_ps(_mm256_add_ps(a0, a1), _mm256_add_ps(a2, a3)));
+        for (int k = rem; k < in_dim; k++) v += wr[k] * x[k];
+        out[i] = v + bias[i];
+    }
+}
+
+/* matmul_q8_avx2_fma, lib.rs:2916-2948: per block an 8-wide FMA accumulator
+ * of (q as f32) * x over 4 chunks, row_sum += hsum(acc) * d, + bias. */
+__attribute__((target("avx2,fma")))
+static void matvec_q8(float *out, const float *x, const uint8_t *w, const float *bias, int in_dim, int r0, int r1) {
+    int bpr = in_dim / 32;
+    for (int i = r0; i < r1; i++) {
+        float row = 0.0f;
+        for (int b = 0; b < bpr; b++) {
+            const uint8_t *blk = w + ((int64_t)i * bpr + b) * CR_Q8_BLOCK_BYTES;
+            const float *xb = x + b * 32;
+            __m256 acc = _mm256_setzero_ps();
+            for (int c = 0; c < 4; c++) {
+                __m128i raw = _mm_loadl_epi64((const __m128i *)(blk + 4 + c * 8));
+                __m256 vq = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(raw));
+                acc = _mm256_fmadd_ps(vq, _mm256_loadu_ps(xb + c * 8), acc);
+            }
+            row += hsum256(acc) * rd_f32(blk);
+        }
+        out[i] = row + bias[i];
+    }
+}
+
+/* matmul_q4_avx2_fma, lib.rs:3155-3210: low nibbles - 8 are elements 0..15,
+ * high nibbles - 8 elements 16..31, four FMAs in element order. */
+__attribute__((target("avx2,fma")))
+static void matvec_q4(float *out, const float *x, const uint8_t *w, const float *bias, int in_dim, int r0, int r1) {
+    int bpr = in_dim / 32;
+    for (int i = r0; i < r1; i++) {
+        float row = 0.0f;
+        for (int b = 0; b < bpr; b++) {
+            const uint8_t *blk = w + ((int64_t)i * bpr + b) * CR_Q4_BLOCK_BYTES;
+            const float *xb = x + b * 32;
+            int8_t lo[16], hi[16];
+            for (int j = 0; j < 16; j++) {
+                lo[j] = (int8_t)((blk[4 + j] & 0x0F) - 8);
+                hi[j] = (int8_t)((blk[4 + j] >> 4) - 8);
+            }
+            __m128i vlo = _mm_loadu_si128((const __m128i *)lo), vhi = _mm_loadu_si128((const __m128i *)hi);
+            __m256 acc = _mm256_setzero_ps();
+            acc = _mm256_fmadd_ps(_mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(vlo)), _mm256_loadu_ps(xb), acc);
+            acc = _mm256_fmadd_ps(_mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_srli_si128(vlo, 8))),
+                                  _mm256_loadu_ps(xb + 8), acc);
+            acc = _mm256_fmadd_ps(_mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(vhi)), _mm256_loadu_ps(xb + 16), acc);
+            acc = _mm256_fmadd_ps(_mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_srli_si128(vhi, 8))),
+                                  _mm256_loadu_ps(xb + 24), acc);
+            row += hsum256(acc) * rd_f32(blk);
+        }
+        out[i] = row + bias[i];
+    }
+}
+
+typedef struct {
+    int32_t wdtype;
+    float *out;
+    const float *x;
+    const void *w;
+    const float *bias;
+    int in_dim, out_dim;
+} matvec_job;
+
+/* run_{fp32,q8,q4}_slice, lib.rs:2845-2858, 3011-3025, 3249-3263 */
+static void matvec_slice(const void *ctx, int t, int n) {
+    const matvec_job *j = (const matvec_job *)ctx;
+    int chunk = (j->out_dim + n - 1) / n, r0 = t * chunk;
+    if (r0 >= j->out_dim) return;
+    int r1 = r0 + chunk < j->out_dim ? r0 + chunk : j->out_dim;
+    if (j->wdtype == CR_FP32) matvec_f32(j->out, j->x, (const float *)j->w, j->bias, j->in_dim, r0, r1);
+    else if (j->wdtype == CR_Q8_0) matvec_q8(j->out, j->x, (const uint8_t *)j->w, j->bias, j->in_dim, r0, r1);
+    else matvec_q4(j->out, j->x, (const uint8_t *)j->w, j->bias, j->in_dim, r0, r1);
+}
+
+/* matmul_parallel / matmul_q8_parallel / matmul_q4_parallel
+ * (lib.rs:2860-2882, 3027-3051, 3265-3289) */
+void cr_matmul_vec(int32_t wdtype, float *out, const float *x, const void *w, const float *bias,
+                   int32_t in_dim, int32_t out_dim, int32_t num_threads) {
+    matvec_job j = {wdtype, out, x, w, bias, in_dim, out_dim};
+    if (num_threads <= 1 || out_dim < 32) matvec_slice(&j, 0, 1);
+    else run_parallel(num_threads, matvec_slice, &j);
+}
+
+/* RunState::new, lib.rs:2464-2486: per-layer K/V caches [L][max_len][d],
+ * RoPE tables for max_len positions, logits. */
+cr_run_state *cr_run_state_new(const cr_config *cfg, int32_t max_len) {
+    const int hd = cfg->dim / cfg->n_heads;
+    cr_run_state *s = calloc(1, sizeof *s);
+    s->max_len = max_len;
+    s->key_cache = calloc((size_t)cfg->n_layers * max_len * cfg->dim, 4);
+    s->value_cache = calloc((size_t)cfg->n_layers * max_len * cfg->dim, 4);
+    s->rope_cos = calloc((size_t)max_len * (hd / 2), 4);
+    s->rope_sin = calloc((size_t)max_len * (hd / 2), 4);
+    s->logits = calloc((size_t)cfg->vocab_size, 4);
+    cr_rope_tables(max_len, hd, s->rope_cos, s->rope_sin);
+    return s;
+}
+
+void cr_run_state_free(cr_run_state *s) {
+    if (!s) return;
+    free(s->key_cache); free(s->value_cache); free(s->rope_cos); free(s->rope_sin); free(s->logits);
+    free(s);
+}
+
+int32_t cr_forward_step(const cr_config *cfg, const cr_weights *w, int32_t token, int32_t pos, cr_run_state *s,
+                        int32_t nt) {
+    const int d = cfg->dim, F = cfg->hidden_dim, L = cfg->n_layers, H = cfg->n_heads, V = cfg->vocab_size;
+    if (token < 0 || token >= V) return -2;
+    if (pos < 0 || pos >= s->max_len) return -3;
+    const int hd = d / H;
+    const int32_t dt = w->dtype;
+    const float inv_scale = 1.0f / sqrtf((float)hd);
+    const float embed_scale = 1.0f - 0.12f;
+    float *x = calloc(d, 4), *xb = calloc(d, 4), *xb2 = calloc(d, 4);
+    float *q = calloc(d, 4), *k = calloc(d, 4), *v = calloc(d, 4), *att = calloc((size_t)pos + 1, 4);
+    int hbw = F > d ? F : d;
+    float *hb = calloc(hbw, 4), *hb2 = calloc(hbw, 4);
+
+    /* embedding (lib.rs:3567-3575; Q8 3753-3765): <mask> is a zero row */
+    if (token != 32) {
+        if (dt == CR_Q8_0)
+            cr_dequantize_q8((const uint8_t *)w->token_embedding_table + (int64_t)token * (d / 32) * CR_Q8_BLOCK_BYTES,
+                             d / 32, x);
+        else
+            memcpy(x, (const float *)w->token_embedding_table + (int64_t)token * d, sizeof(float) * d);
+        for (int i = 0; i < d; i++) x[i] *= embed_scale;
+    }
+    for (int l = 0; l < L; l++) {
+        cr_layer_norm(xb, x, w->ln_1_weight + (int64_t)l * d, w->ln_1_bias + (int64_t)l * d, d);
+        cr_matmul_vec(dt, q, xb, mat_at(w->wq, dt, l, d, d), w->bq + (int64_t)l * d, d, d, nt);
+        cr_matmul_vec(dt, k, xb, mat_at(w->wk, dt, l, d, d), w->bk + (int64_t)l * d, d, d, nt);
+        cr_matmul_vec(dt, v, xb, mat_at(w->wv, dt, l, d, d), w->bv + (int64_t)l * d, d, d, nt);
+        cr_apply_rope(q, k, s->rope_cos, s->rope_sin, pos, d, H);
+        float *kc = s->key_cache + (int64_t)l * s->max_len * d, *vc = s->value_cache + (int64_t)l * s->max_len * d;
+        memcpy(kc + (int64_t)pos * d, k, sizeof(float) * d);
+        memcpy(vc + (int64_t)pos * d, v, sizeof(float) * d);
+        /* attention_head_avx1, lib.rs:3438-3483 (256-bit path) */
+        for (int h = 0; h < H; h++) {
+            const float *qh = q + h * hd;
+            for (int t = 0; t <= pos; t++) att[t] = dot_head(qh, kc + (int64_t)t * d + h * hd, hd) * inv_scale;
+            cr_softmax(att, pos + 1);
+            float *o = xb2 + h * hd;
+            memset(o, 0, sizeof(float) * hd);
+            for (int t = 0; t <= pos; t++) axpy_head(o, vc + (int64_t)t * d + h * hd, att[t], hd);
+        }
+        cr_matmul_vec(dt, xb, xb2, mat_at(w->wo, dt, l, d, d), w->bo + (int64_t)l * d, d, d, nt);
+        for (int i = 0; i < d; i++) x[i] += xb[i];
+        cr_layer_norm(xb, x, w->ln_2_weight + (int64_t)l * d, w->ln_2_bias + (int64_t)l * d, d);
+        cr_matmul_vec(dt, hb, xb, mat_at(w->fc1_weight, dt, l, F, d), w->fc1_bias + (int64_t)l * F, d, F, nt);
+        cr_gelu(hb2, hb, F);
+        cr_matmul_vec(dt, xb, hb2, mat_at(w->fc2_weight, dt, l, d, F), w->fc2_bias + (int64_t)l * d, F, d, nt);
+        for (int i = 0; i < d; i++) x[i] += xb[i];
+    }
+    cr_layer_norm(xb, x, w->ln_f_weight, w->ln_f_bias, d);
+    /* project_lm_head_parallel / _q8 / _q4, lib.rs:3952-4015, 4203-4233 */
+    int64_t req = 3 * (int64_t)d + (int64_t)d * d + (int64_t)V * d + V;
+    if (w->classifier_len >= req) {
+        const float *cw = w->classifier_weights;
+        const float *lnw = cw, *lnb = cw + d, *dw = cw + 2 * d, *db = cw + 2 * d + (int64_t)d * d;
+        const float *decw = cw + 3 * d + (int64_t)d * d, *decb = decw + (int64_t)V * d;
+        cr_matmul_vec(CR_FP32, hb, xb, dw, db, d, d, nt);
+        cr_gelu(hb2, hb, d);
+        cr_layer_norm(hb, hb2, lnw, lnb, d);
+        cr_matmul_vec(CR_FP32, s->logits, hb, decw, decb, d, V, nt);
+    } else {
+        float *zb = calloc((size_t)V, 4);
+        cr_matmul_vec(dt == CR_Q8_0 ? CR_Q8_0 : CR_FP32, s->logits, xb, w->token_embedding_table, zb, d, V, nt);
+        free(zb);
+    }
+    free(x); free(xb); free(xb2); free(q); free(k); free(v); free(att); free(hb); free(hb2);
+    return 0;
+}
+
+/* SimpleRng, lib.rs:3506-3511: xorshift64 (13, 7, 17); seed 0 is replaced */
+uint64_t cr_rng_seed(uint64_t seed) { return seed == 0 ? 0x123456789abcdefULL : seed; }
+
+uint32_t cr_rng_next_u32(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return (uint32_t)(x & 0xffffffffULL);
+}
+
+float cr_rng_next_f32(uint64_t *state) { return (float)cr_rng_next_u32(state) / (float)UINT32_MAX; }
+
+/* sample, lib.rs:3513-3530: only ids 4..=23 and <eos> (2) stay; T <= 0 is
+ * argmax (first maximum); otherwise logits / T, softmax, inverse CDF. */
+int32_t cr_sample(float *logits, int32_t V, float temperature, uint64_t *rng) {
+    for (int i = 0; i < V; i++)
+        if (!((i >= 4 && i <= 23) || i == 2)) logits[i] = -INFINITY;
+    if (temperature <= 0.0f) {
+        float mv = logits[0];
+        int mi = 0;
+        for (int i = 1; i < V; i++)
+            if (logits[i] > mv) { mv = logits[i]; mi = i; }
+        return mi;
+    }
+    const float inv_temp = 1.0f / temperature;
+    for (int i = 0; i < V; i++)
+        if (logits[i] != -INFINITY) logits[i] *= inv_temp;
+    cr_softmax(logits, V);
+    const float r = cr_rng_next_f32(rng);
+    float cum = 0.0f;
+    for (int i = 0; i < V; i++) {
+        if (isnan(logits[i]) || logits[i] == 0.0f) continue;
+        cum += logits[i];
+        if (r <= cum) return i;
+    }
+    return 4;
+}
+
+/* generate_sequence_parallel / _q8 / _q4, lib.rs:6551-6827, from the token
+ * ids the reference derives from the prompt (Tokenizer::encode minus the
+ * trailing <eos>; [0] if empty).  max_new < 0 means no limit.  Returns the
+ * number of generated tokens (written to out, at most out_cap) or < 0. */
+int32_t cr_generate(const cr_config *cfg, const cr_weights *w, const int32_t *prompt, int32_t n_prompt,
+                    float temperature, int32_t max_new, uint64_t seed, int32_t max_seq_len, int32_t nt,
+                    int32_t *out, int32_t out_cap) {
+    cr_run_state *s = cr_run_state_new(cfg, max_seq_len);
+    int pos = 0, rc = 0;
+    for (int i = 0; i < n_prompt && pos < max_seq_len; i++) {
+        if ((rc = cr_forward_step(cfg, w, prompt[i], pos, s, nt)) != 0) goto done;
+        pos++;
+    }
+    {
+        uint64_t rng = cr_rng_seed(seed);
+        int limit = max_new >= 0 ? (pos + max_new < max_seq_len ? pos + max_new : max_seq_len) : max_seq_len;
+        int n = 0;
+        float *lg = malloc(sizeof(float) * cfg->vocab_size);
+        while (pos < limit) {
+            memcpy(lg, s->logits, sizeof(float) * cfg->vocab_size);
+            int tok = cr_sample(lg, cfg->vocab_size, temperature, &rng);
+            if (tok == 2) break;
+            if (n >= out_cap) { rc = -5; break; }
+            out[n++] = tok;
+            if ((rc = cr_forward_step(cfg, w, tok, pos, s, nt)) != 0) break;
+            pos++;
+        }
+        free(lg);
+        if (!rc) rc = n;
+    }
+done:
+    cr_run_state_free(s);
+    return rc;
 }
 
 /* ------------------------------------------------------------------------ */

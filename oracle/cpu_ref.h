@@ -1,5 +1,6 @@
 /*
- * cpu_ref — CPU restatement of the codon-infer ESM-2 bidirectional forward.
+ * cpu_ref — CPU restatement of the codon-infer ESM-2 bidirectional forward
+ * and of its autoregressive (KV-cache) forward and generation loop.
  *
  * TEST INFRASTRUCTURE ONLY.  This library is the oracle the HIP path is
  * checked against and the timed CPU baseline in bench.py.  Nothing in the
@@ -90,6 +91,40 @@ void cr_matmul_tiled(int32_t wdtype, float *out, const float *x, const void *w,
 /* one sequence, one forward.  Returns 0 or a negative error code. */
 int32_t cr_forward(const cr_config *cfg, const cr_weights *w, const int32_t *tokens,
                    int32_t seq_len, int32_t num_threads, const cr_outputs *out);
+
+/* ---- autoregressive path ---------------------------------------------- */
+
+/* out[i] = sum_k W[i][k] * x[k] + bias[i]  (matmul_{,q8_,q4_}parallel) */
+void cr_matmul_vec(int32_t wdtype, float *out, const float *x, const void *w, const float *bias,
+                   int32_t in_dim, int32_t out_dim, int32_t num_threads);
+
+/* RunState (lib.rs:2459-2486) */
+typedef struct cr_run_state {
+    int32_t max_len;
+    float *key_cache, *value_cache; /* [L][max_len][d] */
+    float *rope_cos, *rope_sin;     /* [max_len][hd/2] */
+    float *logits;                  /* [V] */
+} cr_run_state;
+cr_run_state *cr_run_state_new(const cr_config *cfg, int32_t max_len);
+void cr_run_state_free(cr_run_state *s);
+
+/* forward_parallel / forward_q8 / forward_q4 (lib.rs:3558, 3741, 4016):
+ * token at pos, K/V written to the cache at pos, logits in s->logits.
+ * 0, -2 (token out of range) or -3 (pos out of range). */
+int32_t cr_forward_step(const cr_config *cfg, const cr_weights *w, int32_t token, int32_t pos,
+                        cr_run_state *s, int32_t num_threads);
+
+/* SimpleRng and sample (lib.rs:3506-3530) */
+uint64_t cr_rng_seed(uint64_t seed);
+uint32_t cr_rng_next_u32(uint64_t *state);
+float cr_rng_next_f32(uint64_t *state);
+int32_t cr_sample(float *logits, int32_t vocab, float temperature, uint64_t *rng_state);
+
+/* generate_sequence* (lib.rs:6551-6827) from prompt token ids; returns the
+ * number of generated tokens or < 0 */
+int32_t cr_generate(const cr_config *cfg, const cr_weights *w, const int32_t *prompt, int32_t n_prompt,
+                    float temperature, int32_t max_new, uint64_t seed, int32_t max_seq_len,
+                    int32_t num_threads, int32_t *out, int32_t out_cap);
 
 /* metrics (lib.rs:2271-2377) */
 float cr_cosine_similarity(const float *a, const float *b, int64_t n);

@@ -52,6 +52,11 @@ class _Outputs(ctypes.Structure):
     ]
 
 
+class _RunState(ctypes.Structure):
+    _fields_ = [("max_len", ctypes.c_int32), ("key_cache", _f32p), ("value_cache", _f32p),
+                ("rope_cos", _f32p), ("rope_sin", _f32p), ("logits", _f32p)]
+
+
 WEIGHT_FIELDS = [
     "token_embedding_table", "ln_1_weight", "ln_1_bias", "wq", "bq", "wk", "bk", "wv", "bv",
     "wo", "bo", "ln_2_weight", "ln_2_bias", "fc1_weight", "fc1_bias", "fc2_weight", "fc2_bias",
@@ -88,6 +93,26 @@ def lib():
         L.cr_forward.argtypes = [ctypes.POINTER(_Config), ctypes.POINTER(_Weights), _i32p,
                                  ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_Outputs)]
         L.cr_forward.restype = ctypes.c_int32
+        L.cr_matmul_vec.argtypes = [ctypes.c_int32, _f32p, _f32p, ctypes.c_void_p, _f32p,
+                                    ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+        L.cr_run_state_new.argtypes = [ctypes.POINTER(_Config), ctypes.c_int32]
+        L.cr_run_state_new.restype = ctypes.POINTER(_RunState)
+        L.cr_run_state_free.argtypes = [ctypes.POINTER(_RunState)]
+        L.cr_forward_step.argtypes = [ctypes.POINTER(_Config), ctypes.POINTER(_Weights), ctypes.c_int32,
+                                      ctypes.c_int32, ctypes.POINTER(_RunState), ctypes.c_int32]
+        L.cr_forward_step.restype = ctypes.c_int32
+        L.cr_rng_seed.argtypes = [ctypes.c_uint64]
+        L.cr_rng_seed.restype = ctypes.c_uint64
+        L.cr_rng_next_u32.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.cr_rng_next_u32.restype = ctypes.c_uint32
+        L.cr_rng_next_f32.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.cr_rng_next_f32.restype = ctypes.c_float
+        L.cr_sample.argtypes = [_f32p, ctypes.c_int32, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]
+        L.cr_sample.restype = ctypes.c_int32
+        L.cr_generate.argtypes = [ctypes.POINTER(_Config), ctypes.POINTER(_Weights), _i32p, ctypes.c_int32,
+                                  ctypes.c_float, ctypes.c_int32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32,
+                                  _i32p, ctypes.c_int32]
+        L.cr_generate.restype = ctypes.c_int32
         for name in ("cr_cosine_similarity", "cr_rmse"):
             getattr(L, name).argtypes = [_f32p, _f32p, ctypes.c_int64]
             getattr(L, name).restype = ctypes.c_float
@@ -279,6 +304,94 @@ def matmul_tiled(dtype, x, w, bias, in_dim, out_dim, num_threads=1):
     out = np.empty((seq_len, out_dim), np.float32)
     lib().cr_matmul_tiled(dtype, _f(out), _f(x), w.ctypes.data, _f(bias), in_dim, out_dim, seq_len, num_threads)
     return out
+
+
+def _cfg_weights(cfg, weights):
+    c = _Config(cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.n_heads, cfg.vocab_size)
+    keep = []
+    wc = _Weights()
+    wc.dtype = int(weights.dtype)
+    for name in WEIGHT_FIELDS:
+        arr = np.ascontiguousarray(getattr(weights, name))
+        keep.append(arr)
+        setattr(wc, name, arr.ctypes.data)
+    wc.classifier_len = int(np.asarray(weights.classifier_weights).size)
+    return c, wc, keep
+
+
+def matmul_vec(dtype, x, w, bias, in_dim, out_dim, num_threads=1):
+    """matmul_parallel / matmul_q8_parallel / matmul_q4_parallel
+    (src/lib.rs:2860, 3027, 3265): one token."""
+    x = _c32(x)
+    w = np.ascontiguousarray(w)
+    bias = _c32(bias)
+    out = np.empty(out_dim, np.float32)
+    lib().cr_matmul_vec(dtype, _f(out), _f(x), w.ctypes.data, _f(bias), in_dim, out_dim, num_threads)
+    return out
+
+
+class RunState:
+    """RunState (src/lib.rs:2459-2486) with forward / forward_q8 / forward_q4
+    (3554, 3741, 4016) as step(): one token at one position against the KV
+    cache.  The K/V caches are views [L][max_len][d]."""
+
+    def __init__(self, cfg, weights, max_len=1024, num_threads=1):
+        self.cfg, self.nt = cfg, num_threads
+        self._c, self._w, self._keep = _cfg_weights(cfg, weights)
+        self._s = lib().cr_run_state_new(ctypes.byref(self._c), max_len)
+        self.max_len = max_len
+
+    def step(self, token, pos):
+        rc = lib().cr_forward_step(ctypes.byref(self._c), ctypes.byref(self._w), int(token), int(pos), self._s,
+                                   self.nt)
+        if rc != 0:
+            raise RuntimeError(f"cr_forward_step failed with code {rc}")
+        return np.ctypeslib.as_array(self._s.contents.logits, (self.cfg.vocab_size,)).copy()
+
+    def cache(self):
+        shp = (self.cfg.n_layers, self.max_len, self.cfg.dim)
+        return (np.ctypeslib.as_array(self._s.contents.key_cache, shp),
+                np.ctypeslib.as_array(self._s.contents.value_cache, shp))
+
+    def __del__(self):
+        if getattr(self, "_s", None):
+            lib().cr_run_state_free(self._s)
+            self._s = None
+
+
+class SimpleRng:
+    """SimpleRng (src/lib.rs:3506-3511) over the C restatement."""
+
+    def __init__(self, seed):
+        self.state = ctypes.c_uint64(lib().cr_rng_seed(seed))
+
+    def next_u32(self):
+        return lib().cr_rng_next_u32(ctypes.byref(self.state))
+
+    def next_f32(self):
+        return lib().cr_rng_next_f32(ctypes.byref(self.state))
+
+
+def sample(logits, temperature, rng):
+    """sample (src/lib.rs:3513-3530); rng: SimpleRng (advanced when T > 0)."""
+    lg = _c32(logits).copy()
+    return lib().cr_sample(_f(lg), lg.size, float(temperature), ctypes.byref(rng.state))
+
+
+def generate(cfg, weights, prompt_tokens, temperature=0.0, max_new_tokens=None, seed=0, max_seq_len=1024,
+             num_threads=1):
+    """generate_sequence* (src/lib.rs:6551-6827) from the prompt's token ids
+    (Tokenizer::encode minus the trailing <eos>): the generated token ids."""
+    c, wc, keep = _cfg_weights(cfg, weights)
+    prompt = np.ascontiguousarray(prompt_tokens, np.int32)
+    cap = max_seq_len
+    out = np.zeros(cap, np.int32)
+    n = lib().cr_generate(ctypes.byref(c), ctypes.byref(wc), prompt.ctypes.data_as(_i32p), prompt.size,
+                          float(temperature), -1 if max_new_tokens is None else int(max_new_tokens), seed,
+                          max_seq_len, num_threads, out.ctypes.data_as(_i32p), cap)
+    if n < 0:
+        raise RuntimeError(f"cr_generate failed with code {n}")
+    return out[:n].copy()
 
 
 def forward(cfg, weights, tokens, num_threads=1, contacts=None, attn=False, layer_hidden=False,
