@@ -1,7 +1,8 @@
 """codon_hip — MI355X (gfx950) ESM-2 bidirectional encoder behind a C ABI.
 
 Host-side mirror of codon-infer's model-load / forward / logits /
-attention-map API.  All compute runs in libcodon_hip.so (HIP kernels);
+attention-map API, its deep mutational scan and its autoregressive
+decoding.  All compute runs in libcodon_hip.so (HIP kernels);
 importing fails if the library has not been built.
 """
 from . import _lib
@@ -10,9 +11,10 @@ from ._lib import (CihError, DMS_MASKED_MARGINAL, DMS_WILDTYPE_MARGINAL, DTYPE_F
                    KC_GEMM_QUANT, KC_OTHER, OUT_ATTN, OUT_CONTACTS, OUT_FINAL_ATT, OUT_HIDDEN, OUT_LAYER_HIDDEN,
                    OUT_LOGITS)
 from .model import (CANONICAL_AAS, BidirectionalRunState, DmsPositionRow, EsmConfig, EsmWeights, EsmWeightsQ4,
-                    EsmWeightsQ8, GpuModel, Tokenizer, dequantize_blocks, run_pipeline_dms, dequantize_on_device, quantize_on_device, forward_bidirectional, forward_bidirectional_gpu,
-                    forward_bidirectional_q4, forward_bidirectional_q8, log_softmax_canonical, matmul_tiled,
-                    quantize_slice_to_q4, quantize_slice_to_q8, save_codq)
+                    EsmWeightsQ8, GenerationMetrics, GpuDecoder, GpuModel, Tokenizer, dequantize_blocks,
+                    dequantize_on_device, forward_bidirectional, forward_bidirectional_gpu, forward_bidirectional_q4,
+                    forward_bidirectional_q8, generate_sequence, log_softmax_canonical, matmul_tiled, prompt_tokens,
+                    quantize_on_device, quantize_slice_to_q4, quantize_slice_to_q8, run_pipeline_dms, save_codq)
 
 _lib.lib()  # load now: no silent fallback
 

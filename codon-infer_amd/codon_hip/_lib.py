@@ -31,6 +31,7 @@ EXPORTED = [
     "cih_model_destroy", "cih_forward", "cih_matmul_tiled", "cih_dequantize_device", "cih_quantize_device", "cih_quantize_q8",
     "cih_quantize_q4", "cih_dequantize_q8", "cih_dequantize_q4", "cih_tokenize", "cih_log_softmax_canonical",
     "cih_profile_enable", "cih_profile_read", "cih_last_error", "cih_abi_version", "cih_dms",
+    "cih_decoder_create", "cih_decoder_destroy", "cih_decoder_reset", "cih_decode", "cih_generate",
 ]
 
 DMS_MASKED_MARGINAL, DMS_WILDTYPE_MARGINAL = 0, 1
@@ -91,6 +92,12 @@ def lib():
         "cih_model_destroy": [vp],
         "cih_forward": [vp, vp, vp, i32, i32, ctypes.c_uint32, ctypes.POINTER(Outputs)],
         "cih_dms": [vp, vp, i32, i32, i32, i32, i32, vp, vp],
+        "cih_decoder_create": [vp, i32, i32, i32, pmodel],
+        "cih_decoder_destroy": [vp],
+        "cih_decoder_reset": [vp, i32],
+        "cih_decode": [vp, vp, vp, vp, i32, vp],
+        "cih_generate": [vp, i32, vp, vp, vp, f32, i32, vp, i32, vp, i32, vp, ctypes.POINTER(ctypes.c_double),
+                         ctypes.POINTER(ctypes.c_double)],
         "cih_matmul_tiled": [i32, vp, vp, vp, vp, i32, i32, i32],
         "cih_dequantize_device": [i32, vp, i64, vp],
         "cih_quantize_device": [i32, vp, i64, vp],

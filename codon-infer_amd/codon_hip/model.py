@@ -245,6 +245,14 @@ class Tokenizer:
         n = C.check(C.lib().cih_tokenize(text.encode(), out.ctypes.data, cap))
         return out[:n].copy()
 
+    _DECODE = dict(zip(range(4, 31), "LAGVSERTIDPKQNFYMHWCXBUZO.-"))
+    _DECODE[32] = "*"
+
+    @staticmethod
+    def decode(token_id):
+        """Tokenizer::decode (lib.rs:6523-6530): the residue letter or None."""
+        return Tokenizer._DECODE.get(int(token_id))
+
 
 def log_softmax_canonical(logits):
     """log_softmax_canonical (lib.rs:4426-4441) over one 33-logit row."""
@@ -472,3 +480,85 @@ def run_pipeline_dms(sequence, model, window_size=0, stride=0, mode=C.DMS_MASKED
     rows = [DmsPositionRow(p + 1, sequence[p], deltas[p], ent[p]) for p in range(len(sequence))]
     return rows, (len(sequence) * 20 / el if el > 0 else 0.0)
 
+
+
+class GenerationMetrics:
+    """GenerationMetrics (lib.rs:6533-6536)."""
+
+    def __init__(self, full_sequence, generated_suffix, tokens_generated, prefill_ms, generation_ms):
+        self.full_sequence, self.generated_suffix = full_sequence, generated_suffix
+        self.tokens_generated, self.prefill_ms, self.generation_ms = tokens_generated, prefill_ms, generation_ms
+        self.throughput_tps = tokens_generated / (generation_ms / 1e3) if generation_ms > 0 else 0.0
+
+
+class GpuDecoder:
+    """RunState (lib.rs:2459-2486) on the GPU for n_slots sequences: per-slot
+    KV caches, forward_* for batches of rows (decode), and the
+    generate_sequence* loop (generate)."""
+
+    def __init__(self, model, n_slots=1, max_len=None, max_rows=64):
+        self.model = model
+        self.max_len = max_len or model.cfg.max_seq_len
+        self._h = ctypes.c_void_p()
+        C.check(C.lib().cih_decoder_create(model._h, n_slots, self.max_len, max_rows, ctypes.byref(self._h)))
+        self.n_slots, self.max_rows = n_slots, max_rows
+
+    def close(self):
+        if self._h:
+            C.lib().cih_decoder_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self, slot=-1):
+        C.check(C.lib().cih_decoder_reset(self._h, slot))
+
+    def decode(self, slots, tokens, pos):
+        """forward / forward_q8 / forward_q4 (lib.rs:3554-4233) for rows
+        (slot, token, position): logits [n][vocab]."""
+        slots = np.ascontiguousarray(slots, np.int32)
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        n = slots.size
+        out = np.empty((n, self.model.cfg.vocab_size), np.float32)
+        C.check(C.lib().cih_decode(self._h, slots.ctypes.data, tokens.ctypes.data, pos.ctypes.data, n,
+                                   out.ctypes.data))
+        return out
+
+    def generate(self, prompts, temperature=0.0, max_new_tokens=None, seeds=None, slots=None, max_seq_len=0):
+        """generate_sequence* (lib.rs:6551-6827) for a list of prompt id
+        arrays: returns (list of generated id arrays, prefill_ms, generation_ms)."""
+        n = len(prompts)
+        slots = np.arange(n, dtype=np.int32) if slots is None else np.ascontiguousarray(slots, np.int32)
+        seeds = np.zeros(n, np.uint64) if seeds is None else np.ascontiguousarray(seeds, np.uint64)
+        flat = np.concatenate([np.asarray(p, np.int32) for p in prompts]).astype(np.int32)
+        offs = np.zeros(n + 1, np.int32)
+        offs[1:] = np.cumsum([len(p) for p in prompts])
+        cap = self.max_len
+        out = np.zeros((n, cap), np.int32)
+        cnt = np.zeros(n, np.int32)
+        pre, gen = ctypes.c_double(), ctypes.c_double()
+        C.check(C.lib().cih_generate(self._h, n, slots.ctypes.data, flat.ctypes.data, offs.ctypes.data,
+                                     float(temperature), -1 if max_new_tokens is None else int(max_new_tokens),
+                                     seeds.ctypes.data, int(max_seq_len), out.ctypes.data, cap, cnt.ctypes.data,
+                                     ctypes.byref(pre), ctypes.byref(gen)))
+        return [out[i, :cnt[i]].copy() for i in range(n)], pre.value, gen.value
+
+
+def prompt_tokens(prompt):
+    """The ids generate_sequence* feeds (lib.rs:6563-6567): encode, drop the
+    trailing <eos>, [0] if nothing is left."""
+    t = list(Tokenizer.encode(prompt)[:-1])
+    return np.asarray(t or [0], np.int32)
+
+
+def generate_sequence(prompt, decoder, temperature=0.0, max_new_tokens=None, seed=0, slot=0):
+    """generate_sequence / _q8 / _q4 (lib.rs:6538-6827) on the GPU decoder."""
+    toks, pre, gen = decoder.generate([prompt_tokens(prompt)], temperature, max_new_tokens, [seed], [slot],
+                                      decoder.model.cfg.max_seq_len)
+    suffix = "".join(c for c in (Tokenizer.decode(t) for t in toks[0]) if c is not None)
+    return GenerationMetrics(prompt + suffix, suffix, int(toks[0].size), pre, gen)

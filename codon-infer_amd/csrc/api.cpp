@@ -103,15 +103,55 @@ bool use_gemv(int M, int a_fmt, int epi) {
            epi != EPI_GELU_H2;
 }
 
-hipError_t gemm(cih_model *m, const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
-                int M, int epi) {
+}  // namespace
+
+namespace cih {
+
+hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, const void *X, int ldx, int a_fmt,
+                      const float *bias, void *Y, int ldy, int M, int epi) {
     const double flops = 2.0 * M * W.N * W.K;
     const double in_b = a_fmt == AF_X3 ? 6.0 : 4.0, out_b = epi == EPI_GELU_X3 ? 6.0 : 4.0;  // H2: 4 B/element
     const double bytes = wbytes(W) + in_b * M * W.K + out_b * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
     ProfScope ps(m, W.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, flops, bytes);
     if (use_gemv(M, a_fmt, epi))
-        return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, m->ws.part, m->stream);
-    return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, &m->ws.part, m->stream);
+        return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, pb, m->stream);
+    return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, &pb, m->stream);
+}
+
+size_t model_part_floats(const cih_model *m) {
+    size_t pf = 0;
+    std::vector<const DevMatrix *> mats = {&m->emb};
+    if (m->has_head) mats.insert(mats.end(), {&m->dense, &m->dec});
+    if (!m->layers.empty()) {
+        const Layer &ly = m->layers[0];
+        mats.insert(mats.end(), {&ly.wqkv, &ly.wo, &ly.w1, &ly.w2});
+    }
+    for (const DevMatrix *w : mats) pf = std::max(pf, gemv_part_floats(w->N, w->K));
+    return std::max(pf, SPLITK_PART_FLOATS);
+}
+
+// RoPE tables (BidirectionalRunState::new / RunState::new, lib.rs:2513-2522,
+// 2466-2474): the same f32 powf / cos / sin calls, evaluated on the host.
+void rope_tables_host(size_t max_len, int hd, std::vector<float> &c, std::vector<float> &s) {
+    const size_t half = hd / 2;
+    c.assign(max_len * half, 0.0f);
+    s.assign(max_len * half, 0.0f);
+    for (size_t pos = 0; pos < max_len; pos++)
+        for (size_t j = 0; j < half; j++) {
+            const float freq = 1.0f / std::pow(10000.0f, (float)(j * 2) / (float)hd);
+            const float val = (float)pos * freq;
+            c[pos * half + j] = std::cos(val);
+            s[pos * half + j] = std::sin(val);
+        }
+}
+
+}  // namespace cih
+
+namespace {
+
+hipError_t gemm(cih_model *m, const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
+                int M, int epi) {
+    return model_gemm(m, m->ws.part, W, X, ldx, a_fmt, bias, Y, ldy, M, epi);
 }
 
 }  // namespace
@@ -169,15 +209,7 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
                 ok(dalloc(ws.logits, T * V, dl)) && ok(dalloc(ws.rope_c, S * half, dl)) &&
                 ok(dalloc(ws.rope_s, S * half, dl));
     if (good) {
-        size_t pf = 0;
-        std::vector<const DevMatrix *> mats = {&m->emb};
-        if (m->has_head) mats.insert(mats.end(), {&m->dense, &m->dec});
-        if (!m->layers.empty()) {
-            const Layer &ly = m->layers[0];
-            mats.insert(mats.end(), {&ly.wqkv, &ly.wo, &ly.w1, &ly.w2});
-        }
-        for (const DevMatrix *w : mats) pf = std::max(pf, gemv_part_floats(w->N, w->K));
-        ws.part.floats = std::max(pf, SPLITK_PART_FLOATS);
+        ws.part.floats = model_part_floats(m);
         const size_t nd = std::max(B, S);
         good = ok(dalloc(ws.part.part, ws.part.floats, dl)) && ok(dalloc(ws.dms_meta, nd * 2, dl)) &&
                ok(dalloc(ws.dms_out, nd * 21, dl));
@@ -205,16 +237,8 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
         free_workspace(ws);
         return CIH_ERR_HIP;
     }
-    // RoPE tables (BidirectionalRunState::new, lib.rs:2513-2522): the same f32
-    // powf / cos / sin calls, evaluated on the host.
-    std::vector<float> c(S * half), s(S * half);
-    for (size_t pos = 0; pos < S; pos++)
-        for (size_t j = 0; j < half; j++) {
-            const float freq = 1.0f / std::pow(10000.0f, (float)(j * 2) / (float)m->hd);
-            const float val = (float)pos * freq;
-            c[pos * half + j] = std::cos(val);
-            s[pos * half + j] = std::sin(val);
-        }
+    std::vector<float> c, s;
+    rope_tables_host(S, m->hd, c, s);
     HIPCHK(hipMemcpy(ws.rope_c, c.data(), c.size() * 4, hipMemcpyHostToDevice));
     HIPCHK(hipMemcpy(ws.rope_s, s.data(), s.size() * 4, hipMemcpyHostToDevice));
     return CIH_OK;

@@ -1,0 +1,313 @@
+// Autoregressive decoding on the device-resident model: RunState with its
+// KV cache (src/lib.rs:2459-2486), forward / forward_q8 / forward_q4 for a
+// batch of rows (3554-4233), SimpleRng + sample (3506-3530) and the
+// generate_sequence* loop (6538-6827).
+//
+// A decoder owns n_slots independent KV caches.  One decode call runs any
+// number of rows, each (slot, token, position): the weights are read once
+// for all rows (the GEMV for up to 8 rows, the MFMA GEMM above), so
+// independent sequences decode together and a prompt prefills in one call.
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+
+#include "model.h"
+
+struct cih_decoder {
+    cih_model *m = nullptr;
+    int slots = 0, max_len = 0, max_rows = 0;
+    int64_t slot_stride = 0;  // floats between slots in one layer's cache
+    float *kc = nullptr, *vc = nullptr;  // [L][slots][max_len][d]
+    float *rope_c = nullptr, *rope_s = nullptr;
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *ao = nullptr, *h = nullptr, *logits = nullptr;
+    int *d_tokens = nullptr, *d_rows = nullptr, *d_cu = nullptr, *d_lens = nullptr;
+    int *h_meta = nullptr;  // pinned: tokens[max_rows] | rows[max_rows][2]
+    cih::PartialBuf part;
+    std::vector<int> filled;  // positions written per slot (0..filled-1 valid)
+    std::vector<void *> allocs;
+};
+
+using namespace cih;
+
+namespace {
+
+void destroy(cih_decoder *dc) {
+    if (!dc) return;
+    if (dc->m && dc->m->stream) hipStreamSynchronize(dc->m->stream);
+    free_list(dc->allocs);
+    if (dc->h_meta) hipHostFree(dc->h_meta);
+    delete dc;
+}
+
+// The rows' forward: embedding (constant 0.88 scale, <mask> -> 0), the
+// layers with cached causal attention, final LN and LM head -> dc->logits.
+int run_rows(cih_decoder *dc, int n) {
+    cih_model *m = dc->m;
+    const int d = m->cfg.dim, F = m->cfg.hidden_dim, V = m->cfg.vocab_size, H = m->cfg.n_heads, L = m->cfg.n_layers;
+    hipStream_t st = m->stream;
+    HIPCHK(hipMemcpyAsync(dc->d_tokens, dc->h_meta, (size_t)n * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(dc->d_rows, dc->h_meta + dc->max_rows, (size_t)n * 8, hipMemcpyHostToDevice, st));
+    // forward_* embedding (lib.rs:3567-3575, 3753-3765): every row is a
+    // one-token sequence, for which the token-dropout scale is 0.88 exactly
+    HIPCHK(launch_embed(dc->d_tokens, SeqMeta{dc->d_cu, dc->d_lens, n, 1}, m->emb.fmt, m->emb.q, m->emb.sc, d, V,
+                        dc->x, st));
+    const int64_t layer = (int64_t)dc->slots * dc->slot_stride;
+    for (int l = 0; l < L; l++) {
+        const Layer &ly = m->layers[l];
+        HIPCHK(launch_layernorm(dc->x, ly.ln1w, ly.ln1b, dc->xb, AF_F32, n, d, st));
+        HIPCHK(model_gemm(m, dc->part, ly.wqkv, dc->xb, d, AF_F32, ly.bqkv, dc->qkv, 3 * d, n, EPI_NONE));
+        float *kc = dc->kc + l * layer, *vc = dc->vc + l * layer;
+        HIPCHK(launch_rope_kv(dc->qkv, d, m->hd, dc->d_rows, n, dc->rope_c, dc->rope_s, kc, vc, dc->slot_stride, st));
+        HIPCHK(launch_decode_attention(dc->qkv, d, H, dc->d_rows, n, dc->max_len, kc, vc, dc->slot_stride, dc->ao, st));
+        HIPCHK(model_gemm(m, dc->part, ly.wo, dc->ao, d, AF_F32, ly.bo, dc->x, d, n, EPI_RESIDUAL));
+        HIPCHK(launch_layernorm(dc->x, ly.ln2w, ly.ln2b, dc->xb, AF_F32, n, d, st));
+        HIPCHK(model_gemm(m, dc->part, ly.w1, dc->xb, d, AF_F32, ly.b1, dc->h, F, n, EPI_GELU));
+        HIPCHK(model_gemm(m, dc->part, ly.w2, dc->h, F, AF_F32, ly.b2, dc->x, d, n, EPI_RESIDUAL));
+    }
+    HIPCHK(launch_layernorm(dc->x, m->lnfw, m->lnfb, dc->ao, AF_F32, n, d, st));
+    // project_lm_head_* (lib.rs:3952-4015): dense + GELU, LN, decoder; or the
+    // tied embedding without bias
+    if (m->has_head) {
+        HIPCHK(model_gemm(m, dc->part, m->dense, dc->ao, d, AF_F32, m->dense_b, dc->h, d, n, EPI_GELU));
+        HIPCHK(launch_layernorm(dc->h, m->lm_lnw, m->lm_lnb, dc->xb, AF_F32, n, d, st));
+        HIPCHK(model_gemm(m, dc->part, m->dec, dc->xb, d, AF_F32, m->dec_b, dc->logits, V, n, EPI_NONE));
+    } else {
+        HIPCHK(model_gemm(m, dc->part, m->emb, dc->ao, d, AF_F32, nullptr, dc->logits, V, n, EPI_NONE));
+    }
+    return 0;
+}
+
+// Validates rows and stages them; rows of one slot must continue its
+// cache: consecutive positions starting at most at the slot's filled count.
+int stage_rows(cih_decoder *dc, const int32_t *slots, const int32_t *tokens, const int32_t *pos, int n) {
+    const int V = dc->m->cfg.vocab_size;
+    if (n < 1 || n > dc->max_rows) return set_error(CIH_ERR_CAPACITY, "%d rows outside [1, %d]", n, dc->max_rows);
+    std::map<int, int> next;  // slot -> next position this call may write
+    for (int i = 0; i < n; i++) {
+        const int s = slots[i], p = pos[i], t = tokens[i];
+        if (s < 0 || s >= dc->slots) return set_error(CIH_ERR_ARG, "row %d: slot %d outside [0, %d)", i, s, dc->slots);
+        if (t < 0 || t >= V) return set_error(CIH_ERR_TOKEN, "row %d: token %d outside [0, %d)", i, t, V);
+        if (p < 0 || p >= dc->max_len)
+            return set_error(CIH_ERR_CAPACITY, "row %d: position %d outside [0, %d)", i, p, dc->max_len);
+        auto it = next.find(s);
+        const int allowed = it == next.end() ? dc->filled[s] : it->second;
+        if (it == next.end() ? p > allowed : p != allowed)
+            return set_error(CIH_ERR_ARG, "row %d: slot %d position %d does not continue its cache (next %d)", i, s, p,
+                             allowed);
+        next[s] = p + 1;
+        dc->h_meta[i] = t;
+        dc->h_meta[dc->max_rows + 2 * i] = s;
+        dc->h_meta[dc->max_rows + 2 * i + 1] = p;
+    }
+    for (auto &kv : next) dc->filled[kv.first] = std::max(dc->filled[kv.first], kv.second);
+    return 0;
+}
+
+// SimpleRng (lib.rs:3506-3511): xorshift64 (13, 7, 17); seed 0 is replaced.
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed == 0 ? 0x123456789abcdefULL : seed) {}
+    uint32_t next_u32() {
+        uint64_t x = s;
+        x ^= x << 13;
+        x ^= x >> 7;
+        x ^= x << 17;
+        s = x;
+        return (uint32_t)x;
+    }
+    float next_f32() { return (float)next_u32() / (float)UINT32_MAX; }
+};
+
+// sample (lib.rs:3513-3530): ids 4..=23 and <eos> only; argmax for T <= 0,
+// else softmax(logits / T) and the first id whose running sum reaches r.
+int sample(float *lg, int V, float temperature, Rng &rng) {
+    for (int i = 0; i < V; i++)
+        if (!((i >= 4 && i <= 23) || i == 2)) lg[i] = -INFINITY;
+    if (temperature <= 0.0f) {
+        float mv = lg[0];
+        int mi = 0;
+        for (int i = 1; i < V; i++)
+            if (lg[i] > mv) { mv = lg[i]; mi = i; }
+        return mi;
+    }
+    const float inv_temp = 1.0f / temperature;
+    for (int i = 0; i < V; i++)
+        if (lg[i] != -INFINITY) lg[i] *= inv_temp;
+    float mx = -INFINITY;
+    for (int i = 0; i < V; i++) mx = std::fmax(mx, lg[i]);
+    float sum = 0.0f;
+    for (int i = 0; i < V; i++) { lg[i] = std::exp(lg[i] - mx); sum += lg[i]; }
+    const float inv = 1.0f / sum;
+    for (int i = 0; i < V; i++) lg[i] *= inv;
+    const float r = rng.next_f32();
+    float cum = 0.0f;
+    for (int i = 0; i < V; i++) {
+        if (std::isnan(lg[i]) || lg[i] == 0.0f) continue;
+        cum += lg[i];
+        if (r <= cum) return i;
+    }
+    return 4;
+}
+
+double ms_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+}  // namespace
+
+extern "C" {
+
+int cih_decoder_create(cih_model *m, int32_t n_slots, int32_t max_len, int32_t max_rows, cih_decoder **out) {
+    if (!m || !out) return set_error(CIH_ERR_ARG, "null argument");
+    *out = nullptr;
+    if (n_slots < 1 || max_len < 1 || max_rows < 1) return set_error(CIH_ERR_ARG, "n_slots, max_len, max_rows must be >= 1");
+    if (max_len > 16000) return set_error(CIH_ERR_SHAPE, "max_len %d above the attention kernel's 16000", max_len);
+    const size_t d = m->cfg.dim, F = m->cfg.hidden_dim, V = m->cfg.vocab_size, L = m->cfg.n_layers;
+    const size_t R = max_rows;
+    cih_decoder *dc = new cih_decoder();
+    dc->m = m;
+    dc->slots = n_slots;
+    dc->max_len = max_len;
+    dc->max_rows = max_rows;
+    dc->slot_stride = (int64_t)max_len * d;
+    dc->filled.assign(n_slots, 0);
+    auto &al = dc->allocs;
+    const size_t cache = L * n_slots * (size_t)max_len * d;
+    bool good = dalloc(dc->kc, cache, al) == hipSuccess && dalloc(dc->vc, cache, al) == hipSuccess &&
+                dalloc(dc->rope_c, (size_t)max_len * (m->hd / 2), al) == hipSuccess &&
+                dalloc(dc->rope_s, (size_t)max_len * (m->hd / 2), al) == hipSuccess &&
+                dalloc(dc->x, R * d, al) == hipSuccess && dalloc(dc->xb, R * d, al) == hipSuccess &&
+                dalloc(dc->qkv, R * 3 * d, al) == hipSuccess && dalloc(dc->ao, R * d, al) == hipSuccess &&
+                dalloc(dc->h, R * std::max(F, d), al) == hipSuccess && dalloc(dc->logits, R * V, al) == hipSuccess &&
+                dalloc(dc->d_tokens, R, al) == hipSuccess && dalloc(dc->d_rows, 2 * R, al) == hipSuccess &&
+                dalloc(dc->d_cu, R, al) == hipSuccess && dalloc(dc->d_lens, R, al) == hipSuccess;
+    dc->part.floats = model_part_floats(m);
+    good = good && dalloc(dc->part.part, dc->part.floats, al) == hipSuccess &&
+           hipHostMalloc((void **)&dc->h_meta, 3 * R * sizeof(int)) == hipSuccess;
+    if (!good) {
+        destroy(dc);
+        return set_error(CIH_ERR_HIP, "decoder allocation failed (%zu MiB of KV cache)", 2 * cache * 4 >> 20);
+    }
+    std::vector<float> c, s;
+    rope_tables_host(max_len, m->hd, c, s);
+    std::vector<int> cu(R), lens(R, 1);
+    for (size_t i = 0; i < R; i++) cu[i] = (int)i;
+    hipError_t e = hipMemcpy(dc->rope_c, c.data(), c.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dc->rope_s, s.data(), s.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dc->d_cu, cu.data(), R * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dc->d_lens, lens.data(), R * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        destroy(dc);
+        return set_error(CIH_ERR_HIP, "decoder set-up failed: %s", hipGetErrorString(e));
+    }
+    *out = dc;
+    return CIH_OK;
+}
+
+int cih_decoder_destroy(cih_decoder *dc) {
+    destroy(dc);
+    return CIH_OK;
+}
+
+int cih_decoder_reset(cih_decoder *dc, int32_t slot) {
+    if (!dc) return set_error(CIH_ERR_ARG, "null decoder");
+    if (slot < 0) std::fill(dc->filled.begin(), dc->filled.end(), 0);
+    else if (slot < dc->slots) dc->filled[slot] = 0;
+    else return set_error(CIH_ERR_ARG, "slot %d outside [0, %d)", slot, dc->slots);
+    return CIH_OK;
+}
+
+int cih_decode(cih_decoder *dc, const int32_t *slots, const int32_t *tokens, const int32_t *pos, int32_t n,
+               float *logits) {
+    if (!dc || !slots || !tokens || !pos) return set_error(CIH_ERR_ARG, "null argument");
+    if (int rc = stage_rows(dc, slots, tokens, pos, n)) return rc;
+    if (int rc = run_rows(dc, n)) return rc;
+    if (logits)
+        HIPCHK(hipMemcpyAsync(logits, dc->logits, (size_t)n * dc->m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
+                              dc->m->stream));
+    HIPCHK(hipStreamSynchronize(dc->m->stream));
+    return CIH_OK;
+}
+
+int cih_generate(cih_decoder *dc, int32_t n, const int32_t *slots, const int32_t *prompts, const int32_t *offsets,
+                 float temperature, int32_t max_new_tokens, const uint64_t *seeds, int32_t max_seq_len,
+                 int32_t *out_tokens, int32_t out_cap, int32_t *n_generated, double *prefill_ms,
+                 double *generation_ms) {
+    if (!dc || !slots || !prompts || !offsets || !seeds || !out_tokens || !n_generated)
+        return set_error(CIH_ERR_ARG, "null argument");
+    if (n < 1) return set_error(CIH_ERR_ARG, "n must be >= 1");
+    const int V = dc->m->cfg.vocab_size;
+    const int msl = max_seq_len > 0 ? std::min(max_seq_len, dc->max_len) : dc->max_len;
+    std::vector<int> pos(n, 0), limit(n), count(n, 0);
+    std::vector<char> seen(dc->slots, 0);
+    for (int i = 0; i < n; i++) {
+        if (slots[i] < 0 || slots[i] >= dc->slots) return set_error(CIH_ERR_ARG, "slot %d out of range", slots[i]);
+        if (seen[slots[i]]++) return set_error(CIH_ERR_ARG, "slot %d used by two streams", slots[i]);
+        if (offsets[i + 1] < offsets[i]) return set_error(CIH_ERR_ARG, "offsets must not decrease");
+        for (int k = offsets[i]; k < offsets[i + 1]; k++)
+            if (prompts[k] < 0 || prompts[k] >= V) return set_error(CIH_ERR_TOKEN, "prompt token %d out of range", prompts[k]);
+        pos[i] = std::min(offsets[i + 1] - offsets[i], msl);
+        limit[i] = max_new_tokens >= 0 ? std::min(pos[i] + max_new_tokens, msl) : msl;
+        if (limit[i] - pos[i] > out_cap)
+            return set_error(CIH_ERR_CAPACITY, "stream %d may generate %d tokens, out_cap is %d", i, limit[i] - pos[i],
+                             out_cap);
+    }
+    std::vector<float> lg((size_t)n * V);
+    // prefill: each stream's prompt through the model, one call per stream
+    // (chunks of max_rows positions), so a stream's cache does not depend on
+    // which other streams run with it
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < n; i++) {
+        dc->filled[slots[i]] = 0;
+        for (int p0 = 0; p0 < pos[i]; p0 += dc->max_rows) {
+            const int k = std::min(dc->max_rows, pos[i] - p0);
+            std::vector<int32_t> sl(k, slots[i]), tk(prompts + offsets[i] + p0, prompts + offsets[i] + p0 + k), ps(k);
+            for (int j = 0; j < k; j++) ps[j] = p0 + j;
+            if (int rc = stage_rows(dc, sl.data(), tk.data(), ps.data(), k)) return rc;
+            if (int rc = run_rows(dc, k)) return rc;
+            if (p0 + k == pos[i])
+                HIPCHK(hipMemcpyAsync(&lg[(size_t)i * V], dc->logits + (size_t)(k - 1) * V, V * 4,
+                                      hipMemcpyDeviceToHost, dc->m->stream));
+        }
+    }
+    HIPCHK(hipStreamSynchronize(dc->m->stream));
+    const double t_prefill = ms_since(t0);
+    // generation: every live stream samples from its last logits and feeds the
+    // token back at its next position; all live streams share one call
+    const auto t1 = std::chrono::steady_clock::now();
+    std::vector<Rng> rng;
+    for (int i = 0; i < n; i++) rng.emplace_back(seeds[i]);
+    std::vector<char> live(n, 1);
+    std::vector<int> idx;
+    std::vector<int32_t> sl, tk, ps;
+    std::vector<float> tmp(V);
+    for (;;) {
+        idx.clear(); sl.clear(); tk.clear(); ps.clear();
+        for (int i = 0; i < n; i++) {
+            if (!live[i]) continue;
+            if (pos[i] >= limit[i]) { live[i] = 0; continue; }
+            std::memcpy(tmp.data(), &lg[(size_t)i * V], V * 4);
+            const int t = sample(tmp.data(), V, temperature, rng[i]);
+            if (t == 2) { live[i] = 0; continue; }
+            out_tokens[(size_t)i * out_cap + count[i]++] = t;
+            idx.push_back(i); sl.push_back(slots[i]); tk.push_back(t); ps.push_back(pos[i]++);
+        }
+        if (idx.empty()) break;
+        for (size_t j0 = 0; j0 < idx.size(); j0 += dc->max_rows) {
+            const int k = (int)std::min<size_t>(dc->max_rows, idx.size() - j0);
+            if (int rc = stage_rows(dc, &sl[j0], &tk[j0], &ps[j0], k)) return rc;
+            if (int rc = run_rows(dc, k)) return rc;
+            for (int j = 0; j < k; j++)
+                HIPCHK(hipMemcpyAsync(&lg[(size_t)idx[j0 + j] * V], dc->logits + (size_t)j * V, V * 4,
+                                      hipMemcpyDeviceToHost, dc->m->stream));
+            HIPCHK(hipStreamSynchronize(dc->m->stream));
+        }
+    }
+    for (int i = 0; i < n; i++) n_generated[i] = count[i];
+    if (prefill_ms) *prefill_ms = t_prefill;
+    if (generation_ms) *generation_ms = ms_since(t1);
+    return CIH_OK;
+}
+
+}  // extern "C"

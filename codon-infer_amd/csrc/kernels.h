@@ -133,6 +133,20 @@ hipError_t launch_apc_finalize(const float *M, const float *r, float *coef, cons
 // deltas in CANONICAL_AAS order and out[i][20] = entropy.
 hipError_t launch_dms_score(const float *logits, int V, const int *meta, int count, float *out, hipStream_t st);
 
+// Autoregressive decoding.  rows: [n][2] = (cache slot, position) per row of
+// qkv [n][3d]; the K/V cache holds [slot][max_len][d] floats per layer
+// (slot_stride floats between slots).  launch_rope_kv rotates Q in place
+// and writes the rotated K and V at the row's position; afterwards
+// launch_decode_attention writes out[n][d] = causal attention of each row
+// over its slot's positions 0..pos.  A row may read positions written by
+// other rows of the same launch pair.
+hipError_t launch_rope_kv(float *qkv, int d, int hd, const int *rows, int n, const float *rope_c, const float *rope_s,
+                          float *kc, float *vc, int64_t slot_stride, hipStream_t st);
+hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *rows, int n, int max_len,
+                                   const float *kc, const float *vc, int64_t slot_stride, float *out,
+                                   hipStream_t st);
+size_t decode_attention_lds(int hd, int max_len);  // dynamic LDS bytes per workgroup
+
 // Copies packed rows [T][width] into padded [B][S_max][width] (valid rows only).
 hipError_t launch_scatter_rows(const float *src, int width, SeqMeta sm, float *dst, int64_t dst_b_stride,
                                hipStream_t st);

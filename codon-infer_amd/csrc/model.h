@@ -99,6 +99,15 @@ int upload(cih_model *m, T *&dst, const T *src, size_t n) {
 void free_list(std::vector<void *> &l);
 int check_config(const cih_config *c);
 
+// Y = epi(X W^T + bias) on the model's stream: the weight-streaming GEMV for
+// a few FP32 rows, the MFMA GEMM otherwise; partial sums through pb.
+hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, const void *X, int ldx, int a_fmt,
+                      const float *bias, void *Y, int ldy, int M, int epi);
+// partial-sum floats any GEMM / GEMV of the model needs
+size_t model_part_floats(const cih_model *m);
+// RoPE cos / sin tables [max_len][hd/2] as the reference computes them
+void rope_tables_host(size_t max_len, int hd, std::vector<float> &c, std::vector<float> &s);
+
 // One [N][K] host matrix (FP32 values or reference row-major blocks) that
 // becomes rows [n_off, n_off + N) of a device matrix.
 struct Part {

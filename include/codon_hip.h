@@ -139,6 +139,48 @@ int cih_model_destroy(cih_model *m);
 int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B,
                 int32_t S_max, uint32_t flags, const cih_outputs *out);
 
+/* ---- autoregressive decoding --------------------------------------------- */
+
+typedef struct cih_decoder cih_decoder;
+
+/* Replaces RunState::new (lib.rs:2464-2486) for n_slots independent
+ * sequences: a K and a V cache of [n_layers][n_slots][max_len][dim] floats
+ * on the device, RoPE tables for max_len positions, and row buffers for up
+ * to max_rows rows per cih_decode call.  max_len <= 16000. */
+int cih_decoder_create(cih_model *m, int32_t n_slots, int32_t max_len, int32_t max_rows,
+                       cih_decoder **out);
+int cih_decoder_destroy(cih_decoder *d);
+/* Forgets a slot's cache contents (slot < 0: every slot). */
+int cih_decoder_reset(cih_decoder *d, int32_t slot);
+
+/* Replaces forward / forward_parallel / forward_q8 / forward_q4
+ * (lib.rs:3554, 3558, 3741, 4016) for n rows at once: row i feeds
+ * tokens[i] at position pos[i] of slot slots[i] (its K and V are written to
+ * the cache there, then it attends to the slot's positions 0..pos[i]).
+ * The rows of one slot must be consecutive positions starting at most at the
+ * slot's first unwritten position (a prompt can prefill in one call;
+ * rewriting earlier positions is allowed, as in the reference).  logits:
+ * host [n][vocab] (may be NULL).  Synchronous. */
+int cih_decode(cih_decoder *d, const int32_t *slots, const int32_t *tokens, const int32_t *pos,
+               int32_t n, float *logits);
+
+/* Replaces generate_sequence / _parallel / _q8 / _q4 (lib.rs:6538-6827) for
+ * n independent streams.  Stream i uses slot slots[i] and the prompt ids
+ * prompts[offsets[i] .. offsets[i+1]) (Tokenizer::encode of the prompt
+ * without its trailing <eos>, as the reference feeds it), its own SimpleRng
+ * seed seeds[i], a shared temperature (<= 0: greedy) and max_new_tokens
+ * (< 0: none).  max_seq_len (<= 0: the decoder's max_len) caps positions as
+ * config.max_seq_len does.  Each stream's prompt is prefilled in its own
+ * calls; then all live streams decode together, one token each per step, each
+ * stopping at <eos> (2) or its limit.  out_tokens: [n][out_cap] generated
+ * ids; n_generated[i] their counts; prefill_ms / generation_ms (may be NULL)
+ * the wall times of the two phases.  A stream's tokens do not depend on the
+ * other streams while at most 8 streams decode together. */
+int cih_generate(cih_decoder *d, int32_t n, const int32_t *slots, const int32_t *prompts,
+                 const int32_t *offsets, float temperature, int32_t max_new_tokens,
+                 const uint64_t *seeds, int32_t max_seq_len, int32_t *out_tokens, int32_t out_cap,
+                 int32_t *n_generated, double *prefill_ms, double *generation_ms);
+
 /* ---- in-silico deep mutational scan -------------------------------------- */
 
 enum cih_dms_mode { CIH_DMS_MASKED_MARGINAL = 0, CIH_DMS_WILDTYPE_MARGINAL = 1 };
