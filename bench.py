@@ -165,6 +165,86 @@ def load_bench(args, ch):
     print(json.dumps(line), flush=True)
 
 
+def decode_bench(args, ch):
+    """Autoregressive decoding (forward_q8 / forward_q4 with the KV cache,
+    lib.rs:3741-4233) of --streams independent sequences: each gets a
+    16-token prompt (prefilled in one call), then every step feeds one token
+    per stream at its next position — the greedy choice among the ids
+    sample() allows, <eos> excluded so every step does the same work.
+    --warmup untimed steps, then --new-tokens timed steps; value = generated
+    tokens per second over all streams."""
+    cfg = ch.EsmConfig.by_name(args.model)
+    seeds = {"8M": 8, "35M": 35, "150M": 150, "650M": 650, "3B": 3000}
+    t0 = time.perf_counter()
+    w = ch.EsmWeights.random(cfg, seed=seeds[args.model], bias_std=0.02)
+    w = w.quantize_q8() if args.dtype == "q8" else (w.quantize_q4() if args.dtype == "q4" else w)
+    n, P, K = args.streams, 16, args.new_tokens
+    model = ch.GpuModel(cfg, w, max_batch=1, max_len=16)
+    dec = ch.GpuDecoder(model, n_slots=n, max_len=cfg.max_seq_len, max_rows=max(16, n))
+    assert P + args.warmup + K <= cfg.max_seq_len
+    rng = np.random.default_rng(7)
+    allowed = np.arange(4, 24)
+    last = []
+    for s in range(n):
+        pr = np.concatenate([[0], 4 + rng.integers(0, 20, P - 1)]).astype(np.int32)
+        last.append(dec.decode(np.full(P, s), pr, np.arange(P))[-1])
+    print(f"[bench] decode model + prefill ready ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+    slots = np.arange(n, dtype=np.int32)
+    state = {"pos": P, "logits": np.stack(last)}
+
+    def step():
+        toks = allowed[np.argmax(state["logits"][:, allowed], axis=1)].astype(np.int32)
+        state["logits"] = dec.decode(slots, toks, np.full(n, state["pos"], np.int32))
+        state["pos"] += 1
+
+    for _ in range(args.warmup):
+        step()
+    model.profile(True)
+    t1 = time.perf_counter()
+    for _ in range(K):
+        step()
+    el = time.perf_counter() - t1
+    model.profile(False)
+    q = model.profile_read(ch.KC_GEMM_QUANT if args.dtype != "fp32" else ch.KC_GEMM_FP32)
+    a = model.profile_read(ch.KC_ATTENTION)
+    o = model.profile_read(ch.KC_OTHER)
+    f = model.profile_read(ch.KC_GEMM_FP32) if args.dtype != "fp32" else {"total_ms": 0.0, "bytes": 0.0}
+    gbs = q["bytes"] / (q["total_ms"] * 1e-3) / 1e9 if q["total_ms"] > 0 else 0.0
+    step_bytes = (q["bytes"] + a["bytes"] + o["bytes"] + f["bytes"]) / K
+    ms = el * 1e3 / K
+    line = {
+        "metric": f"decode tokens/s ESM-2 {args.model} {args.dtype} ({n} stream{'s' if n > 1 else ''})",
+        "value": round(n * K / el, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"ESM-2 {args.model} {args.dtype} autoregressive decode, {n} stream(s), 16-token "
+                               f"prompts, positions {P + args.warmup}..{P + args.warmup + K - 1}, seeded weights",
+                   "streams": n, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "k_gemv (weights streamed once per step for all streams)",
+                     "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "timing": TIMING},
+        "step_breakdown_ms": {"gemv": round(q["total_ms"] / K, 4), "attention": round(a["total_ms"] / K, 4),
+                              "other": round(o["total_ms"] / K, 4), "lm_head_fp32": round(f["total_ms"] / K, 4)},
+        "step_bytes": round(step_bytes), "step_GB_per_s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import cpu_ref as cr
+        threads = max(1, min(16, physical_cores(), os.cpu_count() or 1))
+        rs = cr.RunState(cfg, w, max_len=cfg.max_seq_len, num_threads=threads)
+        done, tc = 0, time.perf_counter()
+        while time.perf_counter() - tc < args.cpu_budget and done < P + K:
+            rs.step(4 + done % 20, done)
+            done += 1
+        ec = time.perf_counter() - tc
+        line["cpu_baseline"] = {"value": done / ec, "unit": "tokens/s", "cores": threads, "kind": "port",
+                                "sample": f"{done} one-token steps of one stream (positions 0..{done - 1}), "
+                                          f"{threads} threads, {ec:.1f} s"}
+    dec.close()
+    model.close()
+    print(json.dumps(line), flush=True)
+
+
 def dms_bench(args, ch):
     """ESM-2 650M Q8_0 in-silico DMS: a seeded 400-residue protein, every
     position masked in turn (400 copies of L=402) in chunks of 32, scored on
@@ -245,9 +325,12 @@ def main():
                     help="residues per sequence uniform in [LO, HI] (padded to --seq-len)")
     ap.add_argument("--outputs", choices=["logits", "contacts", "maps", "maps+contacts"], default="logits",
                     help="contacts: + contact probabilities; maps: + every layer's attention maps")
-    ap.add_argument("--workload", choices=["forward", "dms", "load"], default="forward",
+    ap.add_argument("--workload", choices=["forward", "dms", "load", "decode"], default="forward",
                     help="forward: batched forward (the headline); dms: in-silico deep mutational scan of a "
-                         "400-residue protein (400 masked copies, L=402, chunks of 32)")
+                         "400-residue protein (400 masked copies, L=402, chunks of 32); load: CODQ file -> device; "
+                         "decode: autoregressive decoding with the KV cache")
+    ap.add_argument("--streams", type=int, default=1, help="decode: independent sequences decoded together")
+    ap.add_argument("--new-tokens", type=int, default=256, help="decode: timed steps (tokens per stream)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="issue one device-to-device copy of this many MiB first (a known-size kernel that "
                          "calibrates FETCH_SIZE / WRITE_SIZE counter runs)")
@@ -263,6 +346,8 @@ def main():
         return dms_bench(args, ch)
     if args.workload == "load":
         return load_bench(args, ch)
+    if args.workload == "decode":
+        return decode_bench(args, ch)
     B, S = args.batch, args.seq_len
     cfg = ch.EsmConfig.by_name(args.model)
     headline = (args.model, args.dtype, args.ragged, args.outputs) == ("650M", "q8", None, "logits")

@@ -65,31 +65,6 @@ void free_workspace(Workspace &ws) {
     ws = Workspace();
 }
 
-struct ProfScope {
-    cih_model *m;
-    int idx = -1;
-    ProfScope(cih_model *m_, int cls, double flops, double bytes) : m(m_) {
-        Prof &p = m->prof;
-        if (!p.on) return;
-        if (p.used >= p.cls.size()) {
-            hipEvent_t a, b;
-            if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return;
-            p.ev.push_back(a);
-            p.ev.push_back(b);
-            p.cls.push_back(0);
-            p.flops.push_back(0);
-            p.bytes.push_back(0);
-        }
-        idx = (int)p.used++;
-        p.cls[idx] = cls;
-        p.flops[idx] = flops;
-        p.bytes[idx] = bytes;
-        hipEventRecord(p.ev[2 * idx], m->stream);
-    }
-    ~ProfScope() {
-        if (idx >= 0) hipEventRecord(m->prof.ev[2 * idx + 1], m->stream);
-    }
-};
 
 double wbytes(const DevMatrix &W) {
     const double e = (double)W.N * W.K;
@@ -116,6 +91,21 @@ hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, co
     if (use_gemv(M, a_fmt, epi))
         return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, pb, m->stream);
     return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, &pb, m->stream);
+}
+
+void profile_collect(cih_model *m) {
+    if (m->prof.on) {
+        for (size_t i = 0; i < m->prof.used; i++) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, m->prof.ev[2 * i], m->prof.ev[2 * i + 1]) != hipSuccess) continue;
+            cih_kernel_stats &s = m->prof.st[m->prof.cls[i]];
+            s.launches++;
+            s.total_ms += ms;
+            s.flops += m->prof.flops[i];
+            s.bytes += m->prof.bytes[i];
+        }
+    }
+    m->prof.used = 0;
 }
 
 size_t model_part_floats(const cih_model *m) {
@@ -430,17 +420,7 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             }
         }
     }
-    if (m->prof.on) {
-        for (size_t i = 0; i < m->prof.used; i++) {
-            float ms = 0.0f;
-            if (hipEventElapsedTime(&ms, m->prof.ev[2 * i], m->prof.ev[2 * i + 1]) != hipSuccess) continue;
-            cih_kernel_stats &s = m->prof.st[m->prof.cls[i]];
-            s.launches++;
-            s.total_ms += ms;
-            s.flops += m->prof.flops[i];
-            s.bytes += m->prof.bytes[i];
-        }
-    }
+    profile_collect(m);
     return CIH_OK;
 }
 

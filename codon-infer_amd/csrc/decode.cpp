@@ -50,27 +50,51 @@ int run_rows(cih_decoder *dc, int n) {
     HIPCHK(hipMemcpyAsync(dc->d_rows, dc->h_meta + dc->max_rows, (size_t)n * 8, hipMemcpyHostToDevice, st));
     // forward_* embedding (lib.rs:3567-3575, 3753-3765): every row is a
     // one-token sequence, for which the token-dropout scale is 0.88 exactly
-    HIPCHK(launch_embed(dc->d_tokens, SeqMeta{dc->d_cu, dc->d_lens, n, 1}, m->emb.fmt, m->emb.q, m->emb.sc, d, V,
-                        dc->x, st));
+    {
+        ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
+        HIPCHK(launch_embed(dc->d_tokens, SeqMeta{dc->d_cu, dc->d_lens, n, 1}, m->emb.fmt, m->emb.q, m->emb.sc, d,
+                            V, dc->x, st));
+    }
     const int64_t layer = (int64_t)dc->slots * dc->slot_stride;
+    // algorithmic attention work of the rows: keys 0..pos of their slot
+    double keys = 0;
+    for (int i = 0; i < n; i++) keys += dc->h_meta[dc->max_rows + 2 * i + 1] + 1;
     for (int l = 0; l < L; l++) {
         const Layer &ly = m->layers[l];
-        HIPCHK(launch_layernorm(dc->x, ly.ln1w, ly.ln1b, dc->xb, AF_F32, n, d, st));
+        {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
+            HIPCHK(launch_layernorm(dc->x, ly.ln1w, ly.ln1b, dc->xb, AF_F32, n, d, st));
+        }
         HIPCHK(model_gemm(m, dc->part, ly.wqkv, dc->xb, d, AF_F32, ly.bqkv, dc->qkv, 3 * d, n, EPI_NONE));
         float *kc = dc->kc + l * layer, *vc = dc->vc + l * layer;
-        HIPCHK(launch_rope_kv(dc->qkv, d, m->hd, dc->d_rows, n, dc->rope_c, dc->rope_s, kc, vc, dc->slot_stride, st));
-        HIPCHK(launch_decode_attention(dc->qkv, d, H, dc->d_rows, n, dc->max_len, kc, vc, dc->slot_stride, dc->ao, st));
+        {
+            // K and V read once per key, Q read, rows written
+            ProfScope ps(m, CIH_KC_ATTENTION, 4.0 * keys * d, 8.0 * keys * d + 24.0 * n * d);
+            HIPCHK(launch_rope_kv(dc->qkv, d, m->hd, dc->d_rows, n, dc->rope_c, dc->rope_s, kc, vc, dc->slot_stride,
+                                  st));
+            HIPCHK(launch_decode_attention(dc->qkv, d, H, dc->d_rows, n, dc->max_len, kc, vc, dc->slot_stride, dc->ao,
+                                           st));
+        }
         HIPCHK(model_gemm(m, dc->part, ly.wo, dc->ao, d, AF_F32, ly.bo, dc->x, d, n, EPI_RESIDUAL));
-        HIPCHK(launch_layernorm(dc->x, ly.ln2w, ly.ln2b, dc->xb, AF_F32, n, d, st));
+        {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
+            HIPCHK(launch_layernorm(dc->x, ly.ln2w, ly.ln2b, dc->xb, AF_F32, n, d, st));
+        }
         HIPCHK(model_gemm(m, dc->part, ly.w1, dc->xb, d, AF_F32, ly.b1, dc->h, F, n, EPI_GELU));
         HIPCHK(model_gemm(m, dc->part, ly.w2, dc->h, F, AF_F32, ly.b2, dc->x, d, n, EPI_RESIDUAL));
     }
-    HIPCHK(launch_layernorm(dc->x, m->lnfw, m->lnfb, dc->ao, AF_F32, n, d, st));
+    {
+        ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
+        HIPCHK(launch_layernorm(dc->x, m->lnfw, m->lnfb, dc->ao, AF_F32, n, d, st));
+    }
     // project_lm_head_* (lib.rs:3952-4015): dense + GELU, LN, decoder; or the
     // tied embedding without bias
     if (m->has_head) {
         HIPCHK(model_gemm(m, dc->part, m->dense, dc->ao, d, AF_F32, m->dense_b, dc->h, d, n, EPI_GELU));
-        HIPCHK(launch_layernorm(dc->h, m->lm_lnw, m->lm_lnb, dc->xb, AF_F32, n, d, st));
+        {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
+            HIPCHK(launch_layernorm(dc->h, m->lm_lnw, m->lm_lnb, dc->xb, AF_F32, n, d, st));
+        }
         HIPCHK(model_gemm(m, dc->part, m->dec, dc->xb, d, AF_F32, m->dec_b, dc->logits, V, n, EPI_NONE));
     } else {
         HIPCHK(model_gemm(m, dc->part, m->emb, dc->ao, d, AF_F32, nullptr, dc->logits, V, n, EPI_NONE));
@@ -227,6 +251,7 @@ int cih_decode(cih_decoder *dc, const int32_t *slots, const int32_t *tokens, con
         HIPCHK(hipMemcpyAsync(logits, dc->logits, (size_t)n * dc->m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
                               dc->m->stream));
     HIPCHK(hipStreamSynchronize(dc->m->stream));
+    profile_collect(dc->m);
     return CIH_OK;
 }
 
@@ -272,6 +297,7 @@ int cih_generate(cih_decoder *dc, int32_t n, const int32_t *slots, const int32_t
         }
     }
     HIPCHK(hipStreamSynchronize(dc->m->stream));
+    profile_collect(dc->m);
     const double t_prefill = ms_since(t0);
     // generation: every live stream samples from its last logits and feeds the
     // token back at its next position; all live streams share one call
@@ -302,6 +328,7 @@ int cih_generate(cih_decoder *dc, int32_t n, const int32_t *slots, const int32_t
                 HIPCHK(hipMemcpyAsync(&lg[(size_t)idx[j0 + j] * V], dc->logits + (size_t)j * V, V * 4,
                                       hipMemcpyDeviceToHost, dc->m->stream));
             HIPCHK(hipStreamSynchronize(dc->m->stream));
+            profile_collect(dc->m);
         }
     }
     for (int i = 0; i < n; i++) n_generated[i] = count[i];

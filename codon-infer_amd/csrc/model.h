@@ -96,6 +96,34 @@ int upload(cih_model *m, T *&dst, const T *src, size_t n) {
     return 0;
 }
 
+// Records an event pair around the launches of its scope on the model's
+// stream when profiling is on (class, algorithmic flops and bytes).
+struct ProfScope {
+    cih_model *m;
+    int idx = -1;
+    ProfScope(cih_model *m_, int cls, double flops, double bytes) : m(m_) {
+        Prof &p = m->prof;
+        if (!p.on) return;
+        if (p.used >= p.cls.size()) {
+            hipEvent_t a, b;
+            if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return;
+            p.ev.push_back(a);
+            p.ev.push_back(b);
+            p.cls.push_back(0);
+            p.flops.push_back(0);
+            p.bytes.push_back(0);
+        }
+        idx = (int)p.used++;
+        p.cls[idx] = cls;
+        p.flops[idx] = flops;
+        p.bytes[idx] = bytes;
+        hipEventRecord(p.ev[2 * idx], m->stream);
+    }
+    ~ProfScope() {
+        if (idx >= 0) hipEventRecord(m->prof.ev[2 * idx + 1], m->stream);
+    }
+};
+
 void free_list(std::vector<void *> &l);
 int check_config(const cih_config *c);
 
@@ -103,6 +131,9 @@ int check_config(const cih_config *c);
 // a few FP32 rows, the MFMA GEMM otherwise; partial sums through pb.
 hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, const void *X, int ldx, int a_fmt,
                       const float *bias, void *Y, int ldy, int M, int epi);
+// After the stream has drained: adds the launches recorded since the last
+// call (event pairs of model_gemm and friends) to the per-class totals.
+void profile_collect(cih_model *m);
 // partial-sum floats any GEMM / GEMV of the model needs
 size_t model_part_floats(const cih_model *m);
 // RoPE cos / sin tables [max_len][hd/2] as the reference computes them
