@@ -172,7 +172,8 @@ def decode_bench(args, ch):
     per stream at its next position — the greedy choice among the ids
     sample() allows, <eos> excluded so every step does the same work.
     --warmup untimed steps, then --new-tokens timed steps; value = generated
-    tokens per second over all streams."""
+    tokens per second over all streams (steps replay a captured graph); a
+    second, instrumented pass of up to 64 steps gives the kernel breakdown."""
     cfg = ch.EsmConfig.by_name(args.model)
     seeds = {"8M": 8, "35M": 35, "150M": 150, "650M": 650, "3B": 3000}
     t0 = time.perf_counter()
@@ -199,23 +200,33 @@ def decode_bench(args, ch):
 
     for _ in range(args.warmup):
         step()
-    model.profile(True)
     t1 = time.perf_counter()
     for _ in range(K):
         step()
     el = time.perf_counter() - t1
+    # instrumented pass (kernel by kernel, an event pair per launch) at the
+    # same positions for the breakdown and the roofline
+    K2 = min(K, 64)
+    state["pos"] -= K2
+    model.profile(True)
+    t2 = time.perf_counter()
+    for _ in range(K2):
+        step()
+    el_instr = time.perf_counter() - t2
     model.profile(False)
+    K_prof = K2
     q = model.profile_read(ch.KC_GEMM_QUANT if args.dtype != "fp32" else ch.KC_GEMM_FP32)
     a = model.profile_read(ch.KC_ATTENTION)
     o = model.profile_read(ch.KC_OTHER)
     f = model.profile_read(ch.KC_GEMM_FP32) if args.dtype != "fp32" else {"total_ms": 0.0, "bytes": 0.0}
     gbs = q["bytes"] / (q["total_ms"] * 1e-3) / 1e9 if q["total_ms"] > 0 else 0.0
-    step_bytes = (q["bytes"] + a["bytes"] + o["bytes"] + f["bytes"]) / K
+    step_bytes = (q["bytes"] + a["bytes"] + o["bytes"] + f["bytes"]) / K_prof
     ms = el * 1e3 / K
     line = {
         "metric": f"decode tokens/s ESM-2 {args.model} {args.dtype} ({n} stream{'s' if n > 1 else ''})",
         "value": round(n * K / el, 1), "unit": "tokens/s",
         "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "ms_per_step_instrumented": round(el_instr * 1e3 / K_prof, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"ESM-2 {args.model} {args.dtype} autoregressive decode, {n} stream(s), 16-token "
                                f"prompts, positions {P + args.warmup}..{P + args.warmup + K - 1}, seeded weights",
@@ -223,8 +234,10 @@ def decode_bench(args, ch):
         "roofline": {"bound": "hbm", "kernel": "k_gemv (weights streamed once per step for all streams)",
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "timing": TIMING},
-        "step_breakdown_ms": {"gemv": round(q["total_ms"] / K, 4), "attention": round(a["total_ms"] / K, 4),
-                              "other": round(o["total_ms"] / K, 4), "lm_head_fp32": round(f["total_ms"] / K, 4)},
+        "step_breakdown_ms": {"gemv": round(q["total_ms"] / K_prof, 4),
+                              "attention": round(a["total_ms"] / K_prof, 4),
+                              "other": round(o["total_ms"] / K_prof, 4),
+                              "lm_head_fp32": round(f["total_ms"] / K_prof, 4)},
         "step_bytes": round(step_bytes), "step_GB_per_s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
     }
     if not args.no_cpu_baseline:

@@ -25,6 +25,8 @@ struct cih_decoder {
     int *h_meta = nullptr;  // pinned: tokens[max_rows] | rows[max_rows][2]
     cih::PartialBuf part;
     std::vector<int> filled;  // positions written per slot (0..filled-1 valid)
+    bool unique = false;      // staged rows: every slot at most once
+    std::map<std::pair<int, bool>, hipGraphExec_t> graphs;  // (rows, fused) -> captured step
     std::vector<void *> allocs;
 };
 
@@ -35,19 +37,20 @@ namespace {
 void destroy(cih_decoder *dc) {
     if (!dc) return;
     if (dc->m && dc->m->stream) hipStreamSynchronize(dc->m->stream);
+    for (auto &g : dc->graphs) hipGraphExecDestroy(g.second);
     free_list(dc->allocs);
     if (dc->h_meta) hipHostFree(dc->h_meta);
     delete dc;
 }
 
-// The rows' forward: embedding (constant 0.88 scale, <mask> -> 0), the
-// layers with cached causal attention, final LN and LM head -> dc->logits.
-int run_rows(cih_decoder *dc, int n) {
+// The rows' forward from the staged device tokens / rows: embedding
+// (constant 0.88 scale, <mask> -> 0), the layers with cached causal
+// attention, final LN and LM head -> dc->logits.  Kernel launches only, so
+// that a step can be captured into a graph.
+int enqueue_rows(cih_decoder *dc, int n, bool fused) {
     cih_model *m = dc->m;
     const int d = m->cfg.dim, F = m->cfg.hidden_dim, V = m->cfg.vocab_size, H = m->cfg.n_heads, L = m->cfg.n_layers;
     hipStream_t st = m->stream;
-    HIPCHK(hipMemcpyAsync(dc->d_tokens, dc->h_meta, (size_t)n * 4, hipMemcpyHostToDevice, st));
-    HIPCHK(hipMemcpyAsync(dc->d_rows, dc->h_meta + dc->max_rows, (size_t)n * 8, hipMemcpyHostToDevice, st));
     // forward_* embedding (lib.rs:3567-3575, 3753-3765): every row is a
     // one-token sequence, for which the token-dropout scale is 0.88 exactly
     {
@@ -70,10 +73,15 @@ int run_rows(cih_decoder *dc, int n) {
         {
             // K and V read once per key, Q read, rows written
             ProfScope ps(m, CIH_KC_ATTENTION, 4.0 * keys * d, 8.0 * keys * d + 24.0 * n * d);
-            HIPCHK(launch_rope_kv(dc->qkv, d, m->hd, dc->d_rows, n, dc->rope_c, dc->rope_s, kc, vc, dc->slot_stride,
-                                  st));
-            HIPCHK(launch_decode_attention(dc->qkv, d, H, dc->d_rows, n, dc->max_len, kc, vc, dc->slot_stride, dc->ao,
-                                           st));
+            if (fused) {
+                HIPCHK(launch_decode_attention_fused(dc->qkv, d, H, dc->d_rows, n, dc->max_len, dc->rope_c,
+                                                     dc->rope_s, kc, vc, dc->slot_stride, dc->ao, st));
+            } else {
+                HIPCHK(launch_rope_kv(dc->qkv, d, m->hd, dc->d_rows, n, dc->rope_c, dc->rope_s, kc, vc,
+                                      dc->slot_stride, st));
+                HIPCHK(launch_decode_attention(dc->qkv, d, H, dc->d_rows, n, dc->max_len, kc, vc, dc->slot_stride,
+                                               dc->ao, st));
+            }
         }
         HIPCHK(model_gemm(m, dc->part, ly.wo, dc->ao, d, AF_F32, ly.bo, dc->x, d, n, EPI_RESIDUAL));
         {
@@ -102,6 +110,42 @@ int run_rows(cih_decoder *dc, int n) {
     return 0;
 }
 
+// Decode steps (at most GEMV_MAX_M rows) replay a captured graph of the
+// whole step, one per (rows, fused); the graph reads tokens and positions
+// from the decoder's device buffers, which are refreshed before each replay.
+// Profiling runs and CIH_DECODE_GRAPH=0 launch kernel by kernel.
+bool use_graph(const cih_decoder *dc, int n) {
+    const char *e = getenv("CIH_DECODE_GRAPH");
+    return n <= GEMV_MAX_M && !dc->m->prof.on && !(e && !std::strcmp(e, "0"));
+}
+
+int run_rows(cih_decoder *dc, int n) {
+    hipStream_t st = dc->m->stream;
+    const bool fused = dc->unique;
+    HIPCHK(hipMemcpyAsync(dc->d_tokens, dc->h_meta, (size_t)n * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(dc->d_rows, dc->h_meta + dc->max_rows, (size_t)n * 8, hipMemcpyHostToDevice, st));
+    if (!use_graph(dc, n)) return enqueue_rows(dc, n, fused);
+    auto key = std::make_pair(n, fused);
+    auto it = dc->graphs.find(key);
+    if (it == dc->graphs.end()) {
+        hipGraph_t g = nullptr;
+        HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_rows(dc, n, fused);
+        const hipError_t e = hipStreamEndCapture(st, &g);
+        if (rc || e != hipSuccess) {
+            if (g) hipGraphDestroy(g);
+            return rc ? rc : set_error(CIH_ERR_HIP, "decode step capture failed: %s", hipGetErrorString(e));
+        }
+        hipGraphExec_t ex = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ei != hipSuccess) return set_error(CIH_ERR_HIP, "decode step graph: %s", hipGetErrorString(ei));
+        it = dc->graphs.emplace(key, ex).first;
+    }
+    HIPCHK(hipGraphLaunch(it->second, st));
+    return 0;
+}
+
 // Validates rows and stages them; rows of one slot must continue its
 // cache: consecutive positions starting at most at the slot's filled count.
 int stage_rows(cih_decoder *dc, const int32_t *slots, const int32_t *tokens, const int32_t *pos, int n) {
@@ -125,6 +169,7 @@ int stage_rows(cih_decoder *dc, const int32_t *slots, const int32_t *tokens, con
         dc->h_meta[dc->max_rows + 2 * i + 1] = p;
     }
     for (auto &kv : next) dc->filled[kv.first] = std::max(dc->filled[kv.first], kv.second);
+    dc->unique = (int)next.size() == n;
     return 0;
 }
 
@@ -186,7 +231,7 @@ int cih_decoder_create(cih_model *m, int32_t n_slots, int32_t max_len, int32_t m
     if (!m || !out) return set_error(CIH_ERR_ARG, "null argument");
     *out = nullptr;
     if (n_slots < 1 || max_len < 1 || max_rows < 1) return set_error(CIH_ERR_ARG, "n_slots, max_len, max_rows must be >= 1");
-    if (max_len > 16000) return set_error(CIH_ERR_SHAPE, "max_len %d above the attention kernel's 16000", max_len);
+    if (max_len > 15000) return set_error(CIH_ERR_SHAPE, "max_len %d above the attention kernel's 15000", max_len);
     const size_t d = m->cfg.dim, F = m->cfg.hidden_dim, V = m->cfg.vocab_size, L = m->cfg.n_layers;
     const size_t R = max_rows;
     cih_decoder *dc = new cih_decoder();

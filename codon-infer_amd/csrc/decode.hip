@@ -41,6 +41,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_rope_kv(float *__restrict__ qkv
     for (int i = threadIdx.x; i < d; i += DEC_THREADS) vd[i] = v[i];
 }
 
+constexpr int ATT_THREADS = 512;  // 8 waves per (row, head)
+
 __device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_max) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -53,79 +55,126 @@ __device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_m
     __syncthreads();
     float r = scratch[0];
 #pragma unroll
-    for (int i = 1; i < DEC_THREADS / 64; i++) r = is_max ? fmaxf(r, scratch[i]) : r + scratch[i];
+    for (int i = 1; i < ATT_THREADS / 64; i++) r = is_max ? fmaxf(r, scratch[i]) : r + scratch[i];
     return r;
 }
 
 // One workgroup per (row, head).  Scores s_t = (q . k_t) / sqrt(hd) for
 // t = 0..pos (a thread per key), softmax as softmax() (lib.rs:3500-3504:
-// max, exp(s - max), 1 / sum, p = e * (1/sum)), then out = sum_t p_t v_t with
-// G = 256 / HD key groups of HD lanes (a group reads whole V rows) whose
-// partial sums are added in group order.
-template <int HD>
-__global__ __launch_bounds__(DEC_THREADS) void k_decode_attention(const float *__restrict__ qkv, int d,
+// max, exp(s - max), 1 / sum), then out = sum_t p_t v_t with G = 512 / HD
+// key groups of HD lanes (a group reads whole V rows, four rows in flight)
+// whose partial sums are added in group order.
+//
+// FUSED (each slot at most once in the launch): the workgroup also applies
+// RoPE to its head's Q and K, writes K and V at pos into the cache for later
+// steps, and takes key pos from LDS rather than from the cache, so no
+// workgroup reads what another one writes.  Otherwise k_rope_kv has run.
+template <int HD, bool FUSED>
+__global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *__restrict__ qkv, int d,
                                                                   const int *__restrict__ rows,
-                                                                  const float *__restrict__ kc,
-                                                                  const float *__restrict__ vc, int64_t slot_stride,
+                                                                  const float *__restrict__ rc,
+                                                                  const float *__restrict__ rs, float *__restrict__ kc,
+                                                                  float *__restrict__ vc, int64_t slot_stride,
                                                                   float inv_scale, float *__restrict__ out) {
-    constexpr int G = DEC_THREADS / HD;
+    constexpr int G = ATT_THREADS / HD;
+    constexpr int HALF = HD / 2;
     extern __shared__ float sm[];
-    float *qs = sm;                 // [HD]
-    float *part = qs + HD;          // [G][HD]
-    float *red = part + G * HD;     // [4]
-    float *p = red + 4;             // [pos + 1]
+    float *qs = sm;                        // [HD] rotated query
+    float *kcur = qs + HD, *vcur = kcur + HD;  // [HD] key and value at pos (FUSED)
+    float *part = vcur + HD;               // [G][HD]
+    float *red = part + ATT_THREADS;       // [8]
+    float *p = red + 8;                    // [pos + 1]
     const int r = blockIdx.x, h = blockIdx.y;
     const int slot = rows[2 * r], pos = rows[2 * r + 1];
     const float *q = qkv + (size_t)r * 3 * d + h * HD;
-    const float *K = kc + slot * slot_stride + h * HD;
-    const float *V = vc + slot * slot_stride + h * HD;
-    if (threadIdx.x < HD) qs[threadIdx.x] = q[threadIdx.x];
+    float *K = kc + slot * slot_stride + h * HD;
+    float *V = vc + slot * slot_stride + h * HD;
+    const int t = threadIdx.x;
+    if constexpr (FUSED) {
+        // apply_rope (lib.rs:3533-3552) for this head, products rounded one by one
+        if (t < HALF) {
+            const float c = rc[(size_t)pos * HALF + t], s = rs[(size_t)pos * HALF + t];
+            const float *k = q + d;
+            const float q0 = q[t], q1 = q[t + HALF], k0 = k[t], k1 = k[t + HALF];
+            qs[t] = __fsub_rn(__fmul_rn(q0, c), __fmul_rn(q1, s));
+            qs[t + HALF] = __fadd_rn(__fmul_rn(q1, c), __fmul_rn(q0, s));
+            const float r0 = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
+            const float r1 = __fadd_rn(__fmul_rn(k1, c), __fmul_rn(k0, s));
+            kcur[t] = r0;
+            kcur[t + HALF] = r1;
+            K[(size_t)pos * d + t] = r0;
+            K[(size_t)pos * d + t + HALF] = r1;
+        } else if (t >= 64 && t < 64 + HD) {
+            const float v = q[2 * d + t - 64];
+            vcur[t - 64] = v;
+            V[(size_t)pos * d + t - 64] = v;
+        }
+    } else {
+        if (t < HD) qs[t] = q[t];
+    }
     __syncthreads();
+    const int n_cached = FUSED ? pos : pos + 1;  // keys read from the cache
     float mx = -INFINITY;
-    for (int t = threadIdx.x; t <= pos; t += DEC_THREADS) {
-        const float4 *kr = reinterpret_cast<const float4 *>(K + (size_t)t * d);
+    for (int j = t; j <= pos; j += ATT_THREADS) {
         float acc = 0.0f;
+        if (j < n_cached) {
+            const float4 *kr = reinterpret_cast<const float4 *>(K + (size_t)j * d);
 #pragma unroll
-        for (int i = 0; i < HD / 4; i++) {
-            const float4 kv = kr[i];
-            acc = fmaf(qs[4 * i], kv.x, acc);
-            acc = fmaf(qs[4 * i + 1], kv.y, acc);
-            acc = fmaf(qs[4 * i + 2], kv.z, acc);
-            acc = fmaf(qs[4 * i + 3], kv.w, acc);
+            for (int i = 0; i < HD / 4; i++) {
+                const float4 kv = kr[i];
+                acc = fmaf(qs[4 * i], kv.x, acc);
+                acc = fmaf(qs[4 * i + 1], kv.y, acc);
+                acc = fmaf(qs[4 * i + 2], kv.z, acc);
+                acc = fmaf(qs[4 * i + 3], kv.w, acc);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < HD; i++) acc = fmaf(qs[i], kcur[i], acc);
         }
         const float sc = acc * inv_scale;
-        p[t] = sc;
+        p[j] = sc;
         mx = fmaxf(mx, sc);
     }
     mx = block_reduce(mx, red, true);
     float sum = 0.0f;
-    for (int t = threadIdx.x; t <= pos; t += DEC_THREADS) {
-        const float e = expf(p[t] - mx);
-        p[t] = e;
+    for (int j = t; j <= pos; j += ATT_THREADS) {
+        const float e = expf(p[j] - mx);
+        p[j] = e;
         sum += e;
     }
     sum = block_reduce(sum, red, false);
     const float inv = 1.0f / sum;
     __syncthreads();
-    const int g = threadIdx.x / HD, i = threadIdx.x - g * HD;
+    const int g = t / HD, i = t - g * HD;
     if (g < G) {
-        float acc = 0.0f;
-        for (int t = g; t <= pos; t += G) acc = fmaf(p[t] * inv, V[(size_t)t * d + i], acc);
-        part[g * HD + i] = acc;
+        const float *vi = V + i;
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        int j = g;
+        for (; j + 3 * G < n_cached; j += 4 * G) {
+            const float v0 = vi[(size_t)j * d], v1 = vi[(size_t)(j + G) * d];
+            const float v2 = vi[(size_t)(j + 2 * G) * d], v3 = vi[(size_t)(j + 3 * G) * d];
+            a0 = fmaf(p[j] * inv, v0, a0);
+            a1 = fmaf(p[j + G] * inv, v1, a1);
+            a2 = fmaf(p[j + 2 * G] * inv, v2, a2);
+            a3 = fmaf(p[j + 3 * G] * inv, v3, a3);
+        }
+        for (; j < n_cached; j += G) a0 = fmaf(p[j] * inv, vi[(size_t)j * d], a0);
+        if (FUSED && j == pos) a0 = fmaf(p[j] * inv, vcur[i], a0);
+        part[g * HD + i] = (a0 + a1) + (a2 + a3);
     }
     __syncthreads();
-    if (threadIdx.x < HD) {
-        float o = part[threadIdx.x];
+    if (t < HD) {
+        float o = part[t];
 #pragma unroll
-        for (int j = 1; j < G; j++) o += part[j * HD + threadIdx.x];
-        out[(size_t)r * d + h * HD + threadIdx.x] = o;
+        for (int k = 1; k < G; k++) o += part[k * HD + t];
+        out[(size_t)r * d + h * HD + t] = o;
     }
 }
 
 }  // namespace
 
 size_t decode_attention_lds(int hd, int max_len) {
-    return sizeof(float) * ((size_t)hd + DEC_THREADS + 4 + (size_t)max_len);
+    return sizeof(float) * (3 * (size_t)hd + ATT_THREADS + 8 + (size_t)max_len);
 }
 
 hipError_t launch_rope_kv(float *qkv, int d, int hd, const int *rows, int n, const float *rope_c, const float *rope_s,
@@ -136,22 +185,42 @@ hipError_t launch_rope_kv(float *qkv, int d, int hd, const int *rows, int n, con
     return hipGetLastError();
 }
 
+template <bool FUSED>
+static hipError_t launch_att(const float *qkv, int d, int H, const int *rows, int n, int max_len, const float *rc,
+                             const float *rs, float *kc, float *vc, int64_t slot_stride, float *out, hipStream_t st) {
+    const int hd = d / H;
+    const float inv_scale = 1.0f / sqrtf((float)hd);
+    const size_t lds = decode_attention_lds(hd, max_len);
+    const dim3 grid(n, H), block(ATT_THREADS);
+#define CIH_ATT_CASE(HDV)                                                                                           \
+    case HDV:                                                                                                      \
+        hipLaunchKernelGGL((k_decode_attention<HDV, FUSED>), grid, block, lds, st, qkv, d, rows, rc, rs, kc, vc,   \
+                           slot_stride, inv_scale, out);                                                           \
+        break;
+    switch (hd) {
+        CIH_ATT_CASE(16)
+        CIH_ATT_CASE(24)
+        CIH_ATT_CASE(32)
+        CIH_ATT_CASE(64)
+    default: return hipErrorInvalidValue;
+    }
+#undef CIH_ATT_CASE
+    return hipGetLastError();
+}
+
 hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *rows, int n, int max_len,
                                    const float *kc, const float *vc, int64_t slot_stride, float *out,
                                    hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    const int hd = d / H;
-    const float inv_scale = 1.0f / sqrtf((float)hd);
-    const size_t lds = decode_attention_lds(hd, max_len);
-    const dim3 grid(n, H), block(DEC_THREADS);
-    switch (hd) {
-    case 16: hipLaunchKernelGGL(k_decode_attention<16>, grid, block, lds, st, qkv, d, rows, kc, vc, slot_stride, inv_scale, out); break;
-    case 24: hipLaunchKernelGGL(k_decode_attention<24>, grid, block, lds, st, qkv, d, rows, kc, vc, slot_stride, inv_scale, out); break;
-    case 32: hipLaunchKernelGGL(k_decode_attention<32>, grid, block, lds, st, qkv, d, rows, kc, vc, slot_stride, inv_scale, out); break;
-    case 64: hipLaunchKernelGGL(k_decode_attention<64>, grid, block, lds, st, qkv, d, rows, kc, vc, slot_stride, inv_scale, out); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    return launch_att<false>(qkv, d, H, rows, n, max_len, nullptr, nullptr, const_cast<float *>(kc),
+                             const_cast<float *>(vc), slot_stride, out, st);
+}
+
+hipError_t launch_decode_attention_fused(float *qkv, int d, int H, const int *rows, int n, int max_len,
+                                         const float *rope_c, const float *rope_s, float *kc, float *vc,
+                                         int64_t slot_stride, float *out, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    return launch_att<true>(qkv, d, H, rows, n, max_len, rope_c, rope_s, kc, vc, slot_stride, out, st);
 }
 
 }  // namespace cih

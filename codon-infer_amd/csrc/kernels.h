@@ -145,6 +145,12 @@ hipError_t launch_rope_kv(float *qkv, int d, int hd, const int *rows, int n, con
 hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *rows, int n, int max_len,
                                    const float *kc, const float *vc, int64_t slot_stride, float *out,
                                    hipStream_t st);
+// Both steps in one launch when every slot appears at most once among the
+// rows (one new token per sequence): each (row, head) workgroup rotates its
+// head's Q and K, writes K and V at pos, and attends with key pos from LDS.
+hipError_t launch_decode_attention_fused(float *qkv, int d, int H, const int *rows, int n, int max_len,
+                                         const float *rope_c, const float *rope_s, float *kc, float *vc,
+                                         int64_t slot_stride, float *out, hipStream_t st);
 size_t decode_attention_lds(int hd, int max_len);  // dynamic LDS bytes per workgroup
 
 // Copies packed rows [T][width] into padded [B][S_max][width] (valid rows only).

@@ -146,7 +146,7 @@ typedef struct cih_decoder cih_decoder;
 /* Replaces RunState::new (lib.rs:2464-2486) for n_slots independent
  * sequences: a K and a V cache of [n_layers][n_slots][max_len][dim] floats
  * on the device, RoPE tables for max_len positions, and row buffers for up
- * to max_rows rows per cih_decode call.  max_len <= 16000. */
+ * to max_rows rows per cih_decode call.  max_len <= 15000. */
 int cih_decoder_create(cih_model *m, int32_t n_slots, int32_t max_len, int32_t max_rows,
                        cih_decoder **out);
 int cih_decoder_destroy(cih_decoder *d);

@@ -78,6 +78,38 @@ def test_slots_are_independent_and_batch_invariant(w8m_all):
     m.close()
 
 
+def test_graph_replays_match_eager(w8m_all, monkeypatch):
+    """Decode steps replay a captured graph; every replay, with eager prefill
+    calls and host syncs in between, equals the kernel-by-kernel run."""
+    cfg, ws = w8m_all
+    m = ch.GpuModel(cfg, ws["q4"], max_batch=1, max_len=16)
+    d_graph = ch.GpuDecoder(m, n_slots=2, max_len=64, max_rows=16)
+    d_eager = ch.GpuDecoder(m, n_slots=2, max_len=64, max_rows=16)
+    prompt = [0, 20, 5, 7, 9, 11, 4, 4, 13, 6]                   # 10 rows: eager in both
+    for dec in (d_graph, d_eager):
+        monkeypatch.setenv("CIH_DECODE_GRAPH", "1" if dec is d_graph else "0")
+        dec.decode(np.zeros(10), prompt, np.arange(10))
+        dec.decode(np.ones(4), prompt[:4], np.arange(4))
+    rng = np.random.default_rng(2)
+    p1 = 4                                                       # next position of slot 1
+    for step in range(20):
+        t = (4 + rng.integers(0, 20, 3)).astype(np.int32)
+        if step % 3 == 2:                                        # two rows of slot 1: the unfused kernels
+            rows = ([0, 1, 1], t, [10 + step, p1, p1 + 1])
+            p1 += 2
+        else:                                                    # one row per slot: the fused kernel
+            rows = ([0, 1], t[:2], [10 + step, p1])
+            p1 += 1
+        monkeypatch.setenv("CIH_DECODE_GRAPH", "1")
+        a = d_graph.decode(*rows)
+        monkeypatch.setenv("CIH_DECODE_GRAPH", "0")
+        b = d_eager.decode(*rows)
+        assert np.array_equal(a, b), step
+    d_graph.close()
+    d_eager.close()
+    m.close()
+
+
 def test_row_validation(w8m_all):
     cfg, ws = w8m_all
     m = ch.GpuModel(cfg, ws["q8"], max_batch=1, max_len=16)
