@@ -66,6 +66,10 @@ void free_workspace(Workspace &ws) {
 }
 
 
+}  // namespace
+
+namespace cih {
+
 double wbytes(const DevMatrix &W) {
     const double e = (double)W.N * W.K;
     return W.fmt == WF_F32 ? 4.0 * e : (W.fmt == WF_Q8 ? 1.125 * e : 0.625 * e);
@@ -77,6 +81,10 @@ bool use_gemv(int M, int a_fmt, int epi) {
     return !(e && !std::strcmp(e, "0")) && M <= GEMV_MAX_M && a_fmt == AF_F32 && epi != EPI_GELU_X3 &&
            epi != EPI_GELU_H2;
 }
+
+}  // namespace cih
+
+namespace {
 
 }  // namespace
 

@@ -68,14 +68,25 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
             HIPCHK(launch_layernorm(dc->x, ly.ln1w, ly.ln1b, dc->xb, AF_F32, n, d, st));
         }
-        HIPCHK(model_gemm(m, dc->part, ly.wqkv, dc->xb, d, AF_F32, ly.bqkv, dc->qkv, 3 * d, n, EPI_NONE));
+        // one row per sequence through the GEMV: the attention kernel adds
+        // the QKV partial sums itself (no separate reduction)
+        const bool qkv_parts = fused && use_gemv(n, AF_F32, EPI_NONE);
+        int splits = 0;
+        if (qkv_parts) {
+            ProfScope ps(m, ly.wqkv.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, 2.0 * n * ly.wqkv.N * d,
+                         wbytes(ly.wqkv) + 4.0 * n * d + 4.0 * n * ly.wqkv.N);
+            HIPCHK(launch_gemv_partials(ly.wqkv, dc->xb, d, n, dc->part, &splits, st));
+        } else {
+            HIPCHK(model_gemm(m, dc->part, ly.wqkv, dc->xb, d, AF_F32, ly.bqkv, dc->qkv, 3 * d, n, EPI_NONE));
+        }
         float *kc = dc->kc + l * layer, *vc = dc->vc + l * layer;
         {
             // K and V read once per key, Q read, rows written
             ProfScope ps(m, CIH_KC_ATTENTION, 4.0 * keys * d, 8.0 * keys * d + 24.0 * n * d);
             if (fused) {
-                HIPCHK(launch_decode_attention_fused(dc->qkv, d, H, dc->d_rows, n, dc->max_len, dc->rope_c,
-                                                     dc->rope_s, kc, vc, dc->slot_stride, dc->ao, st));
+                HIPCHK(launch_decode_attention_fused(dc->qkv, qkv_parts ? dc->part.part : nullptr, splits, ly.bqkv, d,
+                                                     H, dc->d_rows, n, dc->max_len, dc->rope_c, dc->rope_s, kc, vc,
+                                                     dc->slot_stride, dc->ao, st));
             } else {
                 HIPCHK(launch_rope_kv(dc->qkv, d, m->hd, dc->d_rows, n, dc->rope_c, dc->rope_s, kc, vc,
                                       dc->slot_stride, st));

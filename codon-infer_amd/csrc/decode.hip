@@ -70,7 +70,9 @@ __device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_m
 // steps, and takes key pos from LDS rather than from the cache, so no
 // workgroup reads what another one writes.  Otherwise k_rope_kv has run.
 template <int HD, bool FUSED>
-__global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *__restrict__ qkv, int d,
+__global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *__restrict__ qkv,
+                                                                  const float *__restrict__ part, int splits,
+                                                                  const float *__restrict__ bias, int d,
                                                                   const int *__restrict__ rows,
                                                                   const float *__restrict__ rc,
                                                                   const float *__restrict__ rs, float *__restrict__ kc,
@@ -81,21 +83,35 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
     extern __shared__ float sm[];
     float *qs = sm;                        // [HD] rotated query
     float *kcur = qs + HD, *vcur = kcur + HD;  // [HD] key and value at pos (FUSED)
-    float *part = vcur + HD;               // [G][HD]
-    float *red = part + ATT_THREADS;       // [8]
+    float *gsum = vcur + HD;               // [G][HD] per-group partial outputs
+    float *red = gsum + ATT_THREADS;       // [8]
     float *p = red + 8;                    // [pos + 1]
     const int r = blockIdx.x, h = blockIdx.y;
     const int slot = rows[2 * r], pos = rows[2 * r + 1];
-    const float *q = qkv + (size_t)r * 3 * d + h * HD;
     float *K = kc + slot * slot_stride + h * HD;
     float *V = vc + slot * slot_stride + h * HD;
     const int t = threadIdx.x;
     if constexpr (FUSED) {
+        // this head's q, k, v: the row of qkv, or the GEMV's partial sums
+        // (split order) + bias
+        if (t < 3 * HD) {
+            const int which = t / HD, col = which * d + h * HD + (t - which * HD);
+            float v;
+            if (part) {
+                const int n = gridDim.x;
+                float acc = 0.0f;
+                for (int y = 0; y < splits; y++) acc += part[((size_t)y * n + r) * 3 * d + col];
+                v = acc + bias[col];
+            } else {
+                v = qkv[(size_t)r * 3 * d + col];
+            }
+            qs[t] = v;  // qs | kcur | vcur are contiguous
+        }
+        __syncthreads();
         // apply_rope (lib.rs:3533-3552) for this head, products rounded one by one
         if (t < HALF) {
             const float c = rc[(size_t)pos * HALF + t], s = rs[(size_t)pos * HALF + t];
-            const float *k = q + d;
-            const float q0 = q[t], q1 = q[t + HALF], k0 = k[t], k1 = k[t + HALF];
+            const float q0 = qs[t], q1 = qs[t + HALF], k0 = kcur[t], k1 = kcur[t + HALF];
             qs[t] = __fsub_rn(__fmul_rn(q0, c), __fmul_rn(q1, s));
             qs[t + HALF] = __fadd_rn(__fmul_rn(q1, c), __fmul_rn(q0, s));
             const float r0 = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
@@ -105,11 +121,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
             K[(size_t)pos * d + t] = r0;
             K[(size_t)pos * d + t + HALF] = r1;
         } else if (t >= 64 && t < 64 + HD) {
-            const float v = q[2 * d + t - 64];
-            vcur[t - 64] = v;
-            V[(size_t)pos * d + t - 64] = v;
+            V[(size_t)pos * d + t - 64] = vcur[t - 64];
         }
     } else {
+        const float *q = qkv + (size_t)r * 3 * d + h * HD;
         if (t < HD) qs[t] = q[t];
     }
     __syncthreads();
@@ -160,13 +175,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
         }
         for (; j < n_cached; j += G) a0 = fmaf(p[j] * inv, vi[(size_t)j * d], a0);
         if (FUSED && j == pos) a0 = fmaf(p[j] * inv, vcur[i], a0);
-        part[g * HD + i] = (a0 + a1) + (a2 + a3);
+        gsum[g * HD + i] = (a0 + a1) + (a2 + a3);
     }
     __syncthreads();
     if (t < HD) {
-        float o = part[t];
+        float o = gsum[t];
 #pragma unroll
-        for (int k = 1; k < G; k++) o += part[k * HD + t];
+        for (int k = 1; k < G; k++) o += gsum[k * HD + t];
         out[(size_t)r * d + h * HD + t] = o;
     }
 }
@@ -186,16 +201,17 @@ hipError_t launch_rope_kv(float *qkv, int d, int hd, const int *rows, int n, con
 }
 
 template <bool FUSED>
-static hipError_t launch_att(const float *qkv, int d, int H, const int *rows, int n, int max_len, const float *rc,
-                             const float *rs, float *kc, float *vc, int64_t slot_stride, float *out, hipStream_t st) {
+static hipError_t launch_att(const float *qkv, const float *part, int splits, const float *bias, int d, int H,
+                             const int *rows, int n, int max_len, const float *rc, const float *rs, float *kc,
+                             float *vc, int64_t slot_stride, float *out, hipStream_t st) {
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
     const size_t lds = decode_attention_lds(hd, max_len);
     const dim3 grid(n, H), block(ATT_THREADS);
 #define CIH_ATT_CASE(HDV)                                                                                           \
     case HDV:                                                                                                      \
-        hipLaunchKernelGGL((k_decode_attention<HDV, FUSED>), grid, block, lds, st, qkv, d, rows, rc, rs, kc, vc,   \
-                           slot_stride, inv_scale, out);                                                           \
+        hipLaunchKernelGGL((k_decode_attention<HDV, FUSED>), grid, block, lds, st, qkv, part, splits, bias, d,     \
+                           rows, rc, rs, kc, vc, slot_stride, inv_scale, out);                                     \
         break;
     switch (hd) {
         CIH_ATT_CASE(16)
@@ -212,15 +228,18 @@ hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *ro
                                    const float *kc, const float *vc, int64_t slot_stride, float *out,
                                    hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    return launch_att<false>(qkv, d, H, rows, n, max_len, nullptr, nullptr, const_cast<float *>(kc),
-                             const_cast<float *>(vc), slot_stride, out, st);
+    return launch_att<false>(qkv, nullptr, 0, nullptr, d, H, rows, n, max_len, nullptr, nullptr,
+                             const_cast<float *>(kc), const_cast<float *>(vc), slot_stride, out, st);
 }
 
-hipError_t launch_decode_attention_fused(float *qkv, int d, int H, const int *rows, int n, int max_len,
-                                         const float *rope_c, const float *rope_s, float *kc, float *vc,
-                                         int64_t slot_stride, float *out, hipStream_t st) {
+hipError_t launch_decode_attention_fused(float *qkv, const float *part, int splits, const float *bias, int d, int H,
+                                         const int *rows, int n, int max_len, const float *rope_c,
+                                         const float *rope_s, float *kc, float *vc, int64_t slot_stride, float *out,
+                                         hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    return launch_att<true>(qkv, d, H, rows, n, max_len, rope_c, rope_s, kc, vc, slot_stride, out, st);
+    if (part && (!bias || splits < 1)) return hipErrorInvalidValue;
+    return launch_att<true>(qkv, part, splits, bias, d, H, rows, n, max_len, rope_c, rope_s, kc, vc, slot_stride, out,
+                            st);
 }
 
 }  // namespace cih

@@ -103,7 +103,7 @@ template <int WF, int MM, int NB>
 __global__ __launch_bounds__(256) void k_gemv(const float *__restrict__ X, int ldx, const void *__restrict__ Wq,
                                               const float *__restrict__ Wsc, int N, int KB,
                                               const float *__restrict__ bias, float *__restrict__ Y, int ldy, int epi,
-                                              float *__restrict__ part) {
+                                              float *__restrict__ part, int to_part) {
     __shared__ float red[4][MM][64];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: X reads become scalar
@@ -146,21 +146,32 @@ __global__ __launch_bounds__(256) void k_gemv(const float *__restrict__ X, int l
         const int m = t >> 6, c = t & 63, nn = blockIdx.x * 64 + c;
         if (nn >= N) continue;
         const float s = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
-        if (gridDim.y == 1) store_out(epi, s, bias, nn, Y + (size_t)m * ldy + nn);
+        if (gridDim.y == 1 && !to_part) store_out(epi, s, bias, nn, Y + (size_t)m * ldy + nn);
         else part[((size_t)blockIdx.y * MM + m) * N + nn] = s;
     }
 }
 
-// Y[m][n] = epi(sum over splits of part[split][m][n] + bias[n]), splits in order
+// Y[m][n] = epi(sum over splits of part[split][m][n] + bias[n]).  Eight
+// lanes per output: lane j adds splits j, j + 8, ... (its loads issued
+// together), then a fixed xor tree joins the eight lanes.  The order depends
+// on the split count only, not on M, so a row's result does not depend on
+// the other rows.
 __global__ __launch_bounds__(256) void k_gemv_reduce(const float *__restrict__ part, int splits, int M, int N,
                                                      const float *__restrict__ bias, float *__restrict__ Y, int ldy,
                                                      int epi) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= M * N) return;
-    const int m = i / N, n = i - m * N;
-    float s = part[(size_t)m * N + n];
-    for (int y = 1; y < splits; y++) s += part[((size_t)y * M + m) * N + n];
-    store_out(epi, s, bias, n, Y + (size_t)m * ldy + n);
+    const int MN = M * N;
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    const int e = gid >> 3, j = gid & 7;
+    const int ec = e < MN ? e : MN - 1;  // lanes past the end join the shuffles with a valid address
+    float s = 0.0f;
+    for (int y = j; y < splits; y += 8) s += part[(size_t)y * MN + ec];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (j == 0 && e < MN) {
+        const int m = e / N, n = e - m * N;
+        store_out(epi, s, bias, n, Y + (size_t)m * ldy + n);
+    }
 }
 
 GemvGrid gemv_grid(int N, int K) {
@@ -186,33 +197,50 @@ size_t gemv_part_floats(int N, int K) {
 
 template <int WF, int MM>
 static void launch_mm(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int epi,
-                      float *part, const GemvGrid &g, hipStream_t st) {
+                      float *part, int to_part, const GemvGrid &g, hipStream_t st) {
     const dim3 grid(g.cols, g.splits);
     const int KB = W.K / 32;
     if (g.nb == 1)
         hipLaunchKernelGGL((k_gemv<WF, MM, 1>), grid, dim3(256), 0, st, X, ldx, W.q, W.sc, W.N, KB, bias, Y, ldy, epi,
-                           part);
+                           part, to_part);
     else if (g.nb == 2)
         hipLaunchKernelGGL((k_gemv<WF, MM, 2>), grid, dim3(256), 0, st, X, ldx, W.q, W.sc, W.N, KB, bias, Y, ldy, epi,
-                           part);
+                           part, to_part);
     else
         hipLaunchKernelGGL((k_gemv<WF, MM, 4>), grid, dim3(256), 0, st, X, ldx, W.q, W.sc, W.N, KB, bias, Y, ldy, epi,
-                           part);
+                           part, to_part);
 }
 
 template <int WF>
 static void launch_fmt(const DevMatrix &W, const float *X, int ldx, int M, const float *bias, float *Y, int ldy,
-                       int epi, float *part, const GemvGrid &g, hipStream_t st) {
+                       int epi, float *part, int to_part, const GemvGrid &g, hipStream_t st) {
     switch (M) {
-    case 1: return launch_mm<WF, 1>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
-    case 2: return launch_mm<WF, 2>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
-    case 3: return launch_mm<WF, 3>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
-    case 4: return launch_mm<WF, 4>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
-    case 5: return launch_mm<WF, 5>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
-    case 6: return launch_mm<WF, 6>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
-    case 7: return launch_mm<WF, 7>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
-    default: return launch_mm<WF, 8>(W, X, ldx, bias, Y, ldy, epi, part, g, st);
+    case 1: return launch_mm<WF, 1>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
+    case 2: return launch_mm<WF, 2>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
+    case 3: return launch_mm<WF, 3>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
+    case 4: return launch_mm<WF, 4>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
+    case 5: return launch_mm<WF, 5>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
+    case 6: return launch_mm<WF, 6>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
+    case 7: return launch_mm<WF, 7>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
+    default: return launch_mm<WF, 8>(W, X, ldx, bias, Y, ldy, epi, part, to_part, g, st);
     }
+}
+
+static void launch_any(const DevMatrix &W, const float *X, int ldx, int M, const float *bias, float *Y, int ldy,
+                       int epi, float *part, int to_part, const GemvGrid &g, hipStream_t st) {
+    if (W.fmt == WF_Q8) launch_fmt<WF_Q8>(W, X, ldx, M, bias, Y, ldy, epi, part, to_part, g, st);
+    else if (W.fmt == WF_Q4) launch_fmt<WF_Q4>(W, X, ldx, M, bias, Y, ldy, epi, part, to_part, g, st);
+    else launch_fmt<WF_F32>(W, X, ldx, M, bias, Y, ldy, epi, part, to_part, g, st);
+}
+
+hipError_t launch_gemv_partials(const DevMatrix &W, const float *X, int ldx, int M, const PartialBuf &s, int *splits,
+                                hipStream_t st) {
+    if (M <= 0 || M > GEMV_MAX_M || W.K % 32 || ldx < W.K || ldx % 4) return hipErrorInvalidValue;
+    const GemvGrid g = gemv_grid(W.N, W.K);
+    if (!s.part || s.floats < (size_t)g.splits * M * W.N) return hipErrorInvalidValue;
+    launch_any(W, X, ldx, M, nullptr, nullptr, 0, EPI_NONE, s.part, 1, g, st);
+    *splits = g.splits;
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const float *bias, float *Y, int ldy,
@@ -223,12 +251,10 @@ hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const
         return hipErrorInvalidValue;
     const GemvGrid g = gemv_grid(W.N, W.K);
     if (g.splits > 1 && (!s.part || s.floats < (size_t)g.splits * M * W.N)) return hipErrorInvalidValue;
-    if (W.fmt == WF_Q8) launch_fmt<WF_Q8>(W, X, ldx, M, bias, Y, ldy, epi, s.part, g, st);
-    else if (W.fmt == WF_Q4) launch_fmt<WF_Q4>(W, X, ldx, M, bias, Y, ldy, epi, s.part, g, st);
-    else launch_fmt<WF_F32>(W, X, ldx, M, bias, Y, ldy, epi, s.part, g, st);
+    launch_any(W, X, ldx, M, bias, Y, ldy, epi, s.part, 0, g, st);
     if (g.splits > 1)
-        hipLaunchKernelGGL(k_gemv_reduce, dim3((M * W.N + 255) / 256), dim3(256), 0, st, s.part, g.splits, M, W.N,
-                           bias, Y, ldy, epi);
+        hipLaunchKernelGGL(k_gemv_reduce, dim3((M * W.N * 8 + 255) / 256), dim3(256), 0, st, s.part, g.splits, M,
+                           W.N, bias, Y, ldy, epi);
     return hipGetLastError();
 }
 

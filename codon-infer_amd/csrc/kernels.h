@@ -69,6 +69,10 @@ GemvGrid gemv_grid(int N, int K);
 size_t gemv_part_floats(int N, int K);  // partial-sum floats needed at M = GEMV_MAX_M
 hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const float *bias, float *Y, int ldy,
                        int epi, const PartialBuf &pb, hipStream_t st);
+// The GEMV without its reduction: pb receives [*splits][M][N] partial sums
+// (no bias) for a consumer that adds them itself.
+hipError_t launch_gemv_partials(const DevMatrix &W, const float *X, int ldx, int M, const PartialBuf &pb, int *splits,
+                                hipStream_t st);
 
 // Dequantizes nblocks of a device matrix in k-block-major layout back to the
 // reference's row-major [N][K] FP32 (test path).
@@ -148,9 +152,12 @@ hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *ro
 // Both steps in one launch when every slot appears at most once among the
 // rows (one new token per sequence): each (row, head) workgroup rotates its
 // head's Q and K, writes K and V at pos, and attends with key pos from LDS.
-hipError_t launch_decode_attention_fused(float *qkv, int d, int H, const int *rows, int n, int max_len,
-                                         const float *rope_c, const float *rope_s, float *kc, float *vc,
-                                         int64_t slot_stride, float *out, hipStream_t st);
+// With part != nullptr the rows' Q|K|V come as [splits][n][3d] GEMV partial
+// sums (launch_gemv_partials) plus bias, added in split order; qkv is unused.
+hipError_t launch_decode_attention_fused(float *qkv, const float *part, int splits, const float *bias, int d, int H,
+                                         const int *rows, int n, int max_len, const float *rope_c,
+                                         const float *rope_s, float *kc, float *vc, int64_t slot_stride, float *out,
+                                         hipStream_t st);
 size_t decode_attention_lds(int hd, int max_len);  // dynamic LDS bytes per workgroup
 
 // Copies packed rows [T][width] into padded [B][S_max][width] (valid rows only).

@@ -127,6 +127,11 @@ struct ProfScope {
 void free_list(std::vector<void *> &l);
 int check_config(const cih_config *c);
 
+// algorithmic bytes of a weight matrix
+double wbytes(const DevMatrix &W);
+// A few FP32 rows go to the weight-streaming GEMV (CIH_GEMV=0 turns it off).
+bool use_gemv(int M, int a_fmt, int epi);
+
 // Y = epi(X W^T + bias) on the model's stream: the weight-streaming GEMV for
 // a few FP32 rows, the MFMA GEMM otherwise; partial sums through pb.
 hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, const void *X, int ldx, int a_fmt,
