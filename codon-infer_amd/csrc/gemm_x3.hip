@@ -41,6 +41,9 @@ namespace cih {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+// staging registers as a plain vector type (the struct-with-union uint4 kept
+// the prefetch arrays in scratch memory)
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 enum Limb { LIMB_BF16X3 = 0, LIMB_F16X2 = 1 };
 template <int LIMB> struct LimbT;
@@ -152,55 +155,50 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     const int KB = K / 32;
 
     // two register stages: block kb+2 is in flight while block kb is multiplied
-    uint4 ra[2][A_LOADS];
-    uint4 rb[2][B_LOADS];  // Q8: 16 bytes (elements 16*part..+15); Q4: 8 bytes in .x/.y
+    u32x4 ra[2][A_LOADS];
+    u32x4 rb[2][B_LOADS];  // Q8: 16 bytes (elements 16*part..+15); Q4: 8 bytes in .x/.y
     float rs[2];
 
-    auto gload = [&](int kb, uint4 (&a)[A_LOADS], uint4 (&b)[B_LOADS], float &sc) {
+    // Every load is unconditional: rows past M and columns past N read the
+    // last row / column instead (their outputs are never stored), so the
+    // compiler can count outstanding loads and keep the newer stage in
+    // flight while the older one is waited for.
+    auto gload = [&](int kb, u32x4 (&a)[A_LOADS], u32x4 (&b)[B_LOADS], float &sc) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < A_LOADS; i++) {
             if constexpr (AF == AF_X3) {
                 const int c = tid + 256 * i, row = c / 12, part = c % 12;
-                const int gr = m0 + row;
-                a[i] = gr < M ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const unsigned short *>(Xv) +
-                                                                 ((size_t)gr * KB + kb) * 96 + part * 8)
-                              : make_uint4(0, 0, 0, 0);
+                const int gr = min(m0 + row, M - 1);
+                a[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const unsigned short *>(Xv) +
+                                                        ((size_t)gr * KB + kb) * 96 + part * 8);
             } else if constexpr (AF == AF_H2) {
                 const int row = (tid >> 3) + 32 * i, part = tid & 7;
-                const int gr = m0 + row;
-                a[i] = gr < M ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const unsigned short *>(Xv) +
-                                                                 ((size_t)gr * KB + kb) * 64 + part * 8)
-                              : make_uint4(0, 0, 0, 0);
+                const int gr = min(m0 + row, M - 1);
+                a[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const unsigned short *>(Xv) +
+                                                        ((size_t)gr * KB + kb) * 64 + part * 8);
             } else {
                 const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
-                const int gr = m0 + row;
-                a[i] = gr < M ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(Xv) +
-                                                                 (size_t)gr * ldx + kb * 32 + c4 * 4)
-                              : make_uint4(0, 0, 0, 0);
+                const int gr = min(m0 + row, M - 1);
+                a[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(Xv) + (size_t)gr * ldx +
+                                                        kb * 32 + c4 * 4);
             }
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; i++) {
             const int idx = tid + 256 * i, col = idx >> 1, part = idx & 1;
-            const int gc = n0 + col;
+            const int gc = min(n0 + col, N - 1);
             const unsigned char *src = reinterpret_cast<const unsigned char *>(Wq) + ((size_t)kb * N + gc) * QB;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (idx < B_ITEMS && gc < N) {
-                if constexpr (WF == WF_Q8) {
-                    v = *reinterpret_cast<const uint4 *>(src + part * 16);
-                } else {
-                    const uint2 h = *reinterpret_cast<const uint2 *>(src + part * 8);
-                    v.x = h.x;
-                    v.y = h.y;
-                }
+            if constexpr (WF == WF_Q8) {
+                b[i] = *reinterpret_cast<const u32x4 *>(src + part * 16);
+            } else {
+                const uint2 h = *reinterpret_cast<const uint2 *>(src + part * 8);
+                b[i] = u32x4{h.x, h.y, 0u, 0u};
             }
-            b[i] = v;
         }
-        const int gc = n0 + tid;
-        sc = (tid < BN && gc < N) ? Wsc[(size_t)kb * N + gc] : 0.0f;
+        sc = Wsc[(size_t)kb * N + min(n0 + min(tid, BN - 1), N - 1)];
     };
 
-    auto sstore = [&](int stg, const uint4 (&a)[A_LOADS], const uint4 (&b)[B_LOADS], float sc) {
+    auto sstore = [&](int stg, const u32x4 (&a)[A_LOADS], const u32x4 (&b)[B_LOADS], float sc) __attribute__((always_inline)) {
         unsigned short *Al = Al2[stg], *Bl = Bl2[stg];
         float *Ss = Ss2[stg];
 #pragma unroll
@@ -208,11 +206,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
             if constexpr (AF == AF_X3) {
                 // chunk part p of a row = bf16 elements 8p..8p+7 of [limb0|limb1|limb2]
                 const int c = tid + 256 * i, row = c / 12, part = c % 12;
-                *reinterpret_cast<uint4 *>(&Al[row * AROW + part * 8]) = a[i];
+                *reinterpret_cast<u32x4 *>(&Al[row * AROW + part * 8]) = a[i];
             } else if constexpr (AF == AF_H2) {
                 // chunk part p of a row = f16 elements 8p..8p+7 of [hi|lo]
                 const int row = (tid >> 3) + 32 * i, part = tid & 7;
-                *reinterpret_cast<uint4 *>(&Al[row * AROW + part * 8]) = a[i];
+                *reinterpret_cast<u32x4 *>(&Al[row * AROW + part * 8]) = a[i];
             } else {
                 const int row = (tid >> 3) + 32 * i, c4 = tid & 7;
                 const float4 xv = make_float4(__uint_as_float(a[i].x), __uint_as_float(a[i].y),
@@ -246,8 +244,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                     o[2 * p] = sub1152(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
                     o[2 * p + 1] = sub1152(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
                 }
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16]) = make_uint4(o[0], o[1], o[2], o[3]);
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16 + 8]) = make_uint4(o[4], o[5], o[6], o[7]);
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + part * 16]) = u32x4{o[0], o[1], o[2], o[3]};
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + part * 16 + 8]) = u32x4{o[4], o[5], o[6], o[7]};
             } else if constexpr (WF == WF_Q8) {
                 // 16 int8 = elements 16*part .. 16*part+15, exact in bf16
                 unsigned o[8];
@@ -258,8 +256,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                     o[p] = pack_int<LIMB>((float)(signed char)((word >> sh) & 0xFF),
                                           (float)(signed char)((word >> (sh + 8)) & 0xFF));
                 }
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16]) = make_uint4(o[0], o[1], o[2], o[3]);
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 16 + 8]) = make_uint4(o[4], o[5], o[6], o[7]);
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + part * 16]) = u32x4{o[0], o[1], o[2], o[3]};
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + part * 16 + 8]) = u32x4{o[4], o[5], o[6], o[7]};
             } else if constexpr (LIMB == LIMB_F16X2) {
                 // 8 bytes = elements 8*part+e (low nibble) and 16+8*part+e (high nibble);
                 // nibble n under the f16 exponent of 1024 reads as 1024 + n, minus 1032 = n - 8
@@ -272,8 +270,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                     hi[2 * p] = sub1032(__builtin_amdgcn_perm(0x64646464u, nh, 0x04010400u));
                     hi[2 * p + 1] = sub1032(__builtin_amdgcn_perm(0x64646464u, nh, 0x04030402u));
                 }
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 8]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + 16 + part * 8]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + part * 8]) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + 16 + part * 8]) = u32x4{hi[0], hi[1], hi[2], hi[3]};
             } else {
                 // 8 bytes = elements 8*part+e (low nibble) and 16+8*part+e (high nibble)
                 unsigned lo[4], hi[4];
@@ -285,8 +283,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                     lo[p] = pack_int<LIMB>((float)((int)(b0 & 0xF) - 8), (float)((int)(b1 & 0xF) - 8));
                     hi[p] = pack_int<LIMB>((float)((int)(b0 >> 4) - 8), (float)((int)(b1 >> 4) - 8));
                 }
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + part * 8]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-                *reinterpret_cast<uint4 *>(&Bl[col * XL + 16 + part * 8]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + part * 8]) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + 16 + part * 8]) = u32x4{hi[0], hi[1], hi[2], hi[3]};
             }
         }
         if (tid < BN) Ss[tid] = sc;
@@ -300,7 +298,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
 
-    auto compute = [&](int stg) {
+    auto compute = [&](int stg) __attribute__((always_inline)) {
         const unsigned short *Al = Al2[stg], *Bl = Bl2[stg];
         const float *Ss = Ss2[stg];
         // A operands of this wave's rows for both k-halves and all limbs
@@ -347,19 +345,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
 
     // k-blocks [kb0, kend) of this split (all of K without split-K)
     const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kend = SPLIT ? min(KB, kb0 + kps) : KB;
+    // Prefetches past the last block re-read the last block (unused), so every
+    // path issues the same loads and the waits count only the older stage.
     gload(kb0, ra[0], rb[0], rs[0]);
-    if (kb0 + 1 < kend) gload(kb0 + 1, ra[1], rb[1], rs[1]);
+    gload(min(kb0 + 1, kend - 1), ra[1], rb[1], rs[1]);
     for (int kb = kb0; kb < kend; kb += 2) {
         // Stage 0 was last read by compute(kb - 2); every wave finished that before the
         // previous iteration's barrier, so one barrier per block suffices.
         sstore(0, ra[0], rb[0], rs[0]);
         __syncthreads();
-        if (kb + 2 < kend) gload(kb + 2, ra[0], rb[0], rs[0]);
+        gload(min(kb + 2, kend - 1), ra[0], rb[0], rs[0]);
         compute(0);
         if (kb + 1 >= kend) break;
         sstore(1, ra[1], rb[1], rs[1]);
         __syncthreads();
-        if (kb + 3 < kend) gload(kb + 3, ra[1], rb[1], rs[1]);
+        gload(min(kb + 3, kend - 1), ra[1], rb[1], rs[1]);
         compute(1);
     }
 
