@@ -58,7 +58,20 @@ int check_config(const cih_config *c) {
 
 namespace {
 
+void clear_graphs(Workspace &ws) {
+    for (auto &g : ws.graphs) hipGraphExecDestroy(g.second);
+    ws.graphs.clear();
+}
+
+// Forwards replay captured graphs unless profiling (event pairs per launch)
+// or CIH_FORWARD_GRAPH=0.
+bool use_forward_graph(const cih_model *m) {
+    const char *e = getenv("CIH_FORWARD_GRAPH");
+    return !m->prof.on && !(e && !std::strcmp(e, "0"));
+}
+
 void free_workspace(Workspace &ws) {
+    clear_graphs(ws);
     free_list(ws.dev);
     for (void *p : ws.host) hipHostFree(p);
     ws.host.clear();
@@ -322,11 +335,16 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     const int epi_fc1 = af == AF_X3 ? EPI_GELU_X3 : (af == AF_H2 ? EPI_GELU_H2 : EPI_GELU);
 
     m->prof.used = 0;
+    // the contact accumulator is cleared outside the (possibly captured) kernel sequence
+    if (want_contacts) HIPCHK(hipMemsetAsync(ws.M, 0, (size_t)B * n_max * n_max * 4, st));
+
+    // Everything from the embedding to the output scatters is kernel
+    // launches only; a shape seen before replays a captured graph of it.
+    auto enqueue = [&]() -> int {
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
         HIPCHK(launch_embed(ws.tokens, sm, m->emb.fmt, m->emb.q, m->emb.sc, d, V, ws.x, st));
     }
-    if (want_contacts) HIPCHK(hipMemsetAsync(ws.M, 0, (size_t)B * n_max * n_max * 4, st));
 
     for (int l = 0; l < L; l++) {
         const Layer &ly = m->layers[l];
@@ -393,6 +411,35 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             HIPCHK(gemm(m, m->emb, ws.ao, d, AF_F32, nullptr, ws.logits, V, T, EPI_NONE));
         }
         if (want_logits) HIPCHK(launch_scatter_rows(ws.logits, V, sm, t_logits, (int64_t)S_max * V, st));
+    }
+    return 0;
+    };
+    if (!use_forward_graph(m)) {
+        if (int rc = enqueue()) return rc;
+    } else {
+        // the shape fixes every grid and pointer of the sequence: batch,
+        // padded length, token count, outputs and their destinations
+        const FwdGraphKey key{B, S_max, T, flags | (keep_logits ? 1u << 31 : 0u),
+                              {t_logits, t_hidden, t_final, t_contacts, t_attn, t_layer}};
+        hipGraphExec_t ex = nullptr;
+        for (auto &g : ws.graphs)
+            if (g.first == key) ex = g.second;
+        if (!ex) {
+            if (ws.graphs.size() >= 16) clear_graphs(ws);
+            hipGraph_t g = nullptr;
+            HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            const int rc = enqueue();
+            const hipError_t e = hipStreamEndCapture(st, &g);
+            if (rc || e != hipSuccess) {
+                if (g) hipGraphDestroy(g);
+                return rc ? rc : set_error(CIH_ERR_HIP, "forward capture failed: %s", hipGetErrorString(e));
+            }
+            const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            hipGraphDestroy(g);
+            if (ei != hipSuccess) return set_error(CIH_ERR_HIP, "forward graph: %s", hipGetErrorString(ei));
+            ws.graphs.emplace_back(key, ex);
+        }
+        HIPCHK(hipGraphLaunch(ex, st));
     }
     HIPCHK(hipStreamSynchronize(st));
 

@@ -23,6 +23,19 @@ struct Layer {
     float *ln1w = nullptr, *ln1b = nullptr, *ln2w = nullptr, *ln2b = nullptr;
 };
 
+// What fixes a forward's kernel sequence: grids and pointers.
+struct FwdGraphKey {
+    int B = 0, S_max = 0, T = 0;
+    uint32_t flags = 0;
+    const void *out[6] = {};
+    bool operator==(const FwdGraphKey &o) const {
+        if (B != o.B || S_max != o.S_max || T != o.T || flags != o.flags) return false;
+        for (int i = 0; i < 6; i++)
+            if (out[i] != o.out[i]) return false;
+        return true;
+    }
+};
+
 struct Workspace {
     int maxB = 0, maxS = 0;
     uint32_t flags = 0;
@@ -40,6 +53,8 @@ struct Workspace {
     float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
           *o_layer = nullptr;
     std::vector<void *> dev, host;
+    // captured forwards, by shape
+    std::vector<std::pair<FwdGraphKey, hipGraphExec_t>> graphs;
 };
 
 struct Prof {

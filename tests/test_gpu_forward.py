@@ -219,6 +219,39 @@ def test_forward_few_tokens(dtype, gemv, monkeypatch):
         check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(0.25)))
 
 
+@pytest.mark.parametrize("T", [8, 40])
+def test_forward_graph_replays_match_eager(T, monkeypatch):
+    """Forwards of a shape seen before replay a captured graph (keyed by
+    batch, padded length, token count and outputs).  Different lengths with
+    the same token count reuse one graph; every replay, with eager forwards
+    and host syncs in between, equals the kernel-by-kernel run bit for bit."""
+    rng = np.random.default_rng(T)
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=T, bias_std=0.02).quantize_q8()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_CONTACTS | ch.OUT_FINAL_ATT
+    half = T // 2
+    splits = [(half + 1, T - half - 1), (half, T - half), (half - 1, T - half + 1), (half, T - half)]
+    S_max = T - half + 1
+    mg = ch.GpuModel(cfg, w, contact_head=(cw, 0.3), max_batch=2, max_len=S_max, outputs=flags)
+    me = ch.GpuModel(cfg, w, contact_head=(cw, 0.3), max_batch=2, max_len=S_max, outputs=flags)
+    for a, b in splits:
+        seqs = [rand_tokens(rng, a - 2), rand_tokens(rng, b - 2)]
+        monkeypatch.setenv("CIH_FORWARD_GRAPH", "1")
+        got = mg.forward(seqs, flags)
+        monkeypatch.setenv("CIH_FORWARD_GRAPH", "0")
+        ref = me.forward(seqs, flags)
+        for k in ("logits", "hidden", "contacts", "final_att"):
+            for i, s in enumerate(seqs):
+                n = len(s)
+                g, r = got[k][i], ref[k][i]
+                g, r = (g[:n - 2, :n - 2], r[:n - 2, :n - 2]) if k == "contacts" else \
+                       ((g[:n, :n], r[:n, :n]) if k == "final_att" else (g[:n], r[:n]))
+                assert np.array_equal(g, r), (T, a, b, k)
+    mg.close()
+    me.close()
+
+
 def test_tied_embedding_decoder():
     """A classifier shorter than the LM head selects logits = x . emb^T
     (lib.rs:5427-5439, Q8: 5775-5787)."""
