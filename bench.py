@@ -83,6 +83,23 @@ def measured_traffic(name):
     return None, None
 
 
+def copy_probe(hip, mb):
+    """One device-to-device copy of mb MiB: the known-size transfer the
+    FETCH_SIZE / WRITE_SIZE counters are calibrated against."""
+    nbytes = mb << 20
+    src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+    hip.L.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3)
+    hip.sync()
+    hip.free(src)
+    hip.free(dst)
+
+
+def kernel_overrides():
+    """CIH_* switches that change which kernels run (graph replay switches
+    only change how the same kernels are launched)."""
+    return any(k.startswith("CIH_") and k not in ("CIH_FORWARD_GRAPH", "CIH_DECODE_GRAPH") for k in os.environ)
+
+
 def physical_cores():
     try:
         with open("/proc/cpuinfo") as f:
@@ -181,6 +198,8 @@ def decode_bench(args, ch):
     w = w.quantize_q8() if args.dtype == "q8" else (w.quantize_q4() if args.dtype == "q4" else w)
     n, P, K = args.streams, 16, args.new_tokens
     model = ch.GpuModel(cfg, w, max_batch=1, max_len=16)
+    if args.copy_probe_mb:
+        copy_probe(Hip(), args.copy_probe_mb)
     dec = ch.GpuDecoder(model, n_slots=n, max_len=cfg.max_seq_len, max_rows=max(16, n))
     assert P + args.warmup + K <= cfg.max_seq_len
     rng = np.random.default_rng(7)
@@ -221,6 +240,9 @@ def decode_bench(args, ch):
     f = model.profile_read(ch.KC_GEMM_FP32) if args.dtype != "fp32" else {"total_ms": 0.0, "bytes": 0.0}
     gbs = q["bytes"] / (q["total_ms"] * 1e-3) / 1e9 if q["total_ms"] > 0 else 0.0
     step_bytes = (q["bytes"] + a["bytes"] + o["bytes"] + f["bytes"]) / K_prof
+    traffic, traffic_src = (None, None)
+    if not kernel_overrides() and (args.model, args.dtype, n) == ("650M", "q4", 1):
+        traffic, traffic_src = measured_traffic("gemv_decode_q4_650m.md")
     ms = el * 1e3 / K
     line = {
         "metric": f"decode tokens/s ESM-2 {args.model} {args.dtype} ({n} stream{'s' if n > 1 else ''})",
@@ -233,7 +255,8 @@ def decode_bench(args, ch):
                    "streams": n, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "k_gemv (weights streamed once per step for all streams)",
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "timing": TIMING},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                     "timing": TIMING},
         "step_breakdown_ms": {"gemv": round(q["total_ms"] / K_prof, 4),
                               "attention": round(a["total_ms"] / K_prof, 4),
                               "other": round(o["total_ms"] / K_prof, 4),
@@ -400,12 +423,7 @@ def main():
         outs["attn"] = hip.malloc(B * cfg.n_layers * cfg.n_heads * S * S * 4)
         extra.append(outs["attn"])
     if args.copy_probe_mb:
-        nbytes = args.copy_probe_mb << 20
-        src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
-        hip.L.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3)
-        hip.sync()
-        hip.free(src)
-        hip.free(dst)
+        copy_probe(hip, args.copy_probe_mb)
     print(f"[bench] model resident ({time.perf_counter() - t0:.1f} s); warmup {args.warmup}", file=sys.stderr,
           flush=True)
 
@@ -454,7 +472,7 @@ def main():
         else:
             kname, peak, limbs = f"k_gemm_x3<{wname}> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)", PEAK_F16_MFMA_TFLOPS, 2
     # traffic from the committed PMC summary, for the workloads it was measured on
-    overrides = any(k.startswith("CIH_") for k in os.environ)
+    overrides = kernel_overrides()
     prof = None
     if not overrides and headline and (B, S) == (16, 512):
         prof = "gemm_q8_650m_b16_l512.md"

@@ -91,17 +91,45 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
     float *K = kc + slot * slot_stride + h * HD;
     float *V = vc + slot * slot_stride + h * HD;
     const int t = threadIdx.x;
+    const int n_cached = FUSED ? pos : pos + 1;  // keys read from the cache
+    // This thread's first key row is requested before anything waits, so its
+    // latency overlaps the gather, the rotation and the barriers.
+    float4 kfirst[HD / 4];
+    if (t < n_cached) {
+        const float4 *kr = reinterpret_cast<const float4 *>(K + (size_t)t * d);
+#pragma unroll
+        for (int i = 0; i < HD / 4; i++) kfirst[i] = kr[i];
+    }
+    // likewise the first four V rows of this lane's group (P.V below)
+    const int g = t / HD, i = t - g * HD;
+    float vfirst[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (g < G) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (g + u * G < n_cached) vfirst[u] = V[(size_t)(g + u * G) * d + i];
+    }
     if constexpr (FUSED) {
+        float c = 0.0f, s = 0.0f;
+        if (t < HALF) {
+            c = rc[(size_t)pos * HALF + t];
+            s = rs[(size_t)pos * HALF + t];
+        }
         // this head's q, k, v: the row of qkv, or the GEMV's partial sums
-        // (split order) + bias
+        // (eight interleaved sums over the splits) + bias
         if (t < 3 * HD) {
             const int which = t / HD, col = which * d + h * HD + (t - which * HD);
             float v;
             if (part) {
-                const int n = gridDim.x;
-                float acc = 0.0f;
-                for (int y = 0; y < splits; y++) acc += part[((size_t)y * n + r) * 3 * d + col];
-                v = acc + bias[col];
+                const size_t stride = (size_t)gridDim.x * 3 * d;
+                const float *pp = part + (size_t)r * 3 * d + col;
+                float a[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+                int y = 0;
+                for (; y + 8 <= splits; y += 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; u++) a[u] += pp[(y + u) * stride];
+                }
+                for (int u = 0; y < splits; y++, u++) a[u] += pp[y * stride];
+                v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + bias[col];
             } else {
                 v = qkv[(size_t)r * 3 * d + col];
             }
@@ -110,7 +138,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
         __syncthreads();
         // apply_rope (lib.rs:3533-3552) for this head, products rounded one by one
         if (t < HALF) {
-            const float c = rc[(size_t)pos * HALF + t], s = rs[(size_t)pos * HALF + t];
             const float q0 = qs[t], q1 = qs[t + HALF], k0 = kcur[t], k1 = kcur[t + HALF];
             qs[t] = __fsub_rn(__fmul_rn(q0, c), __fmul_rn(q1, s));
             qs[t + HALF] = __fadd_rn(__fmul_rn(q1, c), __fmul_rn(q0, s));
@@ -128,19 +155,25 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
         if (t < HD) qs[t] = q[t];
     }
     __syncthreads();
-    const int n_cached = FUSED ? pos : pos + 1;  // keys read from the cache
     float mx = -INFINITY;
     for (int j = t; j <= pos; j += ATT_THREADS) {
         float acc = 0.0f;
         if (j < n_cached) {
-            const float4 *kr = reinterpret_cast<const float4 *>(K + (size_t)j * d);
+            float4 kv4[HD / 4];
+            if (j == t) {
+#pragma unroll
+                for (int i = 0; i < HD / 4; i++) kv4[i] = kfirst[i];
+            } else {
+                const float4 *kr = reinterpret_cast<const float4 *>(K + (size_t)j * d);
+#pragma unroll
+                for (int i = 0; i < HD / 4; i++) kv4[i] = kr[i];
+            }
 #pragma unroll
             for (int i = 0; i < HD / 4; i++) {
-                const float4 kv = kr[i];
-                acc = fmaf(qs[4 * i], kv.x, acc);
-                acc = fmaf(qs[4 * i + 1], kv.y, acc);
-                acc = fmaf(qs[4 * i + 2], kv.z, acc);
-                acc = fmaf(qs[4 * i + 3], kv.w, acc);
+                acc = fmaf(qs[4 * i], kv4[i].x, acc);
+                acc = fmaf(qs[4 * i + 1], kv4[i].y, acc);
+                acc = fmaf(qs[4 * i + 2], kv4[i].z, acc);
+                acc = fmaf(qs[4 * i + 3], kv4[i].w, acc);
             }
         } else {
 #pragma unroll
@@ -160,11 +193,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
     sum = block_reduce(sum, red, false);
     const float inv = 1.0f / sum;
     __syncthreads();
-    const int g = t / HD, i = t - g * HD;
     if (g < G) {
         const float *vi = V + i;
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-        int j = g;
+        // rows g, g+G, g+2G, g+3G from the registers, then four at a time
+        if (g < n_cached) a0 = p[g] * inv * vfirst[0];
+        if (g + G < n_cached) a1 = p[g + G] * inv * vfirst[1];
+        if (g + 2 * G < n_cached) a2 = p[g + 2 * G] * inv * vfirst[2];
+        if (g + 3 * G < n_cached) a3 = p[g + 3 * G] * inv * vfirst[3];
+        int j = g + 4 * G;
         for (; j + 3 * G < n_cached; j += 4 * G) {
             const float v0 = vi[(size_t)j * d], v1 = vi[(size_t)(j + G) * d];
             const float v2 = vi[(size_t)(j + 2 * G) * d], v3 = vi[(size_t)(j + 3 * G) * d];
@@ -174,7 +211,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
             a3 = fmaf(p[j + 3 * G] * inv, v3, a3);
         }
         for (; j < n_cached; j += G) a0 = fmaf(p[j] * inv, vi[(size_t)j * d], a0);
-        if (FUSED && j == pos) a0 = fmaf(p[j] * inv, vcur[i], a0);
+        if (FUSED && pos >= g && (pos - g) % G == 0) a0 = fmaf(p[pos] * inv, vcur[i], a0);
         gsum[g * HD + i] = (a0 + a1) + (a2 + a3);
     }
     __syncthreads();
