@@ -1,0 +1,280 @@
+// Quantized GEMM with operands staged global -> LDS by the load unit:
+//   Y = epi(X * W^T + b),  X in f16 limbs (AF_H2), W in Q8_0 / Q4_0 blocks of 32.
+//
+// Arithmetic is that of k_gemm_x3 with LIMB_F16X2 (gemm_x3.hip), operation
+// for operation: per 32-wide block, tmp = sum over both limbs and both
+// k-halves of limb x quant on v_mfma_f32_32x32x16_f16 (exact products, FP32
+// accumulation in the same order), then acc += d * tmp.  Results are
+// bit-identical to that kernel; it replaces matmul_tiled_q8/q4_parallel
+// (codon-infer src/lib.rs:4870, 4937) on the large bidirectional batches.
+//
+// What differs is the data movement:
+//   * the quants come from W.q16, an f16 copy made when the model is loaded,
+//     so no conversion runs in the loop and both operands are plain copies;
+//   * every k-block of A (BM rows x 128 B: 32 hi + 32 lo f16) and of W.q16
+//     (BN columns x 64 B) plus its BN scales is fetched with
+//     global_load_lds_dword{,x4}: the load unit writes LDS directly, nothing
+//     passes through registers;
+//   * three LDS stages: while block kb is multiplied, blocks kb+1 and kb+2
+//     are in flight; one barrier per block;
+//   * LDS layouts are swizzled for gfx950's LDS (64 banks of 4 bytes, a
+//     ds_read_b128 served 16 lanes at a time): 16-byte chunk c of A row r sits
+//     at chunk c ^ ((r >> 1) & 7), chunk c of W column n at c ^ ((n >> 2) & 3),
+//     so the 16 lanes of each MFMA operand read hit 16 distinct bank groups.
+//
+// Workgroup: (BM/64) x (BN/64) waves, each owning a 64 x 64 output tile
+// (2 x 2 MFMA tiles of 32 x 32); 128 x 128 (4 waves, two workgroups per CU)
+// or 128 x 256 (8 waves, one per CU).
+#include <stdlib.h>
+#include <string.h>
+
+#include "kernels.h"
+#include "x3.h"
+
+namespace cih {
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_ptr_t;
+typedef __attribute__((address_space(1))) void glb_ptr_t;
+
+template <int BM, int BN> struct LdsTile {
+    static constexpr int WN = BN / 64, NW = (BM / 64) * WN, THREADS = 64 * NW;
+    static constexpr int SA = BM * 128, SB = BN * 64, SS = BN * 4, STAGE = SA + SB + SS;
+    static constexpr int NA = SA / 1024 / NW;  // 16-byte-per-lane loads of A per wave and block
+    static constexpr int NB = SB / 1024 / NW;  // ... of W
+    static constexpr int SL = BN / NW;         // scales per wave and block (4-byte loads)
+    static constexpr int NI = NA + NB + 1;     // load instructions per wave and block
+    static_assert(NA >= 1 && NB >= 1 && SL <= 64 && SA % (1024 * NW) == 0 && SB % (1024 * NW) == 0, "tile");
+};
+
+template <int EPI, int BM, int BN>
+__global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>::THREADS)) void k_gemm_lds(
+    const unsigned short *__restrict__ X, const unsigned short *__restrict__ W16, const float *__restrict__ Wsc,
+    const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K) {
+    using T = LdsTile<BM, BN>;
+    constexpr int SA = T::SA, SB = T::SB, STAGE = T::STAGE, NA = T::NA, NB = T::NB, SL = T::SL;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[3 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / T::WN, wn = wave % T::WN;
+    const int li = lane & 31, hh = lane >> 5;
+    const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+    int mt, nt;
+    tile_xcd(blockIdx.x, nM * nN, nM, nN, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int KB = K / 32;
+
+    // Per-lane sources at k-block 0.  Load i of a wave fills LDS bytes
+    // [(wave * NA + i) * 1024, +1024) of the stage, lane l the 16 bytes at
+    // l * 16: LDS chunk p holds the (row, chunk) whose swizzled position is p.
+    // Rows past M and columns past N read the last row / column (never stored).
+    const unsigned short *srcA[NA];
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+        const int p = (wave * NA + i) * 64 + lane;
+        const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
+        srcA[i] = X + (size_t)min(m0 + row, M - 1) * KB * 64 + chunk * 8;
+    }
+    const unsigned short *srcB[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int p = (wave * NB + i) * 64 + lane;
+        const int col = p >> 2, chunk = (p & 3) ^ ((col >> 2) & 3);
+        srcB[i] = W16 + (size_t)min(n0 + col, N - 1) * 32 + chunk * 8;
+    }
+    const float *srcS = Wsc + min(n0 + wave * SL + min(lane, SL - 1), N - 1);
+
+    auto request = [&](int kb, int stg) __attribute__((always_inline)) {
+        unsigned char *base = lds + stg * STAGE;
+#pragma unroll
+        for (int i = 0; i < NA; i++)
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcA[i] + (size_t)kb * 64),
+                                             (lds_ptr_t *)(base + (wave * NA + i) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcB[i] + (size_t)kb * N * 32),
+                                             (lds_ptr_t *)(base + SA + (wave * NB + i) * 1024), 16, 0, 0);
+        if (lane < SL)
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcS + (size_t)kb * N),
+                                             (lds_ptr_t *)(base + SA + SB + wave * SL * 4), 4, 0, 0);
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
+
+    const int swA = (li >> 1) & 7, swB = (li >> 2) & 3;
+    auto compute = [&](int stg) __attribute__((always_inline)) {
+        const unsigned char *base = lds + stg * STAGE;
+        f16x8 a[2][2][2];  // [k-half][limb][row tile]
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int l = 0; l < 2; l++)
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const int row = wm * 64 + r * 32 + li, chunk = l * 4 + kh * 2 + hh;
+                    a[kh][l][r] = *reinterpret_cast<const f16x8 *>(base + row * 128 + ((chunk ^ swA) << 4));
+                }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int col = wn * 64 + c * 32 + li;
+            f32x16 tmp[2];
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++) {
+                const f16x8 b = *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((kh * 2 + hh) ^ swB) << 4));
+#pragma unroll
+                for (int l = 0; l < 2; l++)
+#pragma unroll
+                    for (int r = 0; r < 2; r++) {
+                        f32x16 cc;
+                        if (kh == 0 && l == 0) {
+#pragma unroll
+                            for (int q = 0; q < 16; q++) cc[q] = 0.0f;
+                        } else {
+                            cc = tmp[r];
+                        }
+                        tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kh][l][r], b, cc, 0, 0, 0);
+                    }
+            }
+            const float d = *reinterpret_cast<const float *>(base + SA + SB + col * 4);
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) acc[r][c][q] += d * tmp[r][q];
+        }
+    };
+
+    // Before reading block kb: this wave's loads of kb have landed (those of
+    // kb+1 may still be in flight: NI newer instructions), its own LDS reads
+    // are done, and all waves meet.  After the barrier the stage of kb-1 is
+    // free for kb+2.  The load unit's LDS writes are invisible to the
+    // compiler, hence the explicit counts and the memory clobber.
+    auto sync = [&]() __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(T::NI) : "memory");
+    };
+    // Requests past the last block re-read it into a stage nobody reads again,
+    // so every wave issues the same instructions and the counts hold.
+    request(0, 0);
+    request(min(1, KB - 1), 1);
+    for (int kb = 0;;) {
+        sync();
+        request(min(kb + 2, KB - 1), 2);
+        compute(0);
+        if (++kb == KB) break;
+        sync();
+        request(min(kb + 2, KB - 1), 0);
+        compute(1);
+        if (++kb == KB) break;
+        sync();
+        request(min(kb + 2, KB - 1), 1);
+        compute(2);
+        if (++kb == KB) break;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int col = n0 + wn * 64 + c * 32 + li;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int row = m0 + wm * 64 + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                if (row < M) {
+                    float v = acc[r][c][q] + bv;
+                    if constexpr (EPI == EPI_GELU_H2) {
+                        h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
+                    } else {
+                        float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
+                        if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+                        *dst = v;
+                    }
+                }
+            }
+    }
+}
+
+// q16[kb][n][j] = f16 of quant j of block (kb, n): Q8_0 bytes as signed
+// integers; Q4_0 element j < 16 the low nibble of byte j, j >= 16 the high
+// nibble of byte j - 16, minus 8 (the reference's nibble order).
+template <int WF>
+__global__ __launch_bounds__(256) void k_expand_f16(const unsigned char *__restrict__ q, unsigned short *__restrict__ q16,
+                                                    int64_t blocks) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one element
+    if (i >= blocks * 32) return;
+    const int64_t blk = i >> 5;
+    const int j = (int)(i & 31);
+    int v;
+    if constexpr (WF == WF_Q8) {
+        v = (signed char)q[blk * 32 + j];
+    } else {
+        const unsigned b = q[blk * 16 + (j & 15)];
+        v = (int)(j < 16 ? (b & 15u) : (b >> 4)) - 8;
+    }
+    q16[i] = __builtin_bit_cast(unsigned short, (_Float16)(float)v);
+}
+
+template <int EPI, int BM, int BN>
+hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
+    const int tiles = ((M + BM - 1) / BM) * ((W.N + BN - 1) / BN);
+    hipLaunchKernelGGL((k_gemm_lds<EPI, BM, BN>), dim3(tiles), dim3(LdsTile<BM, BN>::THREADS), 0, st,
+                       reinterpret_cast<const unsigned short *>(X), W.q16, W.sc, bias, Y, ldy, M, W.N, W.K);
+    return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
+    // 128 x 256 when it still yields two rounds of workgroups (one per CU), else 128 x 128
+    const long wide = (long)((M + 127) / 128) * ((W.N + 255) / 256);
+    if (wide >= 512) return launch_t<EPI, 128, 256>(W, X, bias, Y, ldy, M, st);
+    return launch_t<EPI, 128, 128>(W, X, bias, Y, ldy, M, st);
+}
+
+}  // namespace
+
+bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi) {
+    if (!W.q16 || a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || W.K % 32 || M <= 0) return false;
+    if (epi != EPI_NONE && epi != EPI_RESIDUAL && epi != EPI_GELU_H2) return false;
+    const char *e = getenv("CIH_GEMM_LDS");
+    if (e && !strcmp(e, "0")) return false;
+    if (e && !strcmp(e, "force")) return true;
+    return (long)((M + 127) / 128) * ((W.N + 127) / 128) >= 256;
+}
+
+hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
+                           hipStream_t st) {
+    if (!W.q16 || W.K % 32 || W.K <= 0 || M <= 0 || W.N <= 0) return hipErrorInvalidValue;
+    if (epi == EPI_GELU_H2 && W.N % 32) return hipErrorInvalidValue;
+    switch (epi) {
+    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st);
+    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st);
+    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_expand_f16(const DevMatrix &W, unsigned short *q16, hipStream_t st) {
+    if (W.fmt != WF_Q8 && W.fmt != WF_Q4) return hipErrorInvalidValue;
+    const int64_t blocks = (int64_t)(W.K / 32) * W.N;
+    if (blocks == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((blocks * 32 + 255) / 256);
+    if (W.fmt == WF_Q8)
+        hipLaunchKernelGGL(k_expand_f16<WF_Q8>, dim3(grid), dim3(256), 0, st,
+                           reinterpret_cast<const unsigned char *>(W.q), q16, blocks);
+    else
+        hipLaunchKernelGGL(k_expand_f16<WF_Q4>, dim3(grid), dim3(256), 0, st,
+                           reinterpret_cast<const unsigned char *>(W.q), q16, blocks);
+    return hipGetLastError();
+}
+
+}  // namespace cih

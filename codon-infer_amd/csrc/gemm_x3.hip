@@ -111,20 +111,6 @@ __device__ __forceinline__ unsigned pack_int(float lo, float hi) {
     else return pack_exact(lo, hi);
 }
 
-__device__ __forceinline__ void tile_of3(int bid, int total, int nM, int nN, int &mt, int &nt) {
-    constexpr int XCD = 8, GROUP_M = 8;
-    int xcd = bid % XCD, local = bid / XCD;
-    int per = total / XCD, rem = total % XCD;
-    int id = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-    int in_group = GROUP_M * nN;
-    int g = id / in_group;
-    int first = g * GROUP_M;
-    int gsize = min(nM - first, GROUP_M);
-    int r = id % in_group;
-    mt = first + r % gsize;
-    nt = r / gsize;
-}
-
 template <int WF, int EPI, int BM, int BN, int AF, int LIMB, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv, int ldx,
                                                     const void *__restrict__ Wq, const float *__restrict__ Wsc,
@@ -150,7 +136,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     const int li = lane & 31, hh = lane >> 5;
     const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
     int mt, nt;
-    tile_of3(blockIdx.x, nM * nN, nM, nN, mt, nt);
+    tile_xcd(blockIdx.x, nM * nN, nM, nN, mt, nt);
     const int m0 = mt * BM, n0 = nt * BN;
     const int KB = K / 32;
 
@@ -501,6 +487,7 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
     if ((epi == EPI_GELU_X3 || epi == EPI_GELU_H2) && W.N % 32 != 0) return hipErrorInvalidValue;
+    if (gemm_lds_applies(W, a_fmt, M, epi)) return launch_gemm_lds(W, X, bias, Y, ldy, M, epi, st);
     // FP32 activations: f16 two-limb split unless CIH_LIMBS=bf16x3
     const char *lv = getenv("CIH_LIMBS");
     const bool bf16 = lv && !strcmp(lv, "bf16x3");

@@ -37,7 +37,29 @@ struct DevMatrix {
     int N = 0, K = 0;          // out_dim, in_dim
     const void *q = nullptr;   // F32 values or packed quants
     const float *sc = nullptr; // per-block scales (quantized formats)
+    // Optional copy of the quants as f16 integers, [K/32][N][32] (element
+    // order of the block, Q4_0 nibbles already minus 8): the operand of the
+    // LDS-staged GEMM.  Same values as q, so the same products.
+    const unsigned short *q16 = nullptr;
 };
+
+// Workgroup -> output tile: consecutive workgroup ids go to the 8 XCDs in
+// turn, so each XCD receives a contiguous range of tiles, ordered GROUP_M row
+// tiles deep so that the tiles resident on one XCD share rows and columns in
+// its L2.
+__device__ __forceinline__ void tile_xcd(int bid, int total, int nM, int nN, int &mt, int &nt) {
+    constexpr int XCD = 8, GROUP_M = 8;
+    const int xcd = bid % XCD, local = bid / XCD;
+    const int per = total / XCD, rem = total % XCD;
+    const int id = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    const int in_group = GROUP_M * nN;
+    const int g = id / in_group;
+    const int first = g * GROUP_M;
+    const int gsize = min(nM - first, GROUP_M);
+    const int r = id % in_group;
+    mt = first + r % gsize;
+    nt = r / gsize;
+}
 
 // Device buffer for partial sums of k-split GEMMs and GEMVs (one stream uses
 // it at a time).  A split-K GEMM needs at most SPLITK_PART_FLOATS floats.
@@ -73,6 +95,18 @@ hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const
 // (no bias) for a consumer that adds them itself.
 hipError_t launch_gemv_partials(const DevMatrix &W, const float *X, int ldx, int M, const PartialBuf &pb, int *splits,
                                 hipStream_t st);
+
+// The same GEMM for activations in f16 limbs (AF_H2) and W.q16 present, with
+// operands copied global -> LDS by the load unit (no staging registers).
+// Epilogues EPI_NONE / EPI_RESIDUAL / EPI_GELU_H2.  gemm_lds_applies says
+// whether launch_gemm_x3 routes a call there: the shape must give at least
+// one full round of 128x128 tiles (smaller problems keep the split-K path);
+// CIH_GEMM_LDS=0 never, =force whenever the formats allow.
+bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi);
+hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
+                           hipStream_t st);
+// W.q16 from W.q (quantized W, k-block-major), on stream st.
+hipError_t launch_expand_f16(const DevMatrix &W, unsigned short *q16, hipStream_t st);
 
 // Dequantizes nblocks of a device matrix in k-block-major layout back to the
 // reference's row-major [N][K] FP32 (test path).

@@ -338,6 +338,7 @@ struct Plan {
     std::vector<std::pair<const void **, size_t>> fix;
     std::vector<Job> jobs;
     std::vector<CopySeg> copies;
+    std::vector<DevMatrix *> expand;  // matrices that also get the f16 copy of their quants
 
     size_t take(size_t b) {
         const size_t off = (bytes + 255) & ~(size_t)255;
@@ -345,7 +346,8 @@ struct Plan {
         return off;
     }
     // a matrix of parts {image offset, rows} in src_dt, stored as dst_dt
-    void matrix(DevMatrix &M, int src_dt, int dst_dt, int K, std::initializer_list<std::pair<int64_t, int>> parts) {
+    void matrix(DevMatrix &M, int src_dt, int dst_dt, int K, std::initializer_list<std::pair<int64_t, int>> parts,
+                bool f16_copy = false) {
         int Ntot = 0;
         for (auto &p : parts) Ntot += p.second;
         M.N = Ntot;
@@ -357,6 +359,10 @@ struct Plan {
         } else {
             fix.push_back({&M.q, take(blocks * (block_bytes(dst_dt) - 4))});
             fix.push_back({(const void **)&M.sc, take(blocks * 4)});
+            if (f16_copy) {
+                fix.push_back({(const void **)&M.q16, take(blocks * 64)});
+                expand.push_back(&M);
+            }
         }
         int off = 0;
         for (auto &p : parts) {
@@ -386,12 +392,17 @@ int build_from_image(cih_model *m, const Layout &y, int dst_dt, const uint8_t *i
     // token embedding: Q8_0 in Q8_0 models, FP32 otherwise (lib.rs:561, 675-687 vs 1113-1125)
     p.matrix(m->emb, y.emb_dtype, dst_dt == DT_Q8 ? DT_Q8 : DT_FP32, (int)d, {{y.emb, (int)V}});
     m->layers.resize(L);
+    // The layer matrices of a quantized model also keep their quants as f16
+    // integers (2 bytes per weight) for the LDS-staged GEMM of large batches;
+    // CIH_GEMM_F16=0 leaves them out.
+    const char *f16e = getenv("CIH_GEMM_F16");
+    const bool f16 = dst_dt != DT_FP32 && !(f16e && !strcmp(f16e, "0"));
     for (int64_t l = 0; l < L; l++) {
         Layer &ly = m->layers[l];
-        p.matrix(ly.wqkv, y.dtype, dst_dt, (int)d, {{y.wq[l], (int)d}, {y.wk[l], (int)d}, {y.wv[l], (int)d}});
-        p.matrix(ly.wo, y.dtype, dst_dt, (int)d, {{y.wo[l], (int)d}});
-        p.matrix(ly.w1, y.dtype, dst_dt, (int)d, {{y.fc1[l], (int)F}});
-        p.matrix(ly.w2, y.dtype, dst_dt, (int)F, {{y.fc2[l], (int)d}});
+        p.matrix(ly.wqkv, y.dtype, dst_dt, (int)d, {{y.wq[l], (int)d}, {y.wk[l], (int)d}, {y.wv[l], (int)d}}, f16);
+        p.matrix(ly.wo, y.dtype, dst_dt, (int)d, {{y.wo[l], (int)d}}, f16);
+        p.matrix(ly.w1, y.dtype, dst_dt, (int)d, {{y.fc1[l], (int)F}}, f16);
+        p.matrix(ly.w2, y.dtype, dst_dt, (int)F, {{y.fc2[l], (int)d}}, f16);
         p.vec(ly.bqkv, {{y.bq[l], d}, {y.bk[l], d}, {y.bv[l], d}});
         p.vec(ly.bo, {{y.bo[l], d}});
         p.vec(ly.b1, {{y.fc1b[l], F}});
@@ -425,6 +436,8 @@ int build_from_image(cih_model *m, const Layout &y, int dst_dt, const uint8_t *i
         const Plan::Job &j = p.jobs[i];
         e = launch_load_matrix(img + j.src, j.src_fmt, j.N, *j.dst, j.n_off, m->stream);
     }
+    for (size_t i = 0; e == hipSuccess && i < p.expand.size(); i++)
+        e = launch_expand_f16(*p.expand[i], const_cast<unsigned short *>(p.expand[i]->q16), m->stream);
     if (e == hipSuccess) e = launch_copy_segments(img, arena, segs, (int)p.copies.size(), m->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
     if (segs) hipFree(segs);

@@ -1,0 +1,86 @@
+"""The LDS-staged quantized GEMM (csrc/gemm_lds.hip: operands loaded global ->
+LDS by the load unit, quants read from an f16 copy made at model load)
+against the register-staged GEMM (csrc/gemm_x3.hip) it replaces on large
+batches.  Both compute matmul_tiled_q8/q4_parallel (src/lib.rs:4870, 4937)
+with the same operations in the same order, so whole forwards must agree
+bit for bit: a wrong swizzle, load count, stage rotation or f16 expansion
+changes the result.
+
+A model built with CIH_GEMM_F16=0 has no f16 copy and always takes the
+register-staged kernel; CIH_GEMM_LDS=force sends every eligible GEMM of the
+other model (activations in f16 limbs) to the LDS-staged one.  CIH_SPLITK=0
+keeps the register-staged kernel from splitting K on small shapes (a split
+sums the blocks in another order).
+"""
+import numpy as np
+import pytest
+
+import codon_hip as ch
+
+pytestmark = pytest.mark.gpu
+
+FLAGS = ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_CONTACTS
+
+
+def rand_tokens(rng, n):
+    t = np.empty(n + 2, np.int32)
+    t[0], t[-1] = 0, 2
+    t[1:-1] = 4 + rng.integers(0, 20, n)
+    return t
+
+
+def two_models(monkeypatch, cfg, w, cw, max_batch, max_len):
+    monkeypatch.setenv("CIH_GEMM_F16", "0")
+    ref = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=max_batch, max_len=max_len, outputs=FLAGS)
+    monkeypatch.delenv("CIH_GEMM_F16")
+    lds = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=max_batch, max_len=max_len, outputs=FLAGS)
+    return ref, lds
+
+
+def assert_same(got, ref, seqs, what):
+    for i, s in enumerate(seqs):
+        n = len(s)
+        for k in ("logits", "hidden", "contacts"):
+            g, r = got[k][i], ref[k][i]
+            g, r = (g[:n - 2, :n - 2], r[:n - 2, :n - 2]) if k == "contacts" else (g[:n], r[:n])
+            assert np.array_equal(g, r), (what, i, k, float(np.abs(g - r).max()))
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_forced_lds_gemm_is_bit_identical(fmt, monkeypatch):
+    """Ragged shapes: token count 687 and projection widths 576 / 192 / 768
+    are not multiples of the 128 x 128 or 128 x 256 tiles, FC2 has K = 768."""
+    rng = np.random.default_rng(11)
+    cfg = ch.EsmConfig(192, 768, 2, 3)
+    w = ch.EsmWeights.random(cfg, seed=11, bias_std=0.02)
+    w = w.quantize_q8() if fmt == "q8" else w.quantize_q4()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    seqs = [rand_tokens(rng, 298), rand_tokens(rng, 255), rand_tokens(rng, 128)]
+    ref, lds = two_models(monkeypatch, cfg, w, cw, 3, 300)
+    monkeypatch.setenv("CIH_GEMM_LDS", "force")
+    monkeypatch.setenv("CIH_SPLITK", "0")
+    b = lds.forward(seqs, FLAGS)
+    a = ref.forward(seqs, FLAGS)
+    print(f"{fmt}: forced LDS GEMM forward equals the register-staged one", flush=True)
+    assert_same(b, a, seqs, fmt)
+    ref.close()
+    lds.close()
+
+
+def test_650m_headline_batch_is_bit_identical(monkeypatch):
+    """ESM-2 650M Q8_0, 16 sequences of 510 residues (8192 tokens): the
+    default tile choice (128 x 256 for QKV and FC1, 128 x 128 for Wo and FC2,
+    K = 1280 and 5120)."""
+    rng = np.random.default_rng(650)
+    cfg = ch.EsmConfig.esm2_650m()
+    w = ch.EsmWeights.random(cfg, seed=650, bias_std=0.02).quantize_q8()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.05).astype(np.float32)
+    seqs = [rand_tokens(rng, 510) for _ in range(16)]
+    ref, lds = two_models(monkeypatch, cfg, w, cw, 16, 512)
+    monkeypatch.delenv("CIH_GEMM_LDS", raising=False)
+    b = lds.forward(seqs, FLAGS)
+    a = ref.forward(seqs, FLAGS)
+    print("650M B=16 L=512: LDS GEMM forward equals the register-staged one", flush=True)
+    assert_same(b, a, seqs, "650M")
+    ref.close()
+    lds.close()
