@@ -110,6 +110,13 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
 
+    // Second column tile of the previous block, not yet scaled: its 32 FMAs
+    // per lane run under the next block's MFMAs instead of after them (the
+    // additions into acc keep their block order).
+    f32x16 pend[2];
+    float dpend = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) pend[0][q] = pend[1][q] = 0.0f;
     const int swA = (li >> 1) & 7, swB = (li >> 2) & 3;
     auto compute = [&](int stg) __attribute__((always_inline)) {
         const unsigned char *base = lds + stg * STAGE;
@@ -127,6 +134,13 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
         for (int c = 0; c < 2; c++) {
             const int col = wn * 64 + c * 32 + li;
             f32x16 tmp[2];
+            if (c == 1) {
+                // the previous block's second column tile, scaled while this block's MFMAs run
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[r][1][q] += dpend * pend[r][q];
+            }
 #pragma unroll
             for (int kh = 0; kh < 2; kh++) {
                 const f16x8 b = *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((kh * 2 + hh) ^ swB) << 4));
@@ -145,10 +159,16 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
                     }
             }
             const float d = *reinterpret_cast<const float *>(base + SA + SB + col * 4);
+            if (c == 1) {
+                pend[0] = tmp[0];
+                pend[1] = tmp[1];
+                dpend = d;
+            } else {
 #pragma unroll
-            for (int r = 0; r < 2; r++)
+                for (int r = 0; r < 2; r++)
 #pragma unroll
-                for (int q = 0; q < 16; q++) acc[r][c][q] += d * tmp[r][q];
+                    for (int q = 0; q < 16; q++) acc[r][0][q] += d * tmp[r][q];
+            }
         }
     };
 
@@ -179,6 +199,10 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
         if (++kb == KB) break;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[r][1][q] += dpend * pend[r][q];
 
 #pragma unroll
     for (int c = 0; c < 2; c++) {
