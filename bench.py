@@ -68,6 +68,18 @@ class Hip:
         self.L.hipFree(ctypes.c_void_p(p))
 
 
+def qgemm_name(wname, T, d):
+    """Which quantized GEMM the forward's projections take at T tokens: the
+    LDS-staged kernel when even the narrowest projection (N = d) gives a full
+    round of 128 x 128 tiles and the f16 copy of the quants exists, else the
+    register-staged one (split-K for small T)."""
+    lds = (os.environ.get("CIH_GEMM_LDS") != "0" and os.environ.get("CIH_GEMM_F16") != "0"
+           and (os.environ.get("CIH_GEMM_LDS") == "force" or -(-T // 128) * -(-d // 128) >= 256))
+    if lds:
+        return f"k_gemm_lds<{wname}> f16 MFMA, 2 limbs, operands global->LDS (QKV, Wo, FC1, FC2)"
+    return f"k_gemm_x3<{wname}> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)"
+
+
 def measured_traffic(name):
     """HBM bytes per launch of the dominant kernel for this workload, from the
     committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated)."""
@@ -321,7 +333,7 @@ def dms_bench(args, ch):
                                f"in chunks of {chunk}, scored on the GPU",
                    "residues_per_step": n * n, "forwards_per_step": (n + chunk - 1) // chunk,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "k_gemm_x3<Q8_0> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)",
+        "roofline": {"bound": "mfma", "kernel": qgemm_name("Q8_0", chunk * (n + 2), cfg.dim),
                      "achieved": round(achieved, 2), "peak": PEAK_F16_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_F16_MFMA_TFLOPS, 4), "traffic": None, "timing": TIMING},
     }
@@ -470,7 +482,7 @@ def main():
         elif os.environ.get("CIH_LIMBS") == "bf16x3":
             kname, peak, limbs = f"k_gemm_x3<{wname}> bf16 MFMA, 3 limbs (QKV, Wo, FC1, FC2)", PEAK_BF16_MFMA_TFLOPS, 3
         else:
-            kname, peak, limbs = f"k_gemm_x3<{wname}> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)", PEAK_F16_MFMA_TFLOPS, 2
+            kname, peak, limbs = qgemm_name(wname, T, cfg.dim), PEAK_F16_MFMA_TFLOPS, 2
     # traffic from the committed PMC summary, for the workloads it was measured on
     overrides = kernel_overrides()
     prof = None
