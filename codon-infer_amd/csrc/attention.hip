@@ -10,8 +10,9 @@
 // sequence's length are masked, so each sequence sees exactly the keys the
 // reference's unpadded call sees.
 //
-// One workgroup = (query block of 128, head, sequence); 4 waves x 32
-// queries.  Scores are computed transposed, S^T = K Q^T, with
+// One workgroup = (query block, head, sequence), 32 queries per wave: 4
+// waves x 32 (k_attention_h also 8 waves x 32 = 256 queries on large batches,
+// which halves the staging of each key tile per query).  Scores are computed transposed, S^T = K Q^T, with
 // v_mfma_f32_32x32x2_f32 so that each lane holds one query column and 16
 // keys: the softmax reductions are lane-local plus one swap between the two
 // lane halves, and the probabilities feed the P.V MFMA (O^T = V^T P^T) as the
@@ -320,8 +321,8 @@ __device__ __forceinline__ void split8(const float *v, f16x8 &hi, f16x8 &lo) {
     }
 }
 
-template <int HD, bool ONEPASS>
-__global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
+template <int HD, bool ONEPASS, int NTH = 256>
+__global__ __launch_bounds__(NTH) void k_attention_h(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
                                                      const int *__restrict__ lens, int S_max,
                                                      const float *__restrict__ rc, const float *__restrict__ rsn,
                                                      void *__restrict__ out, int out_fmt, float *__restrict__ P,
@@ -339,7 +340,7 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
 
     const int b = blockIdx.z, h = blockIdx.y;
     const int len = lens[b], base = cu[b];
-    const int qblk = blockIdx.x * 128;
+    const int qblk = blockIdx.x * (NTH / 2);  // 32 queries per wave
     if (qblk >= len) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, hh = lane >> 5;
     const size_t ld = (size_t)3 * d;
@@ -349,13 +350,13 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
 
     // padding dims (HD..HDP of K, HD..VW of V) stay zero for every tile
     if constexpr (HDP > HD)
-        for (int idx = tid; idx < 32 * (HDP - HD); idx += 256) {
+        for (int idx = tid; idx < 32 * (HDP - HD); idx += NTH) {
             const int key = idx / (HDP - HD), c = HD + idx % (HDP - HD);
             Kh[key * K_LD + c] = (_Float16)0.0f;
             Kl[key * K_LD + c] = (_Float16)0.0f;
         }
     if constexpr (VW > HD)
-        for (int idx = tid; idx < (VW - HD) * 32; idx += 256) {
+        for (int idx = tid; idx < (VW - HD) * 32; idx += NTH) {
             const int c = HD + idx / 32, key = idx % 32;
             Vh[c * V_LD + key] = (_Float16)0.0f;
             Vl[c * V_LD + key] = (_Float16)0.0f;
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
     // K tile: a thread rotates 4 consecutive pair-dims (c..c+3 with c+HALF..) of one key
     auto load_k = [&](int kt0) {
         constexpr int G = HALF / 4;
-        for (int idx = tid; idx < 32 * G; idx += 256) {
+        for (int idx = tid; idx < 32 * G; idx += NTH) {
             const int key = idx / G, c = 4 * (idx % G);
             const int kk = min(kt0 + key, len - 1);
             const float *krow = Kg + (size_t)(base + kk) * ld;
@@ -414,7 +415,7 @@ __global__ __launch_bounds__(256) void k_attention_h(const float *__restrict__ q
     };
     // V tile, transposed: a thread takes 4 consecutive keys of one dim (coalesced over dims)
     auto load_v = [&](int kt0) {
-        for (int idx = tid; idx < 8 * HD; idx += 256) {
+        for (int idx = tid; idx < 8 * HD; idx += NTH) {
             const int c = idx % HD, kg = 4 * (idx / HD);
             f16x4 hv, lv;
 #pragma unroll
@@ -596,16 +597,28 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     if ((out_fmt == AF_X3 || out_fmt == AF_H2) && d % 32) return hipErrorInvalidValue;
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
-    dim3 grid((sm.S_max + 127) / 128, H, sm.B);
     const char *e = getenv("CIH_ATT");
     const bool fp32 = e && !strcmp(e, "fp32");
-#define CIH_ATT_K(KER, HDV, ONE)                                                                                \
-    hipLaunchKernelGGL((KER<HDV, ONE>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, rope_cos,     \
-                       rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum)
+    // f16-limb kernel: 256 queries per workgroup (8 waves) halve the K/V tile
+    // staging per query when that still leaves two workgroups per CU, else 128
+    // (more workgroups for short batches).  CIH_ATT_QB=128|256 forces one.
+    const char *qe = getenv("CIH_ATT_QB");
+    bool wide = (long)((sm.S_max + 255) / 256) * H * sm.B >= 512;
+    if (qe && !strcmp(qe, "128")) wide = false;
+    if (qe && !strcmp(qe, "256")) wide = true;
+    const dim3 grid((sm.S_max + 127) / 128, H, sm.B), grid_w((sm.S_max + 255) / 256, H, sm.B);
+#define CIH_ATT_K(KER, HDV, ONE, ...)                                                                           \
+    hipLaunchKernelGGL((KER<HDV, ONE, ##__VA_ARGS__>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, \
+                       rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum)
+#define CIH_ATT_W(HDV, ONE)                                                                                    \
+    hipLaunchKernelGGL((k_attention_h<HDV, ONE, 512>), grid_w, dim3(512), 0, st, qkv, d, sm.cu, sm.lens,       \
+                       sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum)
 #define CIH_ATT(HDV)                                                                                           \
     if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                          \
     else if (fp32) CIH_ATT_K(k_attention, HDV, true);                                                           \
+    else if (P && wide) CIH_ATT_W(HDV, false);                                                                  \
     else if (P) CIH_ATT_K(k_attention_h, HDV, false);                                                           \
+    else if (wide) CIH_ATT_W(HDV, true);                                                                        \
     else CIH_ATT_K(k_attention_h, HDV, true);
     switch (hd) {
     case 16: CIH_ATT(16) break;
@@ -615,6 +628,7 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     default: return hipErrorInvalidValue;
     }
 #undef CIH_ATT
+#undef CIH_ATT_W
 #undef CIH_ATT_K
     return hipGetLastError();
 }

@@ -276,3 +276,30 @@ def test_forward_errors():
     with pytest.raises(ch.CihError, match="CONTACTS|ARG"):
         m.reserve(1, 1030, ch.OUT_CONTACTS)
     m.close()
+
+
+@pytest.mark.parametrize("with_maps", [False, True])
+def test_attention_query_block_size_is_invisible(with_maps, monkeypatch):
+    """256 queries per attention workgroup (chosen on large batches) and 128
+    give the same bits: each query's scores, softmax and P.V do not depend on
+    the block it is computed in."""
+    rng = np.random.default_rng(31)
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=31, bias_std=0.02).quantize_q8()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | (ch.OUT_CONTACTS | ch.OUT_FINAL_ATT if with_maps else 0)
+    seqs = [rand_tokens(rng, n) for n in (298, 97, 255, 30)]
+    res = {}
+    for qb in ("128", "256"):
+        monkeypatch.setenv("CIH_ATT_QB", qb)
+        m = ch.GpuModel(cfg, w, contact_head=(cw, 0.3), max_batch=4, max_len=300, outputs=flags)
+        res[qb] = m.forward(seqs, flags)
+        m.close()
+    keys = ("logits", "hidden") + (("contacts", "final_att") if with_maps else ())
+    for k in keys:
+        for i, s in enumerate(seqs):
+            n = len(s)
+            a, b = res["128"][k][i], res["256"][k][i]
+            a, b = (a[:n - 2, :n - 2], b[:n - 2, :n - 2]) if k == "contacts" else \
+                   ((a[:n, :n], b[:n, :n]) if k == "final_att" else (a[:n], b[:n]))
+            assert np.array_equal(a, b), (with_maps, k, i)
