@@ -105,7 +105,10 @@ typedef struct cih_outputs {
  * contact_w: [n_layers*n_heads] regression weights (l-major) and contact_b
  * its bias, as returned by EsmConfig::contact_head_weights (lib.rs:154-177);
  * contact_w may be NULL when contacts are never requested.
- * Uses the current HIP device; creates one HIP stream per model. */
+ * Uses the current HIP device; creates one HIP stream per model.
+ * Device memory: the weights in their own format, plus, for Q8_0 / Q4_0
+ * models, the layer quants once more as f16 integers (2 bytes per weight:
+ * the operand of the large-batch GEMM); CIH_GEMM_F16=0 leaves that copy out. */
 int cih_model_create(const cih_config *cfg, int32_t dtype, const cih_host_weights *w,
                      const float *contact_w, float contact_b, cih_model **out);
 
