@@ -204,6 +204,23 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
 #pragma unroll
         for (int q = 0; q < 16; q++) acc[r][1][q] += dpend * pend[r][q];
 
+    // Residual: every value this lane adds to is read before the first store,
+    // so the 64 reads share one wait (read and write go through the same
+    // array, which the compiler cannot reorder).
+    float res[2][2][16];
+    if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int col = min(n0 + wn * 64 + c * 32 + li, N - 1);
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int row = min(m0 + wm * 64 + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3), M - 1);
+                    res[c][r][q] = reinterpret_cast<const float *>(Yv)[(size_t)row * ldy + col];
+                }
+        }
+    }
 #pragma unroll
     for (int c = 0; c < 2; c++) {
         const int col = n0 + wn * 64 + c * 32 + li;
@@ -220,7 +237,7 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
                         h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
                     } else {
                         float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
-                        if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+                        if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
                         *dst = v;
                     }
                 }

@@ -365,6 +365,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         return;
     }
 
+    // Residual: all values this lane adds to are read before the first store
+    // (one wait instead of a read-write round trip per element).
+    float res[NT][MT][16];
+    if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const int col = min(n0 + wn * (BN / 2) + c * 32 + li, N - 1);
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int row = min(m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3), M - 1);
+                    res[c][r][q] = reinterpret_cast<const float *>(Yv)[(size_t)row * ldy + col];
+                }
+        }
+    }
 #pragma unroll
     for (int c = 0; c < NT; c++) {
         const int col = n0 + wn * (BN / 2) + c * 32 + li;
@@ -384,7 +400,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
                     } else {
                         float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
                         if constexpr (EPI == EPI_GELU) v = gelu_as(v);
-                        if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+                        if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
                         *dst = v;
                     }
                 }
