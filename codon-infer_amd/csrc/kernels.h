@@ -20,14 +20,19 @@ enum WFmt { WF_F32 = 0, WF_Q8 = 1, WF_Q4 = 2 };
 enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_GELU_X3 = 3, EPI_GELU_H2 = 4 };
 
 // erf_f32 (src/lib.rs:3485-3491, Abramowitz & Stegun 7.1.26, |error| <= 1.5e-7)
-// and gelu(x) = 0.5 x (1 + erf(x / sqrt 2)) (src/lib.rs:3493-3498).
+// and gelu(x) = 0.5 x (1 + erf(x / sqrt 2)) (src/lib.rs:3493-3498).  Same
+// polynomial; t = 1 / (1 + p|x|) by the hardware reciprocal (<= 1 ulp) and
+// exp(-x^2) as 2^(-x^2 log2 e) by the hardware exponential instead of the
+// correctly rounded division and libm exp: a few ulp of erf, against the
+// approximation's own 1.5e-7.
 __device__ __forceinline__ float erf_as(float x) {
     const float sign = x < 0.0f ? -1.0f : 1.0f;
     const float ax = fabsf(x);
-    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * ax);
+    const float e = __builtin_amdgcn_exp2f(-ax * ax * 1.44269504088896340736f);
     const float y =
         1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) *
-                   t * expf(-ax * ax);
+                   t * e;
     return sign * y;
 }
 __device__ __forceinline__ float gelu_as(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f)); }
