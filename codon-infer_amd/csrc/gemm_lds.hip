@@ -86,6 +86,12 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
         srcB[i] = W16 + (size_t)min(n0 + col, N - 1) * 32 + chunk * 8;
     }
     const float *srcS = Wsc + min(n0 + wave * SL + min(lane, SL - 1), N - 1);
+    // Bias of this lane's two columns, loaded before the k loop: the stores
+    // of the epilogue then follow no pending load (a load still pending at a
+    // branch makes the compiler wait for every earlier store as well).
+    float bv[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) bv[c] = bias ? bias[min(n0 + wn * 64 + c * 32 + li, N - 1)] : 0.0f;
 
     auto request = [&](int kb, int stg) __attribute__((always_inline)) {
         unsigned char *base = lds + stg * STAGE;
@@ -204,9 +210,10 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
 #pragma unroll
         for (int q = 0; q < 16; q++) acc[r][1][q] += dpend * pend[r][q];
 
-    // Residual: every value this lane adds to is read before the first store,
-    // so the 64 reads share one wait (read and write go through the same
-    // array, which the compiler cannot reorder).
+    // Epilogue: every output value is formed before the first store (the
+    // residual reads share one wait, and no store follows a pending load, which
+    // would make the compiler wait for each earlier store at every bounds
+    // branch); tiles inside the matrix store without bounds branches.
     float res[2][2][16];
     if constexpr (EPI == EPI_RESIDUAL) {
 #pragma unroll
@@ -222,27 +229,38 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
         }
     }
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-        const int col = n0 + wn * 64 + c * 32 + li;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
+    for (int c = 0; c < 2; c++)
 #pragma unroll
         for (int r = 0; r < 2; r++)
 #pragma unroll
             for (int q = 0; q < 16; q++) {
-                const int row = m0 + wm * 64 + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                if (row < M) {
-                    float v = acc[r][c][q] + bv;
-                    if constexpr (EPI == EPI_GELU_H2) {
-                        h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
-                    } else {
-                        float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
-                        if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
-                        *dst = v;
-                    }
-                }
+                float v = acc[r][c][q] + bv[c];
+                if constexpr (EPI == EPI_GELU_H2) v = gelu_as(v);
+                if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
+                acc[r][c][q] = v;
             }
-    }
+    auto store = [&](bool guard) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int col = n0 + wn * 64 + c * 32 + li;
+            if (guard && col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int row = m0 + wm * 64 + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    if (guard && row >= M) continue;
+                    if constexpr (EPI == EPI_GELU_H2)
+                        h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, acc[r][c][q]);
+                    else
+                        reinterpret_cast<float *>(Yv)[(size_t)row * ldy + col] = acc[r][c][q];
+                }
+        }
+    };
+    if (m0 + BM <= M && n0 + BN <= N)
+        store(false);
+    else
+        store(true);
 }
 
 // q16[kb][n][j] = f16 of quant j of block (kb, n): Q8_0 bytes as signed

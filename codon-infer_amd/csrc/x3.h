@@ -20,6 +20,13 @@ namespace cih {
 
 enum AFmt { AF_F32 = 0, AF_X3 = 1, AF_H2 = 2 };
 
+// The limbs split the FP32 value x as stored.  Without this (empty) operand
+// barrier the backend may fold the multiply that produced x into the first
+// limb's conversion (v_fma_mixlo_f16 rounds the exact product straight to
+// f16) or into the residual subtraction, depending on the code around the
+// call, and two kernels computing the same x would hand off different limbs.
+__device__ __forceinline__ void limb_source(float &x) { asm("" : "+v"(x)); }
+
 __device__ __forceinline__ unsigned short bf16_bits(float x) {
     return __builtin_bit_cast(unsigned short, (__bf16)x);
 }
@@ -31,6 +38,7 @@ __device__ __forceinline__ size_t x3_index(size_t row, int col, int K, int l) {
 }
 
 __device__ __forceinline__ void x3_store(unsigned short *base, size_t row, int col, int K, float x) {
+    limb_source(x);
     const unsigned short a = bf16_bits(x);
     const float r1 = x - bf16_val(a);
     const unsigned short b = bf16_bits(r1);
@@ -43,6 +51,10 @@ __device__ __forceinline__ void x3_store(unsigned short *base, size_t row, int c
 
 // four consecutive columns col..col+3 (col % 4 == 0) as 8-byte stores per limb
 __device__ __forceinline__ void x3_store4(unsigned short *base, size_t row, int col, int K, float4 x) {
+    limb_source(x.x);
+    limb_source(x.y);
+    limb_source(x.z);
+    limb_source(x.w);
     const float v[4] = {x.x, x.y, x.z, x.w};
     unsigned short l[3][4];
 #pragma unroll
@@ -68,6 +80,7 @@ __device__ __forceinline__ size_t h2_index(size_t row, int col, int K, int l) {
 }
 
 __device__ __forceinline__ void h2_store(unsigned short *base, size_t row, int col, int K, float x) {
+    limb_source(x);
     const unsigned short a = f16_bits(x);
     const size_t i = h2_index(row, col, K, 0);
     base[i] = a;
@@ -76,6 +89,10 @@ __device__ __forceinline__ void h2_store(unsigned short *base, size_t row, int c
 
 // four consecutive columns col..col+3 (col % 4 == 0) as 8-byte stores per limb
 __device__ __forceinline__ void h2_store4(unsigned short *base, size_t row, int col, int K, float4 x) {
+    limb_source(x.x);
+    limb_source(x.y);
+    limb_source(x.z);
+    limb_source(x.w);
     const float v[4] = {x.x, x.y, x.z, x.w};
     unsigned short l[2][4];
 #pragma unroll
