@@ -40,26 +40,35 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 typedef __attribute__((address_space(1))) void glb_ptr_t;
 
-template <int BM, int BN> struct LdsTile {
-    static constexpr int WN = BN / 64, NW = (BM / 64) * WN, THREADS = 64 * NW;
+// Workgroup tile: WM x WN waves, each owning RT x CT MFMA tiles of 32 x 32.
+// A block of A (BM rows x 128 B) and of W.q16 (BN columns x 64 B) is LA and
+// LB load instructions of 1 KiB; instruction j goes to wave j % NW.  When NW
+// does not divide them, the waves with fewer real loads repeat their first
+// one (same source, same LDS bytes), so every wave issues NI loads per block
+// and the wait counts are the same in all waves.
+template <int RT, int CT, int WM, int WN> struct LdsTile {
+    static constexpr int BM = WM * RT * 32, BN = WN * CT * 32, NW = WM * WN, THREADS = 64 * NW;
     static constexpr int SA = BM * 128, SB = BN * 64, SS = BN * 4, STAGE = SA + SB + SS;
-    static constexpr int NA = SA / 1024 / NW;  // 16-byte-per-lane loads of A per wave and block
-    static constexpr int NB = SB / 1024 / NW;  // ... of W
-    static constexpr int SL = BN / NW;         // scales per wave and block (4-byte loads)
-    static constexpr int NI = NA + NB + 1;     // load instructions per wave and block
-    static_assert(NA >= 1 && NB >= 1 && SL <= 64 && SA % (1024 * NW) == 0 && SB % (1024 * NW) == 0, "tile");
+    static constexpr int LA = SA / 1024, LB = SB / 1024;
+    static constexpr int NA = (LA + NW - 1) / NW, NB = (LB + NW - 1) / NW;
+    static constexpr int SL = BN / NW;      // scales per wave and block (4-byte loads)
+    static constexpr int NI = NA + NB + 1;  // load instructions per wave and block
+    static constexpr int OCC = 512 / THREADS;  // workgroups per CU: two waves per SIMD
+    static_assert(SA % 1024 == 0 && SB % 1024 == 0 && LA >= NW && LB >= NW, "loads");
+    static_assert(BN % NW == 0 && SL <= 64 && OCC * 3 * STAGE <= 160 * 1024, "tile");
 };
 
-template <int EPI, int BM, int BN>
-__global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>::THREADS)) void k_gemm_lds(
+template <int EPI, int RT, int CT, int WM, int WN>
+__global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::OCC)) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned short *__restrict__ W16, const float *__restrict__ Wsc,
     const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K) {
-    using T = LdsTile<BM, BN>;
-    constexpr int SA = T::SA, SB = T::SB, STAGE = T::STAGE, NA = T::NA, NB = T::NB, SL = T::SL;
+    using T = LdsTile<RT, CT, WM, WN>;
+    constexpr int BM = T::BM, BN = T::BN, NW = T::NW, SA = T::SA, SB = T::SB, STAGE = T::STAGE, NA = T::NA,
+                  NB = T::NB, SL = T::SL;
     __shared__ __attribute__((aligned(1024))) unsigned char lds[3 * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / T::WN, wn = wave % T::WN;
+    const int wm = wave / WN, wn = wave % WN;
     const int li = lane & 31, hh = lane >> 5;
     const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
     int mt, nt;
@@ -67,113 +76,152 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
     const int m0 = mt * BM, n0 = nt * BN;
     const int KB = K / 32;
 
-    // Per-lane sources at k-block 0.  Load i of a wave fills LDS bytes
-    // [(wave * NA + i) * 1024, +1024) of the stage, lane l the 16 bytes at
-    // l * 16: LDS chunk p holds the (row, chunk) whose swizzled position is p.
+    // Per-lane sources at k-block 0.  Load instruction j fills LDS bytes
+    // [j * 1024, +1024) of its region, lane l the 16 bytes at l * 16: LDS
+    // chunk p = 64 j + l holds the (row, chunk) whose swizzled position is p.
     // Rows past M and columns past N read the last row / column (never stored).
     const unsigned short *srcA[NA];
+    int dstA[NA];
 #pragma unroll
     for (int i = 0; i < NA; i++) {
-        const int p = (wave * NA + i) * 64 + lane;
+        const int j = i * NW + wave < T::LA ? i * NW + wave : wave;
+        const int p = j * 64 + lane;
         const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
         srcA[i] = X + (size_t)min(m0 + row, M - 1) * KB * 64 + chunk * 8;
+        dstA[i] = j * 1024;
     }
     const unsigned short *srcB[NB];
+    int dstB[NB];
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-        const int p = (wave * NB + i) * 64 + lane;
+        const int j = i * NW + wave < T::LB ? i * NW + wave : wave;
+        const int p = j * 64 + lane;
         const int col = p >> 2, chunk = (p & 3) ^ ((col >> 2) & 3);
         srcB[i] = W16 + (size_t)min(n0 + col, N - 1) * 32 + chunk * 8;
+        dstB[i] = SA + j * 1024;
     }
     const float *srcS = Wsc + min(n0 + wave * SL + min(lane, SL - 1), N - 1);
-    // Bias of this lane's two columns, loaded before the k loop: the stores
-    // of the epilogue then follow no pending load (a load still pending at a
+    // Bias of this lane's columns, loaded before the k loop: the stores of
+    // the epilogue then follow no pending load (a load still pending at a
     // branch makes the compiler wait for every earlier store as well).
-    float bv[2];
+    float bv[CT];
 #pragma unroll
-    for (int c = 0; c < 2; c++) bv[c] = bias ? bias[min(n0 + wn * 64 + c * 32 + li, N - 1)] : 0.0f;
+    for (int c = 0; c < CT; c++) bv[c] = bias ? bias[min(n0 + (wn * CT + c) * 32 + li, N - 1)] : 0.0f;
 
     auto request = [&](int kb, int stg) __attribute__((always_inline)) {
         unsigned char *base = lds + stg * STAGE;
 #pragma unroll
         for (int i = 0; i < NA; i++)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcA[i] + (size_t)kb * 64),
-                                             (lds_ptr_t *)(base + (wave * NA + i) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcA[i] + (size_t)kb * 64), (lds_ptr_t *)(base + dstA[i]),
+                                             16, 0, 0);
 #pragma unroll
         for (int i = 0; i < NB; i++)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcB[i] + (size_t)kb * N * 32),
-                                             (lds_ptr_t *)(base + SA + (wave * NB + i) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcB[i] + (size_t)kb * N * 32), (lds_ptr_t *)(base + dstB[i]),
+                                             16, 0, 0);
         if (lane < SL)
             __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcS + (size_t)kb * N),
                                              (lds_ptr_t *)(base + SA + SB + wave * SL * 4), 4, 0, 0);
     };
 
-    f32x16 acc[2][2];
+    // Two schedules with the same arithmetic (per 32 x 32 tile: tmp = both
+    // limbs x both k-halves, then acc += d * tmp in block order):
+    //  * RT >= 2: column tile after column tile, RT chains each; the last
+    //    column tile's scaling is deferred under the next block's MFMAs (its
+    //    FMAs would otherwise trail the block);
+    //  * RT == 1: all CT chains interleaved (one chain per column tile would
+    //    leave each MFMA waiting for its predecessor), scaled after the block.
+    f32x16 acc[RT][CT];
 #pragma unroll
-    for (int r = 0; r < 2; r++)
+    for (int r = 0; r < RT; r++)
 #pragma unroll
-        for (int c = 0; c < 2; c++)
+        for (int c = 0; c < CT; c++)
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
-
-    // Second column tile of the previous block, not yet scaled: its 32 FMAs
-    // per lane run under the next block's MFMAs instead of after them (the
-    // additions into acc keep their block order).
-    f32x16 pend[2];
+    constexpr int NT = RT >= 2 ? RT : CT;  // live chains
+    f32x16 pend[RT >= 2 ? RT : 1];
     float dpend = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 16; q++) pend[0][q] = pend[1][q] = 0.0f;
+    for (int r = 0; r < (RT >= 2 ? RT : 1); r++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) pend[r][q] = 0.0f;
     const int swA = (li >> 1) & 7, swB = (li >> 2) & 3;
+    auto read_b = [&](const unsigned char *base, int c, int kh) __attribute__((always_inline)) {
+        const int col = (wn * CT + c) * 32 + li;
+        return *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((kh * 2 + hh) ^ swB) << 4));
+    };
+    auto scale_of = [&](const unsigned char *base, int c) __attribute__((always_inline)) {
+        return *reinterpret_cast<const float *>(base + SA + SB + ((wn * CT + c) * 32 + li) * 4);
+    };
+    auto mfma = [&](const f16x8 &x, const f16x8 &w, f32x16 &t, bool first) __attribute__((always_inline)) {
+        f32x16 cc;
+        if (first) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) cc[q] = 0.0f;
+        } else {
+            cc = t;
+        }
+        t = __builtin_amdgcn_mfma_f32_32x32x16_f16(x, w, cc, 0, 0, 0);
+    };
     auto compute = [&](int stg) __attribute__((always_inline)) {
         const unsigned char *base = lds + stg * STAGE;
-        f16x8 a[2][2][2];  // [k-half][limb][row tile]
+        f16x8 a[2][2][RT];  // [k-half][limb][row tile]
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
             for (int l = 0; l < 2; l++)
 #pragma unroll
-                for (int r = 0; r < 2; r++) {
-                    const int row = wm * 64 + r * 32 + li, chunk = l * 4 + kh * 2 + hh;
+                for (int r = 0; r < RT; r++) {
+                    const int row = (wm * RT + r) * 32 + li, chunk = l * 4 + kh * 2 + hh;
                     a[kh][l][r] = *reinterpret_cast<const f16x8 *>(base + row * 128 + ((chunk ^ swA) << 4));
                 }
+        if constexpr (RT >= 2) {
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int col = wn * 64 + c * 32 + li;
-            f32x16 tmp[2];
-            if (c == 1) {
-                // the previous block's second column tile, scaled while this block's MFMAs run
+            for (int c = 0; c < CT; c++) {
+                f32x16 tmp[NT];
+                if (c == CT - 1) {
+                    // the previous block's last column tile, scaled while this block's MFMAs run
 #pragma unroll
-                for (int r = 0; r < 2; r++)
+                    for (int r = 0; r < RT; r++)
 #pragma unroll
-                    for (int q = 0; q < 16; q++) acc[r][1][q] += dpend * pend[r][q];
+                        for (int q = 0; q < 16; q++) acc[r][CT - 1][q] += dpend * pend[r][q];
+                }
+#pragma unroll
+                for (int kh = 0; kh < 2; kh++) {
+                    const f16x8 b = read_b(base, c, kh);
+#pragma unroll
+                    for (int l = 0; l < 2; l++)
+#pragma unroll
+                        for (int r = 0; r < RT; r++) mfma(a[kh][l][r], b, tmp[r], kh == 0 && l == 0);
+                }
+                const float d = scale_of(base, c);
+                if (c == CT - 1) {
+#pragma unroll
+                    for (int r = 0; r < RT; r++) pend[r] = tmp[r];
+                    dpend = d;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < RT; r++)
+#pragma unroll
+                        for (int q = 0; q < 16; q++) acc[r][c][q] += d * tmp[r][q];
+                }
             }
+        } else {
+            f32x16 tmp[NT];
 #pragma unroll
             for (int kh = 0; kh < 2; kh++) {
-                const f16x8 b = *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((kh * 2 + hh) ^ swB) << 4));
+                f16x8 b[CT];
+#pragma unroll
+                for (int c = 0; c < CT; c++) b[c] = read_b(base, c, kh);
 #pragma unroll
                 for (int l = 0; l < 2; l++)
 #pragma unroll
-                    for (int r = 0; r < 2; r++) {
-                        f32x16 cc;
-                        if (kh == 0 && l == 0) {
-#pragma unroll
-                            for (int q = 0; q < 16; q++) cc[q] = 0.0f;
-                        } else {
-                            cc = tmp[r];
-                        }
-                        tmp[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kh][l][r], b, cc, 0, 0, 0);
-                    }
+                    for (int c = 0; c < CT; c++) mfma(a[kh][l][0], b[c], tmp[c], kh == 0 && l == 0);
             }
-            const float d = *reinterpret_cast<const float *>(base + SA + SB + col * 4);
-            if (c == 1) {
-                pend[0] = tmp[0];
-                pend[1] = tmp[1];
-                dpend = d;
-            } else {
 #pragma unroll
-                for (int r = 0; r < 2; r++)
+            for (int c = 0; c < CT; c++) {
+                const float d = scale_of(base, c);
 #pragma unroll
-                    for (int q = 0; q < 16; q++) acc[r][0][q] += d * tmp[r][q];
+                for (int q = 0; q < 16; q++) acc[0][c][q] += d * tmp[c][q];
             }
         }
     };
@@ -205,33 +253,35 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
         if (++kb == KB) break;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (RT >= 2) {
 #pragma unroll
-    for (int r = 0; r < 2; r++)
+        for (int r = 0; r < RT; r++)
 #pragma unroll
-        for (int q = 0; q < 16; q++) acc[r][1][q] += dpend * pend[r][q];
+            for (int q = 0; q < 16; q++) acc[r][CT - 1][q] += dpend * pend[r][q];
+    }
 
     // Epilogue: every output value is formed before the first store (the
     // residual reads share one wait, and no store follows a pending load, which
     // would make the compiler wait for each earlier store at every bounds
     // branch); tiles inside the matrix store without bounds branches.
-    float res[2][2][16];
+    float res[CT][RT][16];
     if constexpr (EPI == EPI_RESIDUAL) {
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int col = min(n0 + wn * 64 + c * 32 + li, N - 1);
+        for (int c = 0; c < CT; c++) {
+            const int col = min(n0 + (wn * CT + c) * 32 + li, N - 1);
 #pragma unroll
-            for (int r = 0; r < 2; r++)
+            for (int r = 0; r < RT; r++)
 #pragma unroll
                 for (int q = 0; q < 16; q++) {
-                    const int row = min(m0 + wm * 64 + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3), M - 1);
+                    const int row = min(m0 + (wm * RT + r) * 32 + 8 * (q >> 2) + 4 * hh + (q & 3), M - 1);
                     res[c][r][q] = reinterpret_cast<const float *>(Yv)[(size_t)row * ldy + col];
                 }
         }
     }
 #pragma unroll
-    for (int c = 0; c < 2; c++)
+    for (int c = 0; c < CT; c++)
 #pragma unroll
-        for (int r = 0; r < 2; r++)
+        for (int r = 0; r < RT; r++)
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 float v = acc[r][c][q] + bv[c];
@@ -241,14 +291,14 @@ __global__ __launch_bounds__((LdsTile<BM, BN>::THREADS), (512 / LdsTile<BM, BN>:
             }
     auto store = [&](bool guard) __attribute__((always_inline)) {
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int col = n0 + wn * 64 + c * 32 + li;
+        for (int c = 0; c < CT; c++) {
+            const int col = n0 + (wn * CT + c) * 32 + li;
             if (guard && col >= N) continue;
 #pragma unroll
-            for (int r = 0; r < 2; r++)
+            for (int r = 0; r < RT; r++)
 #pragma unroll
                 for (int q = 0; q < 16; q++) {
-                    const int row = m0 + wm * 64 + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    const int row = m0 + (wm * RT + r) * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
                     if (guard && row >= M) continue;
                     if constexpr (EPI == EPI_GELU_H2)
                         h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, acc[r][c][q]);
@@ -283,20 +333,39 @@ __global__ __launch_bounds__(256) void k_expand_f16(const unsigned char *__restr
     q16[i] = __builtin_bit_cast(unsigned short, (_Float16)(float)v);
 }
 
-template <int EPI, int BM, int BN>
+template <int EPI, int RT, int CT, int WM, int WN>
 hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
-    const int tiles = ((M + BM - 1) / BM) * ((W.N + BN - 1) / BN);
-    hipLaunchKernelGGL((k_gemm_lds<EPI, BM, BN>), dim3(tiles), dim3(LdsTile<BM, BN>::THREADS), 0, st,
+    using T = LdsTile<RT, CT, WM, WN>;
+    const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
+    hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN>), dim3(tiles), dim3(T::THREADS), 0, st,
                        reinterpret_cast<const unsigned short *>(X), W.q16, W.sc, bias, Y, ldy, M, W.N, W.K);
     return hipGetLastError();
 }
 
+// Tile choice.  128 x 256 (8 waves, one workgroup per CU) reads the fewest
+// operand bytes per output and is taken while it yields at least two rounds
+// of workgroups.  Otherwise the 4-wave tiles (two workgroups per CU, 512
+// slots) compete on the time their rounds take: 128 x 128, or 128 x 160
+// (waves of 32 rows x 160 columns) when it needs fewer rounds for the same
+// work (N = 1280 at M = 8192: 640 tiles of 128 x 128 take 2 rounds, the
+// second a quarter full; 512 tiles of 128 x 160 exactly one).
+int tile_choice(int M, int N) {
+    const long mt = (M + 127) / 128;
+    if (mt * ((N + 255) / 256) >= 512) return 256;
+    const long t128 = mt * ((N + 127) / 128), t160 = mt * ((N + 159) / 160);
+    // output elements per slot-round actually occupied: rounds x 512 slots x tile
+    const double cost128 = (double)((t128 + 511) / 512) * 128 * 128;
+    const double cost160 = (double)((t160 + 511) / 512) * 128 * 160;
+    return cost160 < cost128 ? 160 : 128;
+}
+
 template <int EPI>
 hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
-    // 128 x 256 when it still yields two rounds of workgroups (one per CU), else 128 x 128
-    const long wide = (long)((M + 127) / 128) * ((W.N + 255) / 256);
-    if (wide >= 512) return launch_t<EPI, 128, 256>(W, X, bias, Y, ldy, M, st);
-    return launch_t<EPI, 128, 128>(W, X, bias, Y, ldy, M, st);
+    const char *e = getenv("CIH_GEMM_TILE_N");
+    const int bn = e ? atoi(e) : tile_choice(M, W.N);
+    if (bn == 256) return launch_t<EPI, 2, 2, 2, 4>(W, X, bias, Y, ldy, M, st);
+    if (bn == 160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st);
+    return launch_t<EPI, 2, 2, 2, 2>(W, X, bias, Y, ldy, M, st);
 }
 
 }  // namespace
