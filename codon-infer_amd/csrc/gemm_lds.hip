@@ -342,27 +342,57 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     return hipGetLastError();
 }
 
-// Tile choice.  128 x 256 (8 waves, one workgroup per CU) reads the fewest
-// operand bytes per output and is taken while it yields at least two rounds
-// of workgroups.  Otherwise the 4-wave tiles (two workgroups per CU, 512
-// slots) compete on the time their rounds take: 128 x 128, or 128 x 160
-// (waves of 32 rows x 160 columns) when it needs fewer rounds for the same
-// work (N = 1280 at M = 8192: 640 tiles of 128 x 128 take 2 rounds, the
-// second a quarter full; 512 tiles of 128 x 160 exactly one).
+// Tile choice by a model of the time the rounds of workgroups take on the
+// device's CUs.  Candidates, in order of preference (fewest operand bytes per
+// output first): 128 x 320 and 128 x 256 (8 waves, one workgroup per CU),
+// 128 x 160 and 128 x 128 (4 waves, two per CU).  A full round costs the
+// tile area times the workgroups sharing a CU; a last round that leaves a
+// 4-wave workgroup alone on its CU runs it at about 1/1.4 of a CU's rate.
+// At M = 8192 this picks 128 x 320 for every ESM-2 650M projection (QKV:
+// 3 rounds instead of 3.75; N = 1280: one round instead of 1.25); at
+// M = 2552 (a ragged 8-sequence batch) 128 x 320 for QKV, 128 x 256 for FC1,
+// 128 x 128 for Wo and FC2, as measured.
+int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
 int tile_choice(int M, int N) {
+    const int cus = device_cus();
     const long mt = (M + 127) / 128;
-    if (mt * ((N + 255) / 256) >= 512) return 256;
-    const long t128 = mt * ((N + 127) / 128), t160 = mt * ((N + 159) / 160);
-    // output elements per slot-round actually occupied: rounds x 512 slots x tile
-    const double cost128 = (double)((t128 + 511) / 512) * 128 * 128;
-    const double cost160 = (double)((t160 + 511) / 512) * 128 * 160;
-    return cost160 < cost128 ? 160 : 128;
+    struct Cand {
+        int bn, per_cu;
+    };
+    const Cand cand[4] = {{320, 1}, {256, 1}, {160, 2}, {128, 2}};
+    int best = 128;
+    double best_cost = 0;
+    for (const Cand &c : cand) {
+        const long tiles = mt * ((N + c.bn - 1) / c.bn), slots = (long)c.per_cu * cus;
+        const double area = 128.0 * c.bn;
+        const long full = tiles / slots, rest = tiles % slots;
+        double cost = full * area * c.per_cu;
+        if (rest) cost += (c.per_cu == 2 && rest <= cus) ? 1.4 * area : area * c.per_cu;
+        if (best_cost == 0 || cost < best_cost) {
+            best = c.bn;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 template <int EPI>
 hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
     const char *e = getenv("CIH_GEMM_TILE_N");
     const int bn = e ? atoi(e) : tile_choice(M, W.N);
+    if (bn == 320) return launch_t<EPI, 1, 5, 4, 2>(W, X, bias, Y, ldy, M, st);
     if (bn == 256) return launch_t<EPI, 2, 2, 2, 4>(W, X, bias, Y, ldy, M, st);
     if (bn == 160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st);
     return launch_t<EPI, 2, 2, 2, 2>(W, X, bias, Y, ldy, M, st);
