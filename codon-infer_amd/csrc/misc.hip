@@ -107,10 +107,70 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     }
 }
 
+// The same with four consecutive columns per lane (d % 4 == 0): 16-byte
+// loads, and 8-byte stores per limb.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <int PER, int OF>
+__global__ __launch_bounds__(256) void k_layernorm4(const float *__restrict__ x, const float *__restrict__ w,
+                                                    const float *__restrict__ b, void *__restrict__ out, int rows,
+                                                    int d) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)row * d);
+    const f32x4 *wr = reinterpret_cast<const f32x4 *>(w), *br = reinterpret_cast<const f32x4 *>(b);
+    const int n4 = d >> 2;
+    f32x4 v[PER], g[PER], be[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = min(lane + 64 * i, n4 - 1);  // lanes past the row re-read its last quad, masked below
+        v[i] = xr[c];
+        g[i] = wr[c];
+        be[i] = br[c];
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++)
+        if (lane + 64 * i < n4) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float mean = wave_sum(s) / (float)d;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const f32x4 t = v[i] - mean;
+        if (lane + 64 * i < n4) q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+    }
+    const float var = wave_sum(q) / (float)d;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+            f32x4 y;
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+            const float4 yy = make_float4(y.x, y.y, y.z, y.w);
+            if constexpr (OF == AF_X3)
+                x3_store4(reinterpret_cast<unsigned short *>(out), row, 4 * c, d, yy);
+            else if constexpr (OF == AF_H2)
+                h2_store4(reinterpret_cast<unsigned short *>(out), row, 4 * c, d, yy);
+            else
+                reinterpret_cast<f32x4 *>(out)[(size_t)row * n4 + c] = y;
+        }
+    }
+}
+
 template <int OF>
 static hipError_t launch_ln_t(const float *x, const float *w, const float *b, void *out, int rows, int d,
                               hipStream_t st) {
     const dim3 grid((rows + 3) / 4), blk(256);
+    if (d % 4 == 0) {
+        const int per4 = (d / 4 + 63) / 64;
+        if (per4 <= 2) hipLaunchKernelGGL((k_layernorm4<2, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+        else if (per4 <= 5) hipLaunchKernelGGL((k_layernorm4<5, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+        else if (per4 <= 10) hipLaunchKernelGGL((k_layernorm4<10, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     const int per = (d + 63) / 64;
     if (per <= 5) hipLaunchKernelGGL((k_layernorm<5, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
     else if (per <= 10) hipLaunchKernelGGL((k_layernorm<10, OF>), grid, blk, 0, st, x, w, b, out, rows, d);

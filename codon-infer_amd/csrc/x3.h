@@ -51,11 +51,9 @@ __device__ __forceinline__ void x3_store(unsigned short *base, size_t row, int c
 
 // four consecutive columns col..col+3 (col % 4 == 0) as 8-byte stores per limb
 __device__ __forceinline__ void x3_store4(unsigned short *base, size_t row, int col, int K, float4 x) {
-    limb_source(x.x);
-    limb_source(x.y);
-    limb_source(x.z);
-    limb_source(x.w);
-    const float v[4] = {x.x, x.y, x.z, x.w};
+    float v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) limb_source(v[e]);
     unsigned short l[3][4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -89,11 +87,9 @@ __device__ __forceinline__ void h2_store(unsigned short *base, size_t row, int c
 
 // four consecutive columns col..col+3 (col % 4 == 0) as 8-byte stores per limb
 __device__ __forceinline__ void h2_store4(unsigned short *base, size_t row, int col, int K, float4 x) {
-    limb_source(x.x);
-    limb_source(x.y);
-    limb_source(x.z);
-    limb_source(x.w);
-    const float v[4] = {x.x, x.y, x.z, x.w};
+    float v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) limb_source(v[e]);
     unsigned short l[2][4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
