@@ -365,8 +365,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         return;
     }
 
-    // Residual: all values this lane adds to are read before the first store
-    // (one wait instead of a read-write round trip per element).
+    // Epilogue: every output value is formed before the first store (bias and
+    // residual reads share one wait, and no store follows a pending load,
+    // which would make the compiler wait for each earlier store at every
+    // bounds branch); tiles inside the matrix store without bounds branches.
+    float bv[NT];
+#pragma unroll
+    for (int c = 0; c < NT; c++) bv[c] = bias ? bias[min(n0 + wn * (BN / 2) + c * 32 + li, N - 1)] : 0.0f;
     float res[NT][MT][16];
     if constexpr (EPI == EPI_RESIDUAL) {
 #pragma unroll
@@ -382,30 +387,40 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         }
     }
 #pragma unroll
-    for (int c = 0; c < NT; c++) {
-        const int col = n0 + wn * (BN / 2) + c * 32 + li;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
+    for (int c = 0; c < NT; c++)
 #pragma unroll
         for (int r = 0; r < MT; r++)
 #pragma unroll
             for (int q = 0; q < 16; q++) {
-                const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                if (row < M) {
-                    float v = acc[r][c][q] + bv;
-                    if constexpr (EPI == EPI_GELU_X3) {
-                        x3_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
-                    } else if constexpr (EPI == EPI_GELU_H2) {
-                        h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, gelu_as(v));
-                    } else {
-                        float *dst = reinterpret_cast<float *>(Yv) + (size_t)row * ldy + col;
-                        if constexpr (EPI == EPI_GELU) v = gelu_as(v);
-                        if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
-                        *dst = v;
-                    }
-                }
+                float v = acc[r][c][q] + bv[c];
+                if constexpr (EPI == EPI_GELU_X3 || EPI == EPI_GELU_H2 || EPI == EPI_GELU) v = gelu_as(v);
+                if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
+                acc[r][c][q] = v;
             }
-    }
+    auto store = [&](bool guard) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const int col = n0 + wn * (BN / 2) + c * 32 + li;
+            if (guard && col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    if (guard && row >= M) continue;
+                    if constexpr (EPI == EPI_GELU_X3)
+                        x3_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, acc[r][c][q]);
+                    else if constexpr (EPI == EPI_GELU_H2)
+                        h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, acc[r][c][q]);
+                    else
+                        reinterpret_cast<float *>(Yv)[(size_t)row * ldy + col] = acc[r][c][q];
+                }
+        }
+    };
+    if (m0 + BM <= M && n0 + BN <= N)
+        store(false);
+    else
+        store(true);
 }
 
 // Y = epi(sum over splits of part[s] + bias), splits in order
