@@ -222,8 +222,9 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
     if (good) {
         ws.part.floats = model_part_floats(m);
         const size_t nd = std::max(B, S);
+        ws.attp_floats = attention_part_floats((int)m->hd);
         good = ok(dalloc(ws.part.part, ws.part.floats, dl)) && ok(dalloc(ws.dms_meta, nd * 2, dl)) &&
-               ok(dalloc(ws.dms_out, nd * 21, dl));
+               ok(dalloc(ws.dms_out, nd * 21, dl)) && ok(dalloc(ws.attp, ws.attp_floats, dl));
     }
     const bool need_P = flags & (CIH_OUT_CONTACTS | CIH_OUT_FINAL_ATT | CIH_OUT_ATTN);
     if (good && need_P) good = ok(dalloc(ws.P, B * H * S * S, dl));
@@ -369,7 +370,7 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
             ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
             HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, af, P, pb, ph,
-                                    want_contacts && m->nz[l] > 0 ? ws.rowsum : nullptr, st));
+                                    want_contacts && m->nz[l] > 0 ? ws.rowsum : nullptr, ws.attp, ws.attp_floats, st));
         }
         if (want_contacts && m->nz[l] > 0) {
             ProfScope ps(m, CIH_KC_OTHER, 0, 0);

@@ -321,13 +321,19 @@ __device__ __forceinline__ void split8(const float *v, f16x8 &hi, f16x8 &lo) {
     }
 }
 
+// Work items: (sequence, head, query block) tasks, task = (b * H + h) * nq + qb,
+// one workgroup each for the first nfull; every later task is split into
+// nsplit ranges of whole 32-key tiles (one workgroup each, ONEPASS only)
+// that leave their unnormalized output, running max and sum in part for
+// k_attention_merge.
 template <int HD, bool ONEPASS, int NTH = 256>
-__global__ __launch_bounds__(NTH) void k_attention_h(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
+__global__ __launch_bounds__(NTH, ONEPASS ? 4 : 1) void k_attention_h(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
                                                      const int *__restrict__ lens, int S_max,
                                                      const float *__restrict__ rc, const float *__restrict__ rsn,
                                                      void *__restrict__ out, int out_fmt, float *__restrict__ P,
                                                      long long pb, long long ph, float inv_scale,
-                                                     float *__restrict__ rowsum) {
+                                                     float *__restrict__ rowsum, int H, int nq, int nfull, int nsplit,
+                                                     float *__restrict__ part) {
     constexpr int HALF = HD / 2;
     constexpr int HDP = (HD + 15) / 16 * 16;  // dims padded to whole 16-wide k-chunks
     constexpr int NC = HDP / 16;
@@ -338,10 +344,20 @@ __global__ __launch_bounds__(NTH) void k_attention_h(const float *__restrict__ q
     __shared__ __attribute__((aligned(16))) _Float16 Kh[32 * K_LD], Kl[32 * K_LD];
     __shared__ __attribute__((aligned(16))) _Float16 Vh[VW * V_LD], Vl[VW * V_LD];
 
-    const int b = blockIdx.z, h = blockIdx.y;
+    int task = blockIdx.x, ks = 0, ns = 1;
+    if (task >= nfull) {
+        const int t = task - nfull;
+        task = nfull + t / nsplit;
+        ks = t % nsplit;
+        ns = nsplit;
+    }
+    const int qb = task % nq, h = (task / nq) % H, b = task / nq / H;
     const int len = lens[b], base = cu[b];
-    const int qblk = blockIdx.x * (NTH / 2);  // 32 queries per wave
+    const int qblk = qb * (NTH / 2);  // 32 queries per wave
     if (qblk >= len) return;
+    // keys [kbeg, kend) of this workgroup: part ks of ns of the sequence's 32-key tiles
+    const int ntile = (len + 31) / 32, per = (ntile + ns - 1) / ns;
+    const int kbeg = min(ks * per, ntile) * 32, kend = min((ks + 1) * per * 32, len);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, hh = lane >> 5;
     const size_t ld = (size_t)3 * d;
     const float *Qg = qkv + h * HD;
@@ -491,12 +507,12 @@ __global__ __launch_bounds__(NTH) void k_attention_h(const float *__restrict__ q
                 float v = acc[q] * sl2;
                 if constexpr (decltype(masked)::value) {
                     const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                    v = key < len ? v : -INFINITY;
+                    v = key < kend ? v : -INFINITY;
                 }
                 sv[q] = v;
                 tmax = fmaxf(tmax, v);
             }
-            // key kt0 (< len) sits in half 0, so the combined tile max is finite
+            // key kt0 (< kend) sits in half 0, so the combined tile max is finite
             const float mn = fmaxf(m, fmaxf(tmax, __shfl_xor(tmax, 32)));
             const float corr = __builtin_amdgcn_exp2f(m - mn);
             float p[16], sum = 0.0f;
@@ -515,10 +531,28 @@ __global__ __launch_bounds__(NTH) void k_attention_h(const float *__restrict__ q
             }
             pv(oacc, p);
         };
-        int kt0 = 0;
-        for (; kt0 + 32 <= len; kt0 += 32) tile(kt0, std::false_type{});
-        if (kt0 < len) tile(kt0, std::true_type{});
-        out_scale = 1.0f / (l + __shfl_xor(l, 32));
+        int kt0 = kbeg;
+        for (; kt0 + 32 <= kend; kt0 += 32) tile(kt0, std::false_type{});
+        if (kt0 < kend) tile(kt0, std::true_type{});
+        const float lt = l + __shfl_xor(l, 32);
+        if (ns > 1) {
+            // split task: unnormalized output, running max (base 2) and sum
+            if (qi < len) {
+                float *pr = part + ((size_t)(blockIdx.x - nfull) * (NTH / 2) + wave * 32 + li) * (HD + 2);
+#pragma unroll
+                for (int t = 0; t < DT; t++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int dd = t * 32 + 8 * g + 4 * hh;
+                        if (dd >= HD) continue;
+                        *reinterpret_cast<float2 *>(pr + dd) = make_float2(oacc[t][4 * g], oacc[t][4 * g + 1]);
+                        *reinterpret_cast<float2 *>(pr + dd + 2) = make_float2(oacc[t][4 * g + 2], oacc[t][4 * g + 3]);
+                    }
+                if (hh == 0) *reinterpret_cast<float2 *>(pr + HD) = make_float2(m, lt);
+            }
+            return;
+        }
+        out_scale = 1.0f / lt;
     } else {
         // pass 1: running max / sum of exp per lane
         float m = -INFINITY, l = 0.0f;
@@ -568,7 +602,7 @@ __global__ __launch_bounds__(NTH) void k_attention_h(const float *__restrict__ q
             if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
             pv(oacc, p);
         }
-        write_rowsum(rowsum, rs, b, h, gridDim.y, S_max, qi, len, hh);
+        write_rowsum(rowsum, rs, b, h, H, S_max, qi, len, hh);
         out_scale = 1.0f;
     }
     if (qi < len) {
@@ -591,8 +625,53 @@ __global__ __launch_bounds__(NTH) void k_attention_h(const float *__restrict__ q
     }
 }
 
+// Combines the nsplit partial results of each split task (k_attention_h):
+// O = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s (the
+// running maxima are in base-2 units).  One thread per (task, query, 4 dims).
+template <int HD>
+__global__ __launch_bounds__(256) void k_attention_merge(const float *__restrict__ part, int ntask, int nsplit,
+                                                         int nfull, int H, int nq, int QB, const int *__restrict__ cu,
+                                                         const int *__restrict__ lens, int d, void *__restrict__ out,
+                                                         int out_fmt) {
+    constexpr int G = HD / 4;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)ntask * QB * G) return;
+    const int st = (int)(i / ((long)QB * G)), rem = (int)(i % ((long)QB * G)), q = rem / G, c = 4 * (rem % G);
+    const int task = nfull + st, qb = task % nq, h = (task / nq) % H, b = task / nq / H;
+    const int qi = qb * QB + q;
+    if (qi >= lens[b]) return;
+    const float *p0 = part + ((size_t)st * nsplit * QB + q) * (HD + 2);
+    const size_t step = (size_t)QB * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, p0[s * step + HD]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    for (int s = 0; s < nsplit; s++) {
+        const float *ps = p0 + s * step;
+        const float w = __builtin_amdgcn_exp2f(ps[HD] - M);  // an empty range: m = -inf, w = 0
+        L += w * ps[HD + 1];
+        o0 += w * ps[c];
+        o1 += w * ps[c + 1];
+        o2 += w * ps[c + 2];
+        o3 += w * ps[c + 3];
+    }
+    const float inv = 1.0f / L;
+    const float4 v = make_float4(o0 * inv, o1 * inv, o2 * inv, o3 * inv);
+    const size_t row = (size_t)cu[b] + qi;
+    if (out_fmt == AF_X3)
+        x3_store4(reinterpret_cast<unsigned short *>(out), row, h * HD + c, d, v);
+    else if (out_fmt == AF_H2)
+        h2_store4(reinterpret_cast<unsigned short *>(out), row, h * HD + c, d, v);
+    else
+        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + row * d + h * HD + c) = v;
+}
+
+// Rows of partial results the key split may use: one row per query of a
+// workgroup slot, two rounds of 256-query (or four of 128-query) slots.
+size_t attention_part_floats(int hd) { return (size_t)device_cus() * 512 * (hd + 2); }
+
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos, const float *rope_sin,
-                            void *out, int out_fmt, float *P, int64_t pb, int64_t ph, float *rowsum, hipStream_t st) {
+                            void *out, int out_fmt, float *P, int64_t pb, int64_t ph, float *rowsum, float *part,
+                            size_t part_floats, hipStream_t st) {
     if (rowsum && !P) return hipErrorInvalidValue;
     if ((out_fmt == AF_X3 || out_fmt == AF_H2) && d % 32) return hipErrorInvalidValue;
     const int hd = d / H;
@@ -606,20 +685,51 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     bool wide = (long)((sm.S_max + 255) / 256) * H * sm.B >= 512;
     if (qe && !strcmp(qe, "128")) wide = false;
     if (qe && !strcmp(qe, "256")) wide = true;
-    const dim3 grid((sm.S_max + 127) / 128, H, sm.B), grid_w((sm.S_max + 255) / 256, H, sm.B);
-#define CIH_ATT_K(KER, HDV, ONE, ...)                                                                           \
-    hipLaunchKernelGGL((KER<HDV, ONE, ##__VA_ARGS__>), grid, dim3(256), 0, st, qkv, d, sm.cu, sm.lens, sm.S_max, \
-                       rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum)
-#define CIH_ATT_W(HDV, ONE)                                                                                    \
-    hipLaunchKernelGGL((k_attention_h<HDV, ONE, 512>), grid_w, dim3(512), 0, st, qkv, d, sm.cu, sm.lens,       \
-                       sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum)
+    const int QB = wide ? 256 : 128, nq = (sm.S_max + QB - 1) / QB;
+    const int tasks = sm.B * H * nq;
+    // Key split (no probability export): when the tasks do not fill one round
+    // of the 'slots' workgroups resident at once (two of 256 or four of 128
+    // queries per CU), each is cut into nsplit key ranges (at least two
+    // 32-key tiles each) so that they do (a single 402-token sequence: 80
+    // tasks in six ranges, attention 41 -> 27 us per layer).  Splitting only
+    // the tasks past the last whole round of a larger batch measured no gain
+    // (the headline batch: 640 tasks on 512 slots, 3.85 vs 3.82 ms per
+    // forward): the parts repeat the query staging and add the merge.
+    // CIH_ATT_SPLIT=0 or CIH_SPLITK=0 turn it off.
+    int nfull = tasks, nsplit = 1;
+    const char *se = getenv("CIH_ATT_SPLIT"), *ke = getenv("CIH_SPLITK");
+    const bool split_ok = !P && !fp32 && part && !(se && !strcmp(se, "0")) && !(ke && !strcmp(ke, "0"));
+    const int slots = 2 * device_cus() * (wide ? 1 : 2);
+    if (split_ok && tasks < slots) {
+        const int full = 0, rest = tasks;
+        int ns = std::min(slots / rest, (sm.S_max + 31) / 32 / 2);
+        while (ns > 1 && (size_t)rest * ns * QB * (hd + 2) > part_floats) ns--;
+        if (ns > 1) {
+            nfull = full;
+            nsplit = ns;
+        }
+    }
+    const int grid = nfull + (tasks - nfull) * nsplit;
+#define CIH_ATT_K(KER, HDV, ONE)                                                                                \
+    hipLaunchKernelGGL((KER<HDV, ONE>), dim3((sm.S_max + 127) / 128, H, sm.B), dim3(256), 0, st, qkv, d, sm.cu, \
+                       sm.lens, sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph,     \
+                       inv_scale, rowsum)
+#define CIH_ATT_H(HDV, ONE, NTH)                                                                                 \
+    hipLaunchKernelGGL((k_attention_h<HDV, ONE, NTH>), dim3(grid), dim3(NTH), 0, st, qkv, d, sm.cu, sm.lens,     \
+                       sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum, \
+                       H, nq, nfull, nsplit, part)
 #define CIH_ATT(HDV)                                                                                           \
     if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                          \
     else if (fp32) CIH_ATT_K(k_attention, HDV, true);                                                           \
-    else if (P && wide) CIH_ATT_W(HDV, false);                                                                  \
-    else if (P) CIH_ATT_K(k_attention_h, HDV, false);                                                           \
-    else if (wide) CIH_ATT_W(HDV, true);                                                                        \
-    else CIH_ATT_K(k_attention_h, HDV, true);
+    else if (P && wide) CIH_ATT_H(HDV, false, 512);                                                             \
+    else if (P) CIH_ATT_H(HDV, false, 256);                                                                     \
+    else if (wide) CIH_ATT_H(HDV, true, 512);                                                                   \
+    else CIH_ATT_H(HDV, true, 256);                                                                             \
+    if (nsplit > 1) {                                                                                           \
+        const long n = (long)(tasks - nfull) * QB * (HDV / 4);                                                  \
+        hipLaunchKernelGGL((k_attention_merge<HDV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, \
+                           tasks - nfull, nsplit, nfull, H, nq, QB, sm.cu, sm.lens, d, out, out_fmt);           \
+    }
     switch (hd) {
     case 16: CIH_ATT(16) break;
     case 24: CIH_ATT(24) break;
@@ -628,7 +738,7 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     default: return hipErrorInvalidValue;
     }
 #undef CIH_ATT
-#undef CIH_ATT_W
+#undef CIH_ATT_H
 #undef CIH_ATT_K
     return hipGetLastError();
 }

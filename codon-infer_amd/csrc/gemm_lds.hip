@@ -352,19 +352,6 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
 // 3 rounds instead of 3.75; N = 1280: one round instead of 1.25); at
 // M = 2552 (a ragged 8-sequence batch) 128 x 320 for QKV, 128 x 256 for FC1,
 // 128 x 128 for Wo and FC2, as measured.
-int device_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-            cus = n;
-        else
-            cus = 256;
-    }
-    return cus;
-}
-
 int tile_choice(int M, int N) {
     const int cus = device_cus();
     const long mt = (M + 127) / 128;
@@ -399,6 +386,19 @@ hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void
 }
 
 }  // namespace
+
+int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
 
 bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi) {
     if (!W.q16 || a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || W.K % 32 || M <= 0) return false;

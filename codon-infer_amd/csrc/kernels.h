@@ -66,6 +66,9 @@ __device__ __forceinline__ void tile_xcd(int bid, int total, int nM, int nN, int
     nt = r / gsize;
 }
 
+// Compute units of the current device (queried once; 256 if the query fails).
+int device_cus();
+
 // Device buffer for partial sums of k-split GEMMs and GEMVs (one stream uses
 // it at a time).  A split-K GEMM needs at most SPLITK_PART_FLOATS floats.
 struct PartialBuf {
@@ -151,9 +154,13 @@ hipError_t launch_layernorm(const float *x, const float *w, const float *b, void
 // P) receives rowsum[b][h][q] = sum of row q over the residue keys 1..len-2,
 // for residue queries.
 // out: [T][d] FP32 (out_fmt AF_F32) or a limb format (AF_X3 / AF_H2).
+// Without P, tasks that would leave workgroup slots idle are split over key
+// ranges whose partial results (part, part_floats floats; nullptr: no split)
+// a merge kernel combines; attention_part_floats(hd) floats always suffice.
 hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const float *rope_cos,
                             const float *rope_sin, void *out, int out_fmt, float *P, int64_t pb, int64_t ph,
-                            float *rowsum, hipStream_t st);
+                            float *rowsum, float *part, size_t part_floats, hipStream_t st);
+size_t attention_part_floats(int hd);
 
 // final_att[b][p][t] = sum_h P_h[p][t] * (1/H), h ascending
 hipError_t launch_head_mean(const float *P, int64_t pb, int64_t ph, int H, SeqMeta sm, float *final_att,

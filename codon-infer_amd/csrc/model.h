@@ -47,6 +47,8 @@ struct Workspace {
     float *M = nullptr, *r = nullptr, *coef = nullptr;  // contacts
     float *rowsum = nullptr, *colpart = nullptr;        // contacts: map row sums, column partial sums
     PartialBuf part;                                    // partial sums of k-split GEMMs / GEMVs
+    float *attp = nullptr;                              // partial results of key-split attention
+    size_t attp_floats = 0;
     int *dms_meta = nullptr;                            // [max(maxB, maxS)][2] scored row, wild type
     float *dms_out = nullptr;                           // [max(maxB, maxS)][21] deltas, entropy
     // device staging of outputs for host-pointer calls (padded layouts)

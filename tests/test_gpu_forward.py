@@ -289,6 +289,7 @@ def test_attention_query_block_size_is_invisible(with_maps, monkeypatch):
     cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
     flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | (ch.OUT_CONTACTS | ch.OUT_FINAL_ATT if with_maps else 0)
     seqs = [rand_tokens(rng, n) for n in (298, 97, 255, 30)]
+    monkeypatch.setenv("CIH_ATT_SPLIT", "0")  # the key split (tested below) depends on the block size
     res = {}
     for qb in ("128", "256"):
         monkeypatch.setenv("CIH_ATT_QB", qb)
@@ -303,3 +304,36 @@ def test_attention_query_block_size_is_invisible(with_maps, monkeypatch):
             a, b = (a[:n - 2, :n - 2], b[:n - 2, :n - 2]) if k == "contacts" else \
                    ((a[:n, :n], b[:n, :n]) if k == "final_att" else (a[:n], b[:n]))
             assert np.array_equal(a, b), (with_maps, k, i)
+
+
+@pytest.mark.parametrize("case", ["one", "three"])
+def test_attention_key_split(case, monkeypatch):
+    """Attention tasks (sequence, head, query block) that do not fill one round
+    of workgroup slots run as key ranges whose partial softmax results a merge
+    kernel combines: one 402-token sequence (80 tasks of 128 queries, six
+    ranges), or three ragged sequences.  The forward agrees with the unsplit
+    one (CIH_ATT_SPLIT=0) to 1e-5 and with the oracle to the stated
+    tolerances."""
+    rng = np.random.default_rng(77)
+    cfg = ch.EsmConfig(320, 1280, 2, 20)
+    lens = [400] if case == "one" else [300, 61, 190]
+    seqs = [rand_tokens(rng, n) for n in lens]
+    w = ch.EsmWeights.random(cfg, seed=77, bias_std=0.02).quantize_q8()
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN
+    res = {}
+    for sp in ("0", "1"):
+        monkeypatch.setenv("CIH_ATT_SPLIT", sp)
+        m = ch.GpuModel(cfg, w, max_batch=len(seqs), max_len=max(len(t) for t in seqs), outputs=flags)
+        res[sp] = m.forward(seqs, flags)
+        m.close()
+    for i, t in enumerate(seqs):
+        n = len(t)
+        for k in ("logits", "hidden"):
+            e = float(np.abs(res["1"][k][i, :n] - res["0"][k][i, :n]).max())
+            assert e <= 1e-5, (case, i, k, e)
+    ref = cr.forward(cfg, w, seqs[-1], 4, final_att=False)
+    n = len(seqs[-1])
+    for k in ("logits", "hidden"):
+        e = float(np.abs(res["1"][k][-1, :n].astype(np.float64) - ref[k]).max())
+        print(case, k, f"{e:.2e}", flush=True)
+        assert e <= TOL[k], (case, k, e)
