@@ -53,13 +53,14 @@ template <int RT, int CT, int WM, int WN> struct LdsTile {
     static constexpr int NA = (LA + NW - 1) / NW, NB = (LB + NW - 1) / NW;
     static constexpr int SL = BN / NW;      // scales per wave and block (4-byte loads)
     static constexpr int NI = NA + NB + 1;  // load instructions per wave and block
-    static constexpr int OCC = 512 / THREADS;  // workgroups per CU: two waves per SIMD
+    static constexpr int OCC = THREADS >= 512 ? 1 : 512 / THREADS;  // workgroups per CU
+    static constexpr int WPE = NW / 4 * OCC;  // waves per SIMD (HIP's second launch bound)
     static_assert(SA % 1024 == 0 && SB % 1024 == 0 && LA >= NW && LB >= NW, "loads");
     static_assert(BN % NW == 0 && SL <= 64 && OCC * 3 * STAGE <= 160 * 1024, "tile");
 };
 
 template <int EPI, int RT, int CT, int WM, int WN>
-__global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::OCC)) void k_gemm_lds(
+__global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned short *__restrict__ W16, const float *__restrict__ Wsc,
     const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K) {
     using T = LdsTile<RT, CT, WM, WN>;
