@@ -17,6 +17,8 @@
 // A and the raw quantized B tile are double-buffered in LDS; the next k-block
 // is fetched into registers while the current one is multiplied.
 #include <stdlib.h>
+
+#include <algorithm>
 #include <string.h>
 
 #include "kernels.h"
@@ -53,10 +55,13 @@ __device__ __forceinline__ void tile_of(int bid, int total, int nM, int nN, int 
     nt = r / gsize;
 }
 
-template <int WF, int EPI, int BM, int BN>
+// SPLIT: workgroup (tile, y) sums k-blocks [y * kps, (y + 1) * kps) only and,
+// with part, leaves the raw sums in part[y][M][N] for k_splitk_reduce.
+template <int WF, int EPI, int BM, int BN, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void k_gemm(const float *__restrict__ X, int ldx, const void *__restrict__ Wq,
                                                  const float *__restrict__ Wsc, const float *__restrict__ bias,
-                                                 float *__restrict__ Y, int ldy, int M, int N, int K) {
+                                                 float *__restrict__ Y, int ldy, int M, int N, int K, int kps,
+                                                 float *__restrict__ part) {
     constexpr int MT = BM / 64;  // 32-row MFMA tiles per wave
     constexpr int NT = BN / 64;  // 32-col MFMA tiles per wave
     constexpr int A_LOADS = BM / 32;  // float4 per thread for the A tile
@@ -160,13 +165,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const float *__restrict__ X, in
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
 
-    gload(0);
+    const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kend = SPLIT ? min(KB, kb0 + kps) : KB;
+    gload(kb0);
     sstore(0);
     __syncthreads();
 
-    for (int kb = 0; kb < KB; kb++) {
-        const int cur = kb & 1;
-        if (kb + 1 < KB) gload(kb + 1);
+    for (int kb = kb0; kb < kend; kb++) {
+        const int cur = (kb - kb0) & 1;
+        if (kb + 1 < kend) gload(kb + 1);
 
         float a[MT][16];
 #pragma unroll
@@ -218,59 +224,127 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const float *__restrict__ X, in
                 for (int c = 0; c < NT; c++)
                     acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[r][s], b[c][s], acc[r][c], 0, 0, 0);
 
-        if (kb + 1 < KB) sstore(cur ^ 1);
+        if (kb + 1 < kend) sstore(cur ^ 1);
         __syncthreads();
     }
 
     // ---- epilogue: lane holds column li of each 32x32 tile, rows 8*(q/4) + 4*hh + q%4
+    if (SPLIT && part) {  // raw partial sums; bias and epilogue in k_splitk_reduce
 #pragma unroll
-    for (int c = 0; c < NT; c++) {
-        const int col = n0 + wn * (BN / 2) + c * 32 + li;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
+        for (int c = 0; c < NT; c++) {
+            const int col = n0 + wn * (BN / 2) + c * 32 + li;
+            if (col >= N) continue;
 #pragma unroll
-        for (int r = 0; r < MT; r++) {
+            for (int r = 0; r < MT; r++)
 #pragma unroll
-            for (int q = 0; q < 16; q++) {
-                const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                if (row < M) {
-                    float v = acc[r][c][q] + bv;
-                    float *dst = Y + (size_t)row * ldy + col;
-                    if constexpr (EPI == EPI_GELU) v = gelu_as(v);
-                    if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
-                    *dst = v;
+                for (int q = 0; q < 16; q++) {
+                    const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    if (row < M) part[((size_t)blockIdx.y * M + row) * N + col] = acc[r][c][q];
                 }
-            }
+        }
+        return;
+    }
+    // Every output value is formed before the first store (bias and residual
+    // reads share one wait, and no store follows a pending load, which would
+    // make the compiler wait for each earlier store at every bounds branch);
+    // tiles inside the matrix store without bounds branches.
+    float bv[NT];
+#pragma unroll
+    for (int c = 0; c < NT; c++) bv[c] = bias ? bias[min(n0 + wn * (BN / 2) + c * 32 + li, N - 1)] : 0.0f;
+    float res[NT][MT][16];
+    if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const int col = min(n0 + wn * (BN / 2) + c * 32 + li, N - 1);
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int row = min(m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3), M - 1);
+                    res[c][r][q] = Y[(size_t)row * ldy + col];
+                }
         }
     }
+#pragma unroll
+    for (int c = 0; c < NT; c++)
+#pragma unroll
+        for (int r = 0; r < MT; r++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                float v = acc[r][c][q] + bv[c];
+                if constexpr (EPI == EPI_GELU) v = gelu_as(v);
+                if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
+                acc[r][c][q] = v;
+            }
+    auto store = [&](bool guard) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const int col = n0 + wn * (BN / 2) + c * 32 + li;
+            if (guard && col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < MT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int row = m0 + wm * (BM / 2) + r * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    if (guard && row >= M) continue;
+                    Y[(size_t)row * ldy + col] = acc[r][c][q];
+                }
+        }
+    };
+    if (m0 + BM <= M && n0 + BN <= N)
+        store(false);
+    else
+        store(true);
 }
 
+// Split K when the tiles alone leave the GPU mostly idle (small token
+// counts: 256 tokens of the 8M model give 6-20 workgroups): up to ~1024
+// workgroups, at least 4 k-blocks per split, partials within pb; the ordered
+// reduction then adds bias and the epilogue.  CIH_SPLITK=0 turns it off.
 template <int WF, int EPI, int BM, int BN>
 static hipError_t launch_t(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
-                           hipStream_t st) {
-    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm<WF, EPI, BM, BN>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc, bias, Y, ldy, M,
-                       W.N, W.K);
+                           const PartialBuf *pb, hipStream_t st) {
+    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN, KB = W.K / 32;
+    const long wgs = (long)nM * nN;
+    int S = 1, kps = KB;
+    const char *e = getenv("CIH_SPLITK");
+    if (pb && pb->part && !(e && !strcmp(e, "0")) && wgs < 512 && KB >= 8) {
+        S = (int)std::min<long>(1024 / wgs, KB / 4);
+        while (S > 1 && (size_t)S * M * W.N > pb->floats) S--;
+        if (S > 1) {
+            kps = (KB + S - 1) / S;
+            S = (KB + kps - 1) / kps;
+        }
+    }
+    if (S > 1) {
+        hipLaunchKernelGGL((k_gemm<WF, EPI, BM, BN, true>), dim3(nM * nN, S), dim3(256), 0, st, X, ldx, W.q, W.sc,
+                           bias, Y, ldy, M, W.N, W.K, kps, pb->part);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        return launch_splitk_reduce(pb->part, S, M, W.N, bias, Y, ldy, EPI, st);
+    }
+    hipLaunchKernelGGL((k_gemm<WF, EPI, BM, BN, false>), dim3(nM * nN), dim3(256), 0, st, X, ldx, W.q, W.sc, bias, Y,
+                       ldy, M, W.N, W.K, KB, nullptr);
     return hipGetLastError();
 }
 
 template <int WF, int EPI>
 static hipError_t launch_shape(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy,
-                               int M, hipStream_t st) {
+                               int M, const PartialBuf *pb, hipStream_t st) {
     const bool small_m = M <= 64, small_n = W.N <= 64;
-    if (small_m && small_n) return launch_t<WF, EPI, 64, 64>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_m) return launch_t<WF, EPI, 64, 128>(W, X, ldx, bias, Y, ldy, M, st);
-    if (small_n) return launch_t<WF, EPI, 128, 64>(W, X, ldx, bias, Y, ldy, M, st);
-    return launch_t<WF, EPI, 128, 128>(W, X, ldx, bias, Y, ldy, M, st);
+    if (small_m && small_n) return launch_t<WF, EPI, 64, 64>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    if (small_m) return launch_t<WF, EPI, 64, 128>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    if (small_n) return launch_t<WF, EPI, 128, 64>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    return launch_t<WF, EPI, 128, 128>(W, X, ldx, bias, Y, ldy, M, pb, st);
 }
 
 template <int WF>
 static hipError_t launch_epi(const DevMatrix &W, const float *X, int ldx, const float *bias, float *Y, int ldy, int M,
-                             int epi, hipStream_t st) {
+                             int epi, const PartialBuf *pb, hipStream_t st) {
     switch (epi) {
-    case EPI_GELU: return launch_shape<WF, EPI_GELU>(W, X, ldx, bias, Y, ldy, M, st);
-    case EPI_RESIDUAL: return launch_shape<WF, EPI_RESIDUAL>(W, X, ldx, bias, Y, ldy, M, st);
-    default: return launch_shape<WF, EPI_NONE>(W, X, ldx, bias, Y, ldy, M, st);
+    case EPI_GELU: return launch_shape<WF, EPI_GELU>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    case EPI_RESIDUAL: return launch_shape<WF, EPI_RESIDUAL>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    default: return launch_shape<WF, EPI_NONE>(W, X, ldx, bias, Y, ldy, M, pb, st);
     }
 }
 
@@ -289,9 +363,9 @@ hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, c
     if (a_fmt != AF_F32 || epi == EPI_GELU_X3 || epi == EPI_GELU_H2 || ldx % 4 != 0) return hipErrorInvalidValue;
     const float *X = reinterpret_cast<const float *>(Xv);
     float *Y = reinterpret_cast<float *>(Yv);
-    if (W.fmt == WF_Q8) return launch_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    if (W.fmt == WF_Q4) return launch_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, st);
-    return launch_epi<WF_F32>(W, X, ldx, bias, Y, ldy, M, epi, st);
+    if (W.fmt == WF_Q8) return launch_epi<WF_Q8>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+    if (W.fmt == WF_Q4) return launch_epi<WF_Q4>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+    return launch_epi<WF_F32>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
 }
 
 // Test path: k-block-major device matrix -> row-major [N][K] FP32, with the

@@ -446,6 +446,12 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     }
 }
 
+hipError_t launch_splitk_reduce(const float *part, int S, int M, int N, const float *bias, void *Y, int ldy, int epi,
+                                hipStream_t st) {
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((M * N + 255) / 256), dim3(256), 0, st, part, S, M, N, bias, Y, ldy, epi);
+    return hipGetLastError();
+}
+
 template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
 static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy, int M,
                               const PartialBuf *pb, hipStream_t st) {

@@ -66,6 +66,11 @@ __device__ __forceinline__ void tile_xcd(int bid, int total, int nM, int nN, int
     nt = r / gsize;
 }
 
+// Y = epi(sum over s < S of part[s][M][N] + bias), splits in order (the
+// reduction of the split-K GEMMs).
+hipError_t launch_splitk_reduce(const float *part, int S, int M, int N, const float *bias, void *Y, int ldy, int epi,
+                                hipStream_t st);
+
 // Compute units of the current device (queried once; 256 if the query fails).
 int device_cus();
 

@@ -175,8 +175,10 @@ def test_forward_650m_q8_short():
 def test_forward_headline_shape(monkeypatch):
     """The benchmark workload itself (650M Q8_0, B=16, L=512: the largest GEMM
     tiles and the f16-limb hand-off at full size).  One sequence of the batch
-    against the oracle, another bit-identical alone (GEMMs unsplit) and
-    inside the batch."""
+    against the oracle; with every split off (CIH_SPLITK=0: the LM head's
+    33-wide decoder GEMM splits K by default even here), another sequence is
+    bit-identical alone and inside the batch, and the default batch agrees
+    with the unsplit one to 1e-5."""
     rng = np.random.default_rng(650)
     cfg = ch.EsmConfig.esm2_650m()
     w = ch.EsmWeights.random(cfg, seed=650, bias_std=0.02).quantize_q8()
@@ -194,8 +196,11 @@ def test_forward_headline_shape(monkeypatch):
     clear = (top2[:, 1] - top2[:, 0]) > 2e-3
     assert np.array_equal(got["logits"][0].argmax(1)[clear], ref["logits"].argmax(1)[clear])
     monkeypatch.setenv("CIH_SPLITK", "0")
+    monkeypatch.setenv("CIH_FORWARD_GRAPH", "0")  # a replayed graph keeps the splits it was captured with
+    unsplit = m.forward(seqs, flags)
+    assert float(np.abs(unsplit["logits"] - got["logits"]).max()) <= 1e-5
     alone = m.forward([seqs[5]], flags)
-    assert np.array_equal(alone["logits"][0], got["logits"][5])
+    assert np.array_equal(alone["logits"][0], unsplit["logits"][5])
     m.close()
 
 
