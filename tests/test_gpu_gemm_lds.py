@@ -46,10 +46,15 @@ def assert_same(got, ref, seqs, what):
             assert np.array_equal(g, r), (what, i, k, float(np.abs(g - r).max()))
 
 
+@pytest.mark.parametrize("tile", ["model", "128", "160", "256", "320"])
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
-def test_forced_lds_gemm_is_bit_identical(fmt, monkeypatch):
+def test_forced_lds_gemm_is_bit_identical(fmt, tile, monkeypatch):
     """Ragged shapes: token count 687 and projection widths 576 / 192 / 768
-    are not multiples of the 128 x 128 or 128 x 256 tiles, FC2 has K = 768."""
+    are not multiples of any tile (128 x 128, 128 x 160, 128 x 256 and
+    128 x 320, forced through CIH_GEMM_TILE_N, or the round model's choice),
+    FC2 has K = 768."""
+    if tile != "model":
+        monkeypatch.setenv("CIH_GEMM_TILE_N", tile)
     rng = np.random.default_rng(11)
     cfg = ch.EsmConfig(192, 768, 2, 3)
     w = ch.EsmWeights.random(cfg, seed=11, bias_std=0.02)
@@ -61,7 +66,7 @@ def test_forced_lds_gemm_is_bit_identical(fmt, monkeypatch):
     monkeypatch.setenv("CIH_SPLITK", "0")
     b = lds.forward(seqs, FLAGS)
     a = ref.forward(seqs, FLAGS)
-    print(f"{fmt}: forced LDS GEMM forward equals the register-staged one", flush=True)
+    print(f"{fmt} tile {tile}: forced LDS GEMM forward equals the register-staged one", flush=True)
     assert_same(b, a, seqs, fmt)
     ref.close()
     lds.close()
