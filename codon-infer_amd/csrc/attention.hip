@@ -308,10 +308,6 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ qkv
     }
 }
 
-__device__ __forceinline__ f16x8 cat4(f16x4 a, f16x4 b) {
-    return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
 // hi/lo f16 limbs of 8 floats
 __device__ __forceinline__ void split8(const float *v, f16x8 &hi, f16x8 &lo) {
 #pragma unroll
@@ -441,8 +437,11 @@ __global__ __launch_bounds__(NTH, ONEPASS ? 4 : 1) void k_attention_h(const floa
                 hv[e] = (_Float16)v;
                 lv[e] = (_Float16)(v - (float)hv[e]);
             }
-            *reinterpret_cast<f16x4 *>(&Vh[c * V_LD + kg]) = hv;
-            *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + kg]) = lv;
+            // 4-key groups 0, 1, 2, 3 of each 16-key chunk stored as 0, 2, 1, 3, so
+            // the keys one lane half feeds an MFMA are 8 consecutive f16
+            const int pos = (kg & ~15) | ((kg & 4) << 1) | ((kg & 8) >> 1);
+            *reinterpret_cast<f16x4 *>(&Vh[c * V_LD + pos]) = hv;
+            *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + pos]) = lv;
         }
     };
     // S^T tile (32 keys x 32 queries): A = K rows (keys), B = Q columns (queries)
@@ -469,10 +468,8 @@ __global__ __launch_bounds__(NTH, ONEPASS ? 4 : 1) void k_attention_h(const floa
             const int row = (t * 32 + li) * V_LD;
 #pragma unroll
             for (int c = 0; c < 2; c++) {
-                const f16x8 vh = cat4(*reinterpret_cast<const f16x4 *>(&Vh[row + 16 * c + 4 * hh]),
-                                      *reinterpret_cast<const f16x4 *>(&Vh[row + 16 * c + 8 + 4 * hh]));
-                const f16x8 vl = cat4(*reinterpret_cast<const f16x4 *>(&Vl[row + 16 * c + 4 * hh]),
-                                      *reinterpret_cast<const f16x4 *>(&Vl[row + 16 * c + 8 + 4 * hh]));
+                const f16x8 vh = *reinterpret_cast<const f16x8 *>(&Vh[row + 16 * c + 8 * hh]);
+                const f16x8 vl = *reinterpret_cast<const f16x8 *>(&Vl[row + 16 * c + 8 * hh]);
                 oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, phi[c], oacc[t], 0, 0, 0);
                 oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, plo[c], oacc[t], 0, 0, 0);
                 oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, phi[c], oacc[t], 0, 0, 0);
