@@ -21,8 +21,9 @@
 // supplies at step s.
 // When probabilities are requested (attention maps, contacts, last-layer
 // map): two passes over the keys — pass 1 keeps a running max/sum per lane,
-// pass 2 recomputes the scores, forms p = exp(s - max) * (1/sum) exactly as
-// the reference does, stores P and accumulates P.V.  Otherwise one pass with
+// pass 2 recomputes the scores, forms p = exp(s - max) * (1/sum) as the
+// reference does (k_attention_h: base 2, on scores pre-scaled by log2(e)),
+// stores P and accumulates P.V.  Otherwise one pass with
 // an online softmax (P.V accumulated unnormalised, divided by the sum once).
 // RoPE is applied while staging K into LDS and Q into registers, from the
 // host-built cos/sin tables (the reference's f32 powf/cos/sin values).
@@ -47,6 +48,7 @@
 namespace cih {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
@@ -323,7 +325,7 @@ __device__ __forceinline__ void split8(const float *v, f16x8 &hi, f16x8 &lo) {
 // that leave their unnormalized output, running max and sum in part for
 // k_attention_merge.
 template <int HD, bool ONEPASS, int NTH = 256>
-__global__ __launch_bounds__(NTH, ONEPASS ? 4 : 1) void k_attention_h(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
+__global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_h(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
                                                      const int *__restrict__ lens, int S_max,
                                                      const float *__restrict__ rc, const float *__restrict__ rsn,
                                                      void *__restrict__ out, int out_fmt, float *__restrict__ P,
@@ -551,12 +553,90 @@ __global__ __launch_bounds__(NTH, ONEPASS ? 4 : 1) void k_attention_h(const floa
         }
         out_scale = 1.0f / lt;
     } else {
+        // Two passes over the keys (the exported probabilities are final, so
+        // the row max and sum come first), base-2 exponentials of scores
+        // pre-scaled by log2(e) / sqrt(hd).  With one 32-query wave per SIMD
+        // slot and few waves, a tile's global loads are the critical path:
+        // they go to registers one tile ahead (fetch) and into LDS as f16
+        // limbs after the barrier (stage), so tile t+1 is in flight while
+        // tile t is computed.
+        const float sl2 = inv_scale * 1.44269504088896340736f;
+        constexpr int KG = HALF / 4, KI = (32 * KG + NTH - 1) / NTH, VI = (8 * HD + NTH - 1) / NTH;
+        f32x4 kr[KI][4], vr[VI];
+        auto fetch = [&](int kt0, bool with_v) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < KI; i++) {
+                const int idx = tid + i * NTH;
+                if (idx < 32 * KG) {
+                    const int key = idx / KG, c = 4 * (idx % KG);
+                    const int kk = min(kt0 + key, len - 1);
+                    const float *krow = Kg + (size_t)(base + kk) * ld;
+                    kr[i][0] = *reinterpret_cast<const f32x4 *>(krow + c);
+                    kr[i][1] = *reinterpret_cast<const f32x4 *>(krow + c + HALF);
+                    kr[i][2] = *reinterpret_cast<const f32x4 *>(rc + (size_t)kk * HALF + c);
+                    kr[i][3] = *reinterpret_cast<const f32x4 *>(rsn + (size_t)kk * HALF + c);
+                }
+            }
+            if (!with_v) return;
+#pragma unroll
+            for (int i = 0; i < VI; i++) {
+                const int idx = tid + i * NTH;
+                if (idx < 8 * HD) {
+                    const int c = idx % HD, kg = 4 * (idx / HD);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) vr[i][e] = Vg[(size_t)(base + min(kt0 + kg + e, len - 1)) * ld + c];
+                }
+            }
+        };
+        auto stage = [&](bool with_v) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < KI; i++) {
+                const int idx = tid + i * NTH;
+                if (idx < 32 * KG) {
+                    const int key = idx / KG, c = 4 * (idx % KG);
+                    const f32x4 k0 = kr[i][0], k1 = kr[i][1], cs = kr[i][2], sn = kr[i][3];
+                    f16x4 h0, l0, h1, l1;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float r0 = k0[e] * cs[e] - k1[e] * sn[e];
+                        const float r1 = k1[e] * cs[e] + k0[e] * sn[e];
+                        h0[e] = (_Float16)r0;
+                        l0[e] = (_Float16)(r0 - (float)h0[e]);
+                        h1[e] = (_Float16)r1;
+                        l1[e] = (_Float16)(r1 - (float)h1[e]);
+                    }
+                    *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c]) = h0;
+                    *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c]) = l0;
+                    *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c + HALF]) = h1;
+                    *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c + HALF]) = l1;
+                }
+            }
+            if (!with_v) return;
+#pragma unroll
+            for (int i = 0; i < VI; i++) {
+                const int idx = tid + i * NTH;
+                if (idx < 8 * HD) {
+                    const int c = idx % HD, kg = 4 * (idx / HD);
+                    f16x4 hv, lv;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        hv[e] = (_Float16)vr[i][e];
+                        lv[e] = (_Float16)(vr[i][e] - (float)hv[e]);
+                    }
+                    const int pos = (kg & ~15) | ((kg & 4) << 1) | ((kg & 8) >> 1);  // as in load_v
+                    *reinterpret_cast<f16x4 *>(&Vh[c * V_LD + pos]) = hv;
+                    *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + pos]) = lv;
+                }
+            }
+        };
         // pass 1: running max / sum of exp per lane
         float m = -INFINITY, l = 0.0f;
+        fetch(0, false);
         for (int kt0 = 0; kt0 < len; kt0 += 32) {
             __syncthreads();
-            load_k(kt0);
+            stage(false);
             __syncthreads();
+            if (kt0 + 32 < len) fetch(kt0 + 32, false);
             f32x16 acc;
             scores(acc);
             float sv[16];
@@ -564,36 +644,37 @@ __global__ __launch_bounds__(NTH, ONEPASS ? 4 : 1) void k_attention_h(const floa
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                sv[q] = key < len ? acc[q] * inv_scale : -INFINITY;
+                sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
                 tmax = fmaxf(tmax, sv[q]);
             }
             const float mn = fmaxf(m, tmax);
             if (mn != -INFINITY) {
                 float sum = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 16; q++) sum += expf(sv[q] - mn);
-                l = l * expf(m - mn) + sum;
+                for (int q = 0; q < 16; q++) sum += __builtin_amdgcn_exp2f(sv[q] - mn);
+                l = l * __builtin_amdgcn_exp2f(m - mn) + sum;
                 m = mn;
             }
         }
         const float mo = __shfl_xor(m, 32), lo = __shfl_xor(l, 32);
         const float mx = fmaxf(m, mo);
-        const float inv_sum = 1.0f / (l * expf(m - mx) + lo * expf(mo - mx));
+        const float inv_sum = 1.0f / (l * __builtin_amdgcn_exp2f(m - mx) + lo * __builtin_amdgcn_exp2f(mo - mx));
         // pass 2: normalized probabilities, optional export, P.V
         float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
         float rs = 0.0f;  // sum of this query's probabilities over residue keys (contacts)
+        fetch(0, true);
         for (int kt0 = 0; kt0 < len; kt0 += 32) {
             __syncthreads();
-            load_k(kt0);
-            load_v(kt0);
+            stage(true);
             __syncthreads();
+            if (kt0 + 32 < len) fetch(kt0 + 32, true);
             f32x16 acc;
             scores(acc);
             float p[16];
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                p[q] = key < len ? expf(acc[q] * inv_scale - mx) * inv_sum : 0.0f;
+                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - mx) * inv_sum : 0.0f;
             }
             if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
             if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);

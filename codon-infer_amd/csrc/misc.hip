@@ -304,25 +304,63 @@ __global__ __launch_bounds__(256) void k_apc_coef(const float *__restrict__ r, c
     }
 }
 
+// A 64 x 64 block of contacts per workgroup, 4 x 4 per thread (rows
+// i0 + 4ty + m, columns j0 + 4tx + k); the r vectors of 64 layer-heads at a
+// time are staged in LDS, where a thread's four rows and four columns are one
+// 16-byte read each.  Per output the arithmetic is the one-thread-per-output
+// form: corr = fma(c, r_i * r_j, corr) in layer-head order, skipping c == 0.
+constexpr int APC_FT = 64, APC_FL = 64;
 __global__ __launch_bounds__(256) void k_apc_final(const float *__restrict__ M, const float *__restrict__ r,
                                                    const float *__restrict__ coef, int LH, const int *__restrict__ lens,
                                                    int S_max, int B, float bias, float *__restrict__ out,
                                                    int n_stride) {
-    const int i = blockIdx.x, b = blockIdx.y;
+    const int b = blockIdx.z, i0 = blockIdx.y * APC_FT, j0 = blockIdx.x * APC_FT;
     const int n = lens[b] - 2, n_max = S_max - 2;
-    if (i >= n) return;
-    const float *Mb = M + (size_t)b * n_max * n_max;
-    for (int j = threadIdx.x; j < n; j += 256) {
-        float corr = 0.0f;
-        for (int lh = 0; lh < LH; lh++) {
-            const float c = coef[(size_t)lh * B + b];
-            if (c != 0.0f) {
-                const float *rr = r + ((size_t)lh * B + b) * n_max;
-                corr = fmaf(c, rr[i] * rr[j], corr);  // r_i r_j first: (i, j) and (j, i) round alike
-            }
+    if (i0 >= n || j0 >= n) return;
+    __shared__ __attribute__((aligned(16))) float ri[APC_FL][APC_FT], rj[APC_FL][APC_FT];
+    __shared__ float cs[APC_FL];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    float corr[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) corr[m][k] = 0.0f;
+    for (int lh0 = 0; lh0 < LH; lh0 += APC_FL) {
+        __syncthreads();
+        for (int e = tid; e < APC_FL * APC_FT; e += 256) {
+            const int lh = lh0 + e / APC_FT, x = e % APC_FT;
+            const float *rr = r + ((size_t)lh * B + b) * n_max;
+            const bool in = lh < LH;
+            ri[e / APC_FT][x] = in && i0 + x < n ? rr[i0 + x] : 0.0f;
+            rj[e / APC_FT][x] = in && j0 + x < n ? rr[j0 + x] : 0.0f;
         }
-        const float logit = Mb[(size_t)i * n_max + j] + Mb[(size_t)j * n_max + i] - corr;
-        out[((size_t)b * n_stride + i) * n_stride + j] = 1.0f / (1.0f + expf(-(logit + bias)));
+        if (tid < APC_FL) cs[tid] = lh0 + tid < LH ? coef[(size_t)(lh0 + tid) * B + b] : 0.0f;
+        __syncthreads();
+        const int nl = min(APC_FL, LH - lh0);
+        for (int t = 0; t < nl; t++) {
+            const float c = cs[t];
+            if (c == 0.0f) continue;
+            const float4 a = *reinterpret_cast<const float4 *>(&ri[t][4 * ty]);
+            const float4 q = *reinterpret_cast<const float4 *>(&rj[t][4 * tx]);
+            const float av[4] = {a.x, a.y, a.z, a.w}, qv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) corr[m][k] = fmaf(c, av[m] * qv[k], corr[m][k]);  // r_i r_j first: symmetric
+        }
+    }
+    const float *Mb = M + (size_t)b * n_max * n_max;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const int i = i0 + 4 * ty + m;
+        if (i >= n) continue;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int j = j0 + 4 * tx + k;
+            if (j >= n) continue;
+            const float logit = Mb[(size_t)i * n_max + j] + Mb[(size_t)j * n_max + i] - corr[m][k];
+            out[((size_t)b * n_stride + i) * n_stride + j] = 1.0f / (1.0f + expf(-(logit + bias)));
+        }
     }
 }
 
@@ -331,7 +369,8 @@ hipError_t launch_apc_finalize(const float *M, const float *r, float *coef, cons
     if (sm.S_max < 3) return hipSuccess;
     const int n_max = sm.S_max - 2;
     hipLaunchKernelGGL(k_apc_coef, dim3(LH, sm.B), dim3(256), 0, st, r, w_dev, sm.lens, sm.S_max, sm.B, coef);
-    hipLaunchKernelGGL(k_apc_final, dim3(n_max, sm.B), dim3(256), 0, st, M, r, coef, LH, sm.lens, sm.S_max, sm.B, bias,
+    const int nt = (n_max + APC_FT - 1) / APC_FT;
+    hipLaunchKernelGGL(k_apc_final, dim3(nt, nt, sm.B), dim3(256), 0, st, M, r, coef, LH, sm.lens, sm.S_max, sm.B, bias,
                        contacts, n_stride);
     return hipGetLastError();
 }
