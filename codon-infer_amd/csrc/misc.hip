@@ -223,6 +223,10 @@ hipError_t launch_head_mean(const float *P, int64_t pb, int64_t ph, int H, SeqMe
 constexpr int APC_ROWS = 32;  // map rows per workgroup of k_apc_tile
 constexpr int APC_HMAX = 40;  // most heads of any preset (3B)
 
+// HM >= nz heads per pass with branch-free loads (heads past nz repeat head
+// nz - 1 with weight 0 and are not written), two map rows per step, so a
+// thread has 2 * HM loads in flight.
+template <int HM>
 __global__ __launch_bounds__(256) void k_apc_tile(const float *__restrict__ P, long long pb, long long ph, int H,
                                                   int l, const float *__restrict__ w, const int *__restrict__ heads,
                                                   int nz, const int *__restrict__ lens, int S_max,
@@ -233,26 +237,53 @@ __global__ __launch_bounds__(256) void k_apc_tile(const float *__restrict__ P, l
     const int i0 = tile * APC_ROWS;
     if (j >= n || i0 >= n) return;
     const int i1 = min(i0 + APC_ROWS, n);
-    float cs[APC_HMAX];
+    long long off[HM];
+    float wk[HM], cs[HM];
 #pragma unroll
-    for (int k = 0; k < APC_HMAX; k++) cs[k] = 0.0f;
-    for (int i = i0; i < i1; i++) {
-        float *Mij = M + ((size_t)b * n_max + i) * n_max + j;
-        float acc = *Mij;
-        const float *row = P + b * pb + (size_t)(i + 1) * S_max + 1 + j;
+    for (int k = 0; k < HM; k++) {
+        const int h = heads[min(k, nz - 1)];
+        off[k] = h * ph;
+        wk[k] = k < nz ? w[l * H + h] : 0.0f;
+        cs[k] = 0.0f;
+    }
+    const float *P0 = P + b * pb + S_max + 1 + j;  // row i + 1, column j + 1
+    float *M0 = M + (size_t)b * n_max * n_max + j;
+    int i = i0;
+    for (; i + 2 <= i1; i += 2) {
+        const float *r0 = P0 + (size_t)i * S_max, *r1 = r0 + S_max;
+        float a0[HM], a1[HM];
 #pragma unroll
-        for (int k = 0; k < APC_HMAX; k++) {
-            if (k < nz) {
-                const int h = heads[k];
-                const float a = row[h * ph];
-                acc += w[l * H + h] * a;
-                cs[k] += a;
-            }
+        for (int k = 0; k < HM; k++) {
+            a0[k] = r0[off[k]];
+            a1[k] = r1[off[k]];
         }
-        *Mij = acc;
+        float acc0 = M0[(size_t)i * n_max], acc1 = M0[(size_t)(i + 1) * n_max];
+#pragma unroll
+        for (int k = 0; k < HM; k++) {
+            acc0 += wk[k] * a0[k];
+            cs[k] += a0[k];
+        }
+#pragma unroll
+        for (int k = 0; k < HM; k++) {
+            acc1 += wk[k] * a1[k];
+            cs[k] += a1[k];
+        }
+        M0[(size_t)i * n_max] = acc0;
+        M0[(size_t)(i + 1) * n_max] = acc1;
+    }
+    if (i < i1) {
+        const float *r0 = P0 + (size_t)i * S_max;
+        float acc0 = M0[(size_t)i * n_max];
+#pragma unroll
+        for (int k = 0; k < HM; k++) {
+            const float a = r0[off[k]];
+            acc0 += wk[k] * a;
+            cs[k] += a;
+        }
+        M0[(size_t)i * n_max] = acc0;
     }
 #pragma unroll
-    for (int k = 0; k < APC_HMAX; k++)
+    for (int k = 0; k < HM; k++)
         if (k < nz) colpart[(((size_t)b * H + heads[k]) * ntiles + tile) * n_max + j] = cs[k];
 }
 
@@ -277,9 +308,13 @@ hipError_t launch_apc_layer(const float *P, int64_t pb, int64_t ph, int H, int l
     if (n_heads_nz <= 0 || sm.S_max < 3) return hipSuccess;
     if (n_heads_nz > APC_HMAX || H > APC_HMAX) return hipErrorInvalidValue;
     const int n_max = sm.S_max - 2;
-    hipLaunchKernelGGL(k_apc_tile, dim3((n_max + APC_ROWS - 1) / APC_ROWS, (n_max + 255) / 256, sm.B), dim3(256), 0,
-                       st, P, (long long)pb, (long long)ph, H, l, w_dev, heads_dev, n_heads_nz, sm.lens, sm.S_max, M,
-                       colpart, sm.B);
+    const dim3 tg((n_max + APC_ROWS - 1) / APC_ROWS, (n_max + 255) / 256, sm.B);
+    if (n_heads_nz <= 20)
+        hipLaunchKernelGGL(k_apc_tile<20>, tg, dim3(256), 0, st, P, (long long)pb, (long long)ph, H, l, w_dev, heads_dev,
+                           n_heads_nz, sm.lens, sm.S_max, M, colpart, sm.B);
+    else
+        hipLaunchKernelGGL(k_apc_tile<APC_HMAX>, tg, dim3(256), 0, st, P, (long long)pb, (long long)ph, H, l, w_dev,
+                           heads_dev, n_heads_nz, sm.lens, sm.S_max, M, colpart, sm.B);
     hipLaunchKernelGGL(k_apc_r, dim3((n_max + 255) / 256, n_heads_nz, sm.B), dim3(256), 0, st, rowsum, colpart, H, l,
                        heads_dev, sm.lens, sm.S_max, r, sm.B);
     return hipGetLastError();
