@@ -339,8 +339,11 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     constexpr int DT = VW / 32;
     constexpr int K_LD = HDP + 8;             // f16 per LDS key row (16-byte aligned, padded)
     constexpr int V_LD = 32 + 8;              // f16 per LDS dim row of the transposed V tile
-    __shared__ __attribute__((aligned(16))) _Float16 Kh[32 * K_LD], Kl[32 * K_LD];
-    __shared__ __attribute__((aligned(16))) _Float16 Vh[VW * V_LD], Vl[VW * V_LD];
+    constexpr int NBUF = ONEPASS ? 1 : 2;     // the export kernel double-buffers its tiles
+    constexpr int KBUF = 32 * K_LD, VBUF = VW * V_LD;
+    __shared__ __attribute__((aligned(16))) _Float16 Kh[NBUF * KBUF], Kl[NBUF * KBUF];
+    __shared__ __attribute__((aligned(16))) _Float16 Vh[NBUF * VBUF], Vl[NBUF * VBUF];
+    int cur = 0;  // LDS buffer the current tile is read from
 
     int task = blockIdx.x, ks = 0, ns = 1;
     if (task >= nfull) {
@@ -364,16 +367,17 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
 
     // padding dims (HD..HDP of K, HD..VW of V) stay zero for every tile
     if constexpr (HDP > HD)
-        for (int idx = tid; idx < 32 * (HDP - HD); idx += NTH) {
-            const int key = idx / (HDP - HD), c = HD + idx % (HDP - HD);
+        for (int idx = tid; idx < NBUF * 32 * (HDP - HD); idx += NTH) {
+            const int key = idx / (HDP - HD), c = HD + idx % (HDP - HD);  // key spans the buffers
             Kh[key * K_LD + c] = (_Float16)0.0f;
             Kl[key * K_LD + c] = (_Float16)0.0f;
         }
     if constexpr (VW > HD)
-        for (int idx = tid; idx < (VW - HD) * 32; idx += NTH) {
-            const int c = HD + idx / 32, key = idx % 32;
-            Vh[c * V_LD + key] = (_Float16)0.0f;
-            Vl[c * V_LD + key] = (_Float16)0.0f;
+        for (int idx = tid; idx < NBUF * (VW - HD) * 32; idx += NTH) {
+            const int bf = idx / ((VW - HD) * 32), r = idx % ((VW - HD) * 32);
+            const int c = HD + r / 32, key = r % 32;
+            Vh[bf * VBUF + c * V_LD + key] = (_Float16)0.0f;
+            Vl[bf * VBUF + c * V_LD + key] = (_Float16)0.0f;
         }
 
     // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs
@@ -452,8 +456,8 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         for (int q = 0; q < 16; q++) acc[q] = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const f16x8 kh = *reinterpret_cast<const f16x8 *>(&Kh[li * K_LD + 16 * c + 8 * hh]);
-            const f16x8 kl = *reinterpret_cast<const f16x8 *>(&Kl[li * K_LD + 16 * c + 8 * hh]);
+            const f16x8 kh = *reinterpret_cast<const f16x8 *>(&Kh[cur * KBUF + li * K_LD + 16 * c + 8 * hh]);
+            const f16x8 kl = *reinterpret_cast<const f16x8 *>(&Kl[cur * KBUF + li * K_LD + 16 * c + 8 * hh]);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[c], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[c], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[c], acc, 0, 0, 0);
@@ -467,7 +471,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         split8(p + 8, phi[1], plo[1]);
 #pragma unroll
         for (int t = 0; t < DT; t++) {
-            const int row = (t * 32 + li) * V_LD;
+            const int row = cur * VBUF + (t * 32 + li) * V_LD;
 #pragma unroll
             for (int c = 0; c < 2; c++) {
                 const f16x8 vh = *reinterpret_cast<const f16x8 *>(&Vh[row + 16 * c + 8 * hh]);
@@ -588,7 +592,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 }
             }
         };
-        auto stage = [&](bool with_v) __attribute__((always_inline)) {
+        auto stage = [&](bool with_v, int bf) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < KI; i++) {
                 const int idx = tid + i * NTH;
@@ -605,10 +609,10 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                         h1[e] = (_Float16)r1;
                         l1[e] = (_Float16)(r1 - (float)h1[e]);
                     }
-                    *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c]) = h0;
-                    *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c]) = l0;
-                    *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c + HALF]) = h1;
-                    *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c + HALF]) = l1;
+                    *reinterpret_cast<f16x4 *>(&Kh[bf * KBUF + key * K_LD + c]) = h0;
+                    *reinterpret_cast<f16x4 *>(&Kl[bf * KBUF + key * K_LD + c]) = l0;
+                    *reinterpret_cast<f16x4 *>(&Kh[bf * KBUF + key * K_LD + c + HALF]) = h1;
+                    *reinterpret_cast<f16x4 *>(&Kl[bf * KBUF + key * K_LD + c + HALF]) = l1;
                 }
             }
             if (!with_v) return;
@@ -624,19 +628,32 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                         lv[e] = (_Float16)(vr[i][e] - (float)hv[e]);
                     }
                     const int pos = (kg & ~15) | ((kg & 4) << 1) | ((kg & 8) >> 1);  // as in load_v
-                    *reinterpret_cast<f16x4 *>(&Vh[c * V_LD + pos]) = hv;
-                    *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + pos]) = lv;
+                    *reinterpret_cast<f16x4 *>(&Vh[bf * VBUF + c * V_LD + pos]) = hv;
+                    *reinterpret_cast<f16x4 *>(&Vl[bf * VBUF + c * V_LD + pos]) = lv;
                 }
+            }
+        };
+        // One barrier per tile: tile t + 1 is staged into the other buffer
+        // right after the barrier that ends every wave's reads of tile t - 1
+        // there, then tile t + 2 is fetched and tile t computed.
+        auto sweep = [&](bool with_v, auto body) __attribute__((always_inline)) {
+            fetch(0, with_v);
+            __syncthreads();  // the previous sweep's reads of buffer 0 are done
+            stage(with_v, 0);
+            if (32 < len) fetch(32, with_v);
+            for (int kt0 = 0, t = 0; kt0 < len; kt0 += 32, t++) {
+                __syncthreads();
+                cur = t & 1;
+                if (kt0 + 32 < len) {
+                    stage(with_v, cur ^ 1);
+                    if (kt0 + 64 < len) fetch(kt0 + 64, with_v);
+                }
+                body(kt0);
             }
         };
         // pass 1: running max / sum of exp per lane
         float m = -INFINITY, l = 0.0f;
-        fetch(0, false);
-        for (int kt0 = 0; kt0 < len; kt0 += 32) {
-            __syncthreads();
-            stage(false);
-            __syncthreads();
-            if (kt0 + 32 < len) fetch(kt0 + 32, false);
+        sweep(false, [&](int kt0) __attribute__((always_inline)) {
             f32x16 acc;
             scores(acc);
             float sv[16];
@@ -655,19 +672,14 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 l = l * __builtin_amdgcn_exp2f(m - mn) + sum;
                 m = mn;
             }
-        }
+        });
         const float mo = __shfl_xor(m, 32), lo = __shfl_xor(l, 32);
         const float mx = fmaxf(m, mo);
         const float inv_sum = 1.0f / (l * __builtin_amdgcn_exp2f(m - mx) + lo * __builtin_amdgcn_exp2f(mo - mx));
         // pass 2: normalized probabilities, optional export, P.V
         float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
         float rs = 0.0f;  // sum of this query's probabilities over residue keys (contacts)
-        fetch(0, true);
-        for (int kt0 = 0; kt0 < len; kt0 += 32) {
-            __syncthreads();
-            stage(true);
-            __syncthreads();
-            if (kt0 + 32 < len) fetch(kt0 + 32, true);
+        sweep(true, [&](int kt0) __attribute__((always_inline)) {
             f32x16 acc;
             scores(acc);
             float p[16];
@@ -679,7 +691,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
             if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
             if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
             pv(oacc, p);
-        }
+        });
         write_rowsum(rowsum, rs, b, h, H, S_max, qi, len, hh);
         out_scale = 1.0f;
     }
