@@ -94,6 +94,19 @@ def test_forward_small_configs(hd, H, dtype, act, monkeypatch):
     check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(-0.5)))
 
 
+def test_contacts_forty_heads():
+    """Contacts with more than 20 weighted heads per layer (the 3B and 15B
+    head count, 40): the map reader's 40-head pass, with a few zero-weight
+    heads (skipped as in the reference) so the nonzero count is 34 per layer."""
+    rng = np.random.default_rng(4040)
+    cfg = ch.EsmConfig(640, 1280, 2, 40)
+    w = ch.EsmWeights.random(cfg, seed=4040, bias_std=0.02).quantize_q8()
+    cw = rng.standard_normal(cfg.n_layers * 40).astype(np.float32)
+    cw[::7] = 0.0
+    seqs = [rand_tokens(rng, n) for n in (97, 40, 130)]
+    check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(0.1)))
+
+
 @pytest.mark.parametrize("hd,H", [(16, 4), (24, 4), (32, 2), (64, 2)])
 def test_forward_fp32_attention_kernel(hd, H, monkeypatch):
     """The FP32-MFMA attention kernel (CIH_ATT=fp32), kept for A/B runs, on
