@@ -25,6 +25,7 @@ import numpy as np
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "codon-infer_amd"))
+from codon_hip.devmem import Hip  # noqa: E402
 
 METRIC = "residues/sec ESM-2 650M Q8_0 B=16 L=512; HBM GB/s & MFMA util vs peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense FP32 matrix peak
@@ -36,36 +37,6 @@ PEAK_F16_MFMA_TFLOPS = 2500.0   # MI355X dense f16 matrix peak
 # The default quantized GEMM issues 2 f16 MFMA MACs per algorithmic MAC
 # (activation split into two f16 limbs); CIH_LIMBS=bf16x3 issues 3 bf16 MACs,
 # CIH_QGEMM=fp32 selects the FP32-MFMA kernel (1 MAC per MAC).
-
-
-class Hip:
-    """Minimal device-memory plumbing through libamdhip64 (no torch)."""
-
-    def __init__(self):
-        self.L = ctypes.CDLL("libamdhip64.so")
-        self.L.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
-        self.L.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-        self.L.hipFree.argtypes = [ctypes.c_void_p]
-
-    def malloc(self, n):
-        p = ctypes.c_void_p()
-        if self.L.hipMalloc(ctypes.byref(p), n) != 0:
-            raise RuntimeError("hipMalloc failed")
-        return p.value
-
-    def h2d(self, dst, arr):
-        if self.L.hipMemcpy(ctypes.c_void_p(dst), arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes, 1) != 0:
-            raise RuntimeError("hipMemcpy H2D failed")
-
-    def d2h(self, arr, src):
-        if self.L.hipMemcpy(arr.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(src), arr.nbytes, 2) != 0:
-            raise RuntimeError("hipMemcpy D2H failed")
-
-    def sync(self):
-        self.L.hipDeviceSynchronize()
-
-    def free(self, p):
-        self.L.hipFree(ctypes.c_void_p(p))
 
 
 def qgemm_name(wname, T, d):

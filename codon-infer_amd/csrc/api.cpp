@@ -32,6 +32,25 @@ int set_error(int code, const char *fmt, ...) {
 #include "model.h"
 
 namespace cih {
+static thread_local bool g_full_range = false;
+bool full_range_mode() { return g_full_range; }
+void set_full_range_mode(bool on) { g_full_range = on; }
+
+std::string kernel_switches() {
+    static const char *const names[] = {"CIH_ATT",     "CIH_ATT_QB", "CIH_ATT_SPLIT", "CIH_SPLITK",
+                                        "CIH_QGEMM",   "CIH_ACT",    "CIH_LIMBS",     "CIH_GEMV",
+                                        "CIH_GEMV_NB", "CIH_GEMM_LDS", "CIH_GEMM_TILE", "CIH_GEMM_TILE_N"};
+    std::string s = g_full_range ? "R|" : "|";
+    for (const char *n : names) {
+        const char *v = getenv(n);
+        s += v ? v : "";
+        s += '|';
+    }
+    return s;
+}
+}  // namespace cih
+
+namespace cih {
 
 void free_list(std::vector<void *> &l) {
     for (void *p : l) hipFree(p);
@@ -242,8 +261,9 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
     }
     if (good) {
         void *hp = nullptr;
-        if (!ok(hipHostMalloc(&hp, 2 * B * sizeof(int)))) good = false;
+        if (!ok(hipHostMalloc(&hp, (2 * B + 1) * sizeof(int)))) good = false;
         else { ws.host.push_back(hp); ws.h_meta = (int *)hp; }
+        good = good && ok(dalloc(ws.flag, 1, dl));
     }
     if (!good) {
         free_workspace(ws);
@@ -329,22 +349,24 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         const bool fp32_gemm = qpath && !std::strcmp(qpath, "fp32");
         const bool bf16 = lpath && !std::strcmp(lpath, "bf16x3");
         if (m->dtype != DT_FP32 && !fp32_gemm && T > GEMV_MAX_M) {
-            if (apath && !std::strcmp(apath, "x3")) af = AF_X3;
+            if ((apath && !std::strcmp(apath, "x3")) || full_range_mode()) af = AF_X3;
             else if (!(apath && !std::strcmp(apath, "f32")) && !bf16) af = AF_H2;
         }
     }
     const int epi_fc1 = af == AF_X3 ? EPI_GELU_X3 : (af == AF_H2 ? EPI_GELU_H2 : EPI_GELU);
 
     m->prof.used = 0;
-    // the contact accumulator is cleared outside the (possibly captured) kernel sequence
+    // the contact accumulator and the status word are cleared outside the
+    // (possibly captured) kernel sequence
     if (want_contacts) HIPCHK(hipMemsetAsync(ws.M, 0, (size_t)B * n_max * n_max * 4, st));
+    HIPCHK(hipMemsetAsync(ws.flag, 0, sizeof(int), st));
 
     // Everything from the embedding to the output scatters is kernel
     // launches only; a shape seen before replays a captured graph of it.
     auto enqueue = [&]() -> int {
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-        HIPCHK(launch_embed(ws.tokens, sm, m->emb.fmt, m->emb.q, m->emb.sc, d, V, ws.x, st));
+        HIPCHK(launch_embed(ws.tokens, sm, m->emb.fmt, m->emb.q, m->emb.sc, d, V, ws.x, st, ws.flag));
     }
 
     for (int l = 0; l < L; l++) {
@@ -394,10 +416,12 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         ProfScope ps(m, CIH_KC_OTHER, 0, 0);
         HIPCHK(launch_apc_finalize(ws.M, ws.r, ws.coef, m->d_contact_w, L * H, sm, m->contact_b, t_contacts, n_max, st));
     }
-    // final LayerNorm: state.x = LN_f(x) (lib.rs:5379-5387)
+    // final LayerNorm: state.x = LN_f(x) (lib.rs:5379-5387).  It also
+    // reports a residual row that is no longer finite: the f16 limbs hold
+    // |x| < 65504 only, and an overflow there makes the residual non-finite.
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-        HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, AF_F32, T, d, st));
+        HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, AF_F32, T, d, st, ws.flag));
     }
     if (want_hidden) HIPCHK(launch_scatter_rows(ws.ao, d, sm, t_hidden, (int64_t)S_max * d, st));
     if (want_logits || keep_logits) {
@@ -421,7 +445,7 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         // the shape fixes every grid and pointer of the sequence: batch,
         // padded length, token count, outputs and their destinations
         const FwdGraphKey key{B, S_max, T, flags | (keep_logits ? 1u << 31 : 0u),
-                              {t_logits, t_hidden, t_final, t_contacts, t_attn, t_layer}};
+                              {t_logits, t_hidden, t_final, t_contacts, t_attn, t_layer}, kernel_switches()};
         hipGraphExec_t ex = nullptr;
         for (auto &g : ws.graphs)
             if (g.first == key) ex = g.second;
@@ -442,7 +466,18 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         }
         HIPCHK(hipGraphLaunch(ex, st));
     }
+    int *h_flag = ws.h_meta + 2 * ws.maxB;
+    HIPCHK(hipMemcpyAsync(h_flag, ws.flag, sizeof(int), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
+    if (*h_flag & FLAG_BAD_TOKEN) {
+        m->prof.used = 0;
+        return set_error(CIH_ERR_TOKEN, "a token id outside [0, %d) in the device token buffer", V);
+    }
+    // Non-finite residual: run the forward again in full-range mode (three
+    // bf16 limbs, FP32-MFMA attention), whose results then stand, finite or
+    // not, as the reference's would.
+    if ((*h_flag & FLAG_NONFINITE) && !full_range_mode())
+        return in_full_range([&] { return forward_impl(m, tokens, lens, B, S_max, flags, out, keep_logits); });
 
     if (!dev_io) {
         auto rows_out = [&](float *dst, const float *src, int width, int64_t bstride) -> int {

@@ -767,7 +767,7 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
     const char *e = getenv("CIH_ATT");
-    const bool fp32 = e && !strcmp(e, "fp32");
+    const bool fp32 = (e && !strcmp(e, "fp32")) || full_range_mode();
     // f16-limb kernel: 256 queries per workgroup (8 waves) halve the K/V tile
     // staging per query when that still leaves two workgroups per CU, else 128
     // (more workgroups for short batches).  CIH_ATT_QB=128|256 forces one.

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstring>
 #include <map>
+#include <tuple>
 
 #include "model.h"
 
@@ -22,11 +23,13 @@ struct cih_decoder {
     float *rope_c = nullptr, *rope_s = nullptr;
     float *x = nullptr, *xb = nullptr, *qkv = nullptr, *ao = nullptr, *h = nullptr, *logits = nullptr;
     int *d_tokens = nullptr, *d_rows = nullptr, *d_cu = nullptr, *d_lens = nullptr;
-    int *h_meta = nullptr;  // pinned: tokens[max_rows] | rows[max_rows][2]
+    int *h_meta = nullptr;  // pinned: tokens[max_rows] | rows[max_rows][2] | status word read back
+    int *d_flag = nullptr;  // device status word of a step (FLAG_* bits)
     cih::PartialBuf part;
     std::vector<int> filled;  // positions written per slot (0..filled-1 valid)
     bool unique = false;      // staged rows: every slot at most once
-    std::map<std::pair<int, bool>, hipGraphExec_t> graphs;  // (rows, fused) -> captured step
+    // (rows, fused, kernel switches) -> captured step
+    std::map<std::tuple<int, bool, std::string>, hipGraphExec_t> graphs;
     std::vector<void *> allocs;
 };
 
@@ -103,8 +106,11 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
         HIPCHK(model_gemm(m, dc->part, ly.w2, dc->h, F, AF_F32, ly.b2, dc->x, d, n, EPI_RESIDUAL));
     }
     {
+        // more rows than the GEMV takes go through GEMMs on f16 limbs: the
+        // final LayerNorm reports a residual that overflowed them
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
-        HIPCHK(launch_layernorm(dc->x, m->lnfw, m->lnfb, dc->ao, AF_F32, n, d, st));
+        HIPCHK(launch_layernorm(dc->x, m->lnfw, m->lnfb, dc->ao, AF_F32, n, d, st,
+                                n > GEMV_MAX_M && !full_range_mode() ? dc->d_flag : nullptr));
     }
     // project_lm_head_* (lib.rs:3952-4015): dense + GELU, LN, decoder; or the
     // tied embedding without bias
@@ -135,8 +141,20 @@ int run_rows(cih_decoder *dc, int n) {
     const bool fused = dc->unique;
     HIPCHK(hipMemcpyAsync(dc->d_tokens, dc->h_meta, (size_t)n * 4, hipMemcpyHostToDevice, st));
     HIPCHK(hipMemcpyAsync(dc->d_rows, dc->h_meta + dc->max_rows, (size_t)n * 8, hipMemcpyHostToDevice, st));
-    if (!use_graph(dc, n)) return enqueue_rows(dc, n, fused);
-    auto key = std::make_pair(n, fused);
+    if (!use_graph(dc, n)) {
+        if (n <= GEMV_MAX_M) return enqueue_rows(dc, n, fused);
+        // rows through the f16-limb GEMMs: a non-finite residual (an
+        // overflowed limb) runs the rows again in full-range mode, rewriting
+        // the same cache positions
+        int *h_flag = dc->h_meta + 3 * dc->max_rows;
+        HIPCHK(hipMemsetAsync(dc->d_flag, 0, sizeof(int), st));
+        if (int rc = enqueue_rows(dc, n, fused)) return rc;
+        HIPCHK(hipMemcpyAsync(h_flag, dc->d_flag, sizeof(int), hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        if (*h_flag & FLAG_NONFINITE) return in_full_range([&] { return enqueue_rows(dc, n, fused); });
+        return 0;
+    }
+    auto key = std::make_tuple(n, fused, kernel_switches());
     auto it = dc->graphs.find(key);
     if (it == dc->graphs.end()) {
         hipGraph_t g = nullptr;
@@ -261,10 +279,11 @@ int cih_decoder_create(cih_model *m, int32_t n_slots, int32_t max_len, int32_t m
                 dalloc(dc->qkv, R * 3 * d, al) == hipSuccess && dalloc(dc->ao, R * d, al) == hipSuccess &&
                 dalloc(dc->h, R * std::max(F, d), al) == hipSuccess && dalloc(dc->logits, R * V, al) == hipSuccess &&
                 dalloc(dc->d_tokens, R, al) == hipSuccess && dalloc(dc->d_rows, 2 * R, al) == hipSuccess &&
-                dalloc(dc->d_cu, R, al) == hipSuccess && dalloc(dc->d_lens, R, al) == hipSuccess;
+                dalloc(dc->d_cu, R, al) == hipSuccess && dalloc(dc->d_lens, R, al) == hipSuccess &&
+                dalloc(dc->d_flag, 1, al) == hipSuccess;
     dc->part.floats = model_part_floats(m);
     good = good && dalloc(dc->part.part, dc->part.floats, al) == hipSuccess &&
-           hipHostMalloc((void **)&dc->h_meta, 3 * R * sizeof(int)) == hipSuccess;
+           hipHostMalloc((void **)&dc->h_meta, (3 * R + 1) * sizeof(int)) == hipSuccess;
     if (!good) {
         destroy(dc);
         return set_error(CIH_ERR_HIP, "decoder allocation failed (%zu MiB of KV cache)", 2 * cache * 4 >> 20);

@@ -527,7 +527,7 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     if (gemm_lds_applies(W, a_fmt, M, epi)) return launch_gemm_lds(W, X, bias, Y, ldy, M, epi, st);
     // FP32 activations: f16 two-limb split unless CIH_LIMBS=bf16x3
     const char *lv = getenv("CIH_LIMBS");
-    const bool bf16 = lv && !strcmp(lv, "bf16x3");
+    const bool bf16 = (lv && !strcmp(lv, "bf16x3")) || full_range_mode();
     if (a_fmt == AF_H2) {
         if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
         if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);

@@ -146,13 +146,28 @@ struct SeqMeta {
     int B, S_max;
 };
 
-// Embedding + token-dropout rescale, packed rows.
-hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *emb_q,
-                        const float *emb_sc, int d, int V, float *x, hipStream_t st);
+// Bits of a forward's device status word (one int, cleared before the
+// forward, read after it).
+constexpr int FLAG_BAD_TOKEN = 1;  // a token id outside [0, V) (device-pointer input)
+constexpr int FLAG_NONFINITE = 2;  // a LayerNorm row with a non-finite mean or variance
 
-// out = LayerNorm(x) over rows of width d (eps 1e-5); out_fmt AF_F32 or AF_X3
+// Full-range mode: quantized GEMMs take three bf16 limbs and attention the
+// FP32-MFMA kernel, which cover the whole FP32 exponent range (the f16 limbs
+// of the default path need |x| < 65504).  A forward whose residual stream
+// turned non-finite is run again in it.  Thread-local; set by the host
+// around that one forward.
+bool full_range_mode();
+
+// Embedding + token-dropout rescale, packed rows.  flag (may be null):
+// FLAG_BAD_TOKEN is set for an id outside [0, V), which is clamped.
+hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *emb_q,
+                        const float *emb_sc, int d, int V, float *x, hipStream_t st, int *flag = nullptr);
+
+// out = LayerNorm(x) over rows of width d (eps 1e-5); out_fmt AF_F32, AF_X3
+// or AF_H2.  flag (may be null): FLAG_NONFINITE is set when a row's mean or
+// variance is not finite (the row holds an inf or NaN).
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, void *out, int out_fmt, int rows,
-                            int d, hipStream_t st);
+                            int d, hipStream_t st, int *flag = nullptr);
 
 // Bidirectional rotary attention over packed Q|K|V rows.  When P != nullptr
 // every softmax row is stored at P[b*pb + h*ph + q*S_max + k]; rowsum (with

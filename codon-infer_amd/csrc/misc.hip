@@ -19,7 +19,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 __global__ __launch_bounds__(256) void k_embed(const int *__restrict__ tokens, const int *__restrict__ cu,
                                                const int *__restrict__ lens, int S_max, int fmt,
                                                const void *__restrict__ eq, const float *__restrict__ esc, int d,
-                                               int V, float *__restrict__ x) {
+                                               int V, float *__restrict__ x, int *__restrict__ flag) {
     const int s = blockIdx.x, b = blockIdx.y;
     const int len = lens[b];
     if (s >= len) return;
@@ -35,8 +35,11 @@ __global__ __launch_bounds__(256) void k_embed(const int *__restrict__ tokens, c
     const float ratio = (float)mask_count / (float)len;
     const float scale = ratio >= 1.0f ? 0.0f : (1.0f - 0.12f) / (1.0f - ratio);
     // ids outside [0, V) cannot occur on host-pointer calls (validated
-    // there); device-pointer calls are clamped so no read leaves the table.
-    const int t = min(max(tk[s], 0), V - 1);
+    // there); on device-pointer calls such an id sets FLAG_BAD_TOKEN, which
+    // the host turns into CIH_ERR_TOKEN, and is clamped so that no read
+    // leaves the table.
+    const int t0 = tk[s], t = min(max(t0, 0), V - 1);
+    if (t0 != t && flag && threadIdx.x == 0) atomicOr(flag, FLAG_BAD_TOKEN);
     float *xr = x + (size_t)(cu[b] + s) * d;
     for (int i = threadIdx.x; i < d; i += 256) {
         float v = 0.0f;
@@ -54,9 +57,9 @@ __global__ __launch_bounds__(256) void k_embed(const int *__restrict__ tokens, c
 }
 
 hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *emb_q, const float *emb_sc, int d,
-                        int V, float *x, hipStream_t st) {
+                        int V, float *x, hipStream_t st, int *flag) {
     hipLaunchKernelGGL(k_embed, dim3(sm.S_max, sm.B), dim3(256), 0, st, tokens, sm.cu, sm.lens, sm.S_max, emb_fmt,
-                       emb_q, emb_sc, d, V, x);
+                       emb_q, emb_sc, d, V, x, flag);
     return hipGetLastError();
 }
 
@@ -65,7 +68,7 @@ hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *
 template <int PER, int OF>
 __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, const float *__restrict__ w,
                                                    const float *__restrict__ b, void *__restrict__ out, int rows,
-                                                   int d) {
+                                                   int d, int *__restrict__ flag) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
@@ -92,6 +95,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
     }
     const float var = wave_sum(q) / (float)d;
     const float inv = 1.0f / sqrtf(var + 1e-5f);
+    if (flag && lane == 0 && !(__builtin_isfinite(mean) && __builtin_isfinite(var))) atomicOr(flag, FLAG_NONFINITE);
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int c = lane + 64 * i;
@@ -113,7 +117,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <int PER, int OF>
 __global__ __launch_bounds__(256) void k_layernorm4(const float *__restrict__ x, const float *__restrict__ w,
                                                     const float *__restrict__ b, void *__restrict__ out, int rows,
-                                                    int d) {
+                                                    int d, int *__restrict__ flag) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
@@ -141,6 +145,7 @@ __global__ __launch_bounds__(256) void k_layernorm4(const float *__restrict__ x,
     }
     const float var = wave_sum(q) / (float)d;
     const float inv = 1.0f / sqrtf(var + 1e-5f);
+    if (flag && lane == 0 && !(__builtin_isfinite(mean) && __builtin_isfinite(var))) atomicOr(flag, FLAG_NONFINITE);
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int c = lane + 64 * i;
@@ -161,31 +166,31 @@ __global__ __launch_bounds__(256) void k_layernorm4(const float *__restrict__ x,
 
 template <int OF>
 static hipError_t launch_ln_t(const float *x, const float *w, const float *b, void *out, int rows, int d,
-                              hipStream_t st) {
+                              int *flag, hipStream_t st) {
     const dim3 grid((rows + 3) / 4), blk(256);
     if (d % 4 == 0) {
         const int per4 = (d / 4 + 63) / 64;
-        if (per4 <= 2) hipLaunchKernelGGL((k_layernorm4<2, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
-        else if (per4 <= 5) hipLaunchKernelGGL((k_layernorm4<5, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
-        else if (per4 <= 10) hipLaunchKernelGGL((k_layernorm4<10, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+        if (per4 <= 2) hipLaunchKernelGGL((k_layernorm4<2, OF>), grid, blk, 0, st, x, w, b, out, rows, d, flag);
+        else if (per4 <= 5) hipLaunchKernelGGL((k_layernorm4<5, OF>), grid, blk, 0, st, x, w, b, out, rows, d, flag);
+        else if (per4 <= 10) hipLaunchKernelGGL((k_layernorm4<10, OF>), grid, blk, 0, st, x, w, b, out, rows, d, flag);
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }
     const int per = (d + 63) / 64;
-    if (per <= 5) hipLaunchKernelGGL((k_layernorm<5, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
-    else if (per <= 10) hipLaunchKernelGGL((k_layernorm<10, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
-    else if (per <= 20) hipLaunchKernelGGL((k_layernorm<20, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
-    else if (per <= 40) hipLaunchKernelGGL((k_layernorm<40, OF>), grid, blk, 0, st, x, w, b, out, rows, d);
+    if (per <= 5) hipLaunchKernelGGL((k_layernorm<5, OF>), grid, blk, 0, st, x, w, b, out, rows, d, flag);
+    else if (per <= 10) hipLaunchKernelGGL((k_layernorm<10, OF>), grid, blk, 0, st, x, w, b, out, rows, d, flag);
+    else if (per <= 20) hipLaunchKernelGGL((k_layernorm<20, OF>), grid, blk, 0, st, x, w, b, out, rows, d, flag);
+    else if (per <= 40) hipLaunchKernelGGL((k_layernorm<40, OF>), grid, blk, 0, st, x, w, b, out, rows, d, flag);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, void *out, int out_fmt, int rows, int d,
-                            hipStream_t st) {
+                            hipStream_t st, int *flag) {
     if (rows <= 0) return hipSuccess;
-    if (out_fmt == AF_X3) return d % 32 ? hipErrorInvalidValue : launch_ln_t<AF_X3>(x, w, b, out, rows, d, st);
-    if (out_fmt == AF_H2) return d % 32 ? hipErrorInvalidValue : launch_ln_t<AF_H2>(x, w, b, out, rows, d, st);
-    return launch_ln_t<AF_F32>(x, w, b, out, rows, d, st);
+    if (out_fmt == AF_X3) return d % 32 ? hipErrorInvalidValue : launch_ln_t<AF_X3>(x, w, b, out, rows, d, flag, st);
+    if (out_fmt == AF_H2) return d % 32 ? hipErrorInvalidValue : launch_ln_t<AF_H2>(x, w, b, out, rows, d, flag, st);
+    return launch_ln_t<AF_F32>(x, w, b, out, rows, d, flag, st);
 }
 
 // final_layer_att (lib.rs:5201-5204, 5256-5261): acc = 0; acc += P_h * (1/H)

@@ -23,13 +23,15 @@ struct Layer {
     float *ln1w = nullptr, *ln1b = nullptr, *ln2w = nullptr, *ln2b = nullptr;
 };
 
-// What fixes a forward's kernel sequence: grids and pointers.
+// What fixes a forward's kernel sequence: grids, pointers, and the kernel
+// switches read while it is enqueued (kernel_switches()).
 struct FwdGraphKey {
     int B = 0, S_max = 0, T = 0;
     uint32_t flags = 0;
     const void *out[6] = {};
+    std::string sw;
     bool operator==(const FwdGraphKey &o) const {
-        if (B != o.B || S_max != o.S_max || T != o.T || flags != o.flags) return false;
+        if (B != o.B || S_max != o.S_max || T != o.T || flags != o.flags || sw != o.sw) return false;
         for (int i = 0; i < 6; i++)
             if (out[i] != o.out[i]) return false;
         return true;
@@ -40,7 +42,8 @@ struct Workspace {
     int maxB = 0, maxS = 0;
     uint32_t flags = 0;
     int *tokens = nullptr, *cu = nullptr, *lens = nullptr;
-    int *h_meta = nullptr;  // pinned: cu[maxB] | lens[maxB]
+    int *h_meta = nullptr;  // pinned: cu[maxB] | lens[maxB] | status word read back
+    int *flag = nullptr;    // device status word of the forward (FLAG_* bits)
     float *x = nullptr, *xb = nullptr, *qkv = nullptr, *ao = nullptr, *hbuf = nullptr, *logits = nullptr;
     float *rope_c = nullptr, *rope_s = nullptr;
     float *P = nullptr;                            // [maxB][H][maxS][maxS] probabilities scratch
@@ -143,6 +146,22 @@ struct ProfScope {
 
 void free_list(std::vector<void *> &l);
 int check_config(const cih_config *c);
+
+// The values of the environment switches that choose kernels while a
+// forward or decode step is enqueued, plus full-range mode: part of the key
+// of a captured graph, so that a change of switch is never hidden by the
+// replay of a graph captured under other settings.
+std::string kernel_switches();
+
+// Runs fn() with full-range mode on for this thread (full_range_mode()).
+void set_full_range_mode(bool on);
+template <class F>
+int in_full_range(F fn) {
+    set_full_range_mode(true);
+    const int rc = fn();
+    set_full_range_mode(false);
+    return rc;
+}
 
 // algorithmic bytes of a weight matrix
 double wbytes(const DevMatrix &W);

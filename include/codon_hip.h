@@ -138,7 +138,16 @@ int cih_model_destroy(cih_model *m);
  * _q4_ext (5790, 5800) for a batch of B independent sequences.
  * tokens: [B][S_max] int32 ids (padding ignored), lens: [B] host array with
  * 1 <= lens[b] <= S_max.  B=1, lens[0]=S equals one reference call on
- * tokens[0..S].  Synchronous: outputs are complete on return. */
+ * tokens[0..S].  Synchronous: outputs are complete on return.
+ * Token ids outside [0, vocab) return CIH_ERR_TOKEN: checked on the host, or
+ * with CIH_IO_DEVICE on the device during the forward (the outputs are then
+ * undefined).
+ * Range: the default kernels hand activations to the quantized GEMMs and to
+ * attention as two f16 limbs, which hold |x| < 65504 only.  A forward whose
+ * residual stream turns non-finite is run once more with the full-range
+ * kernels (three bf16 limbs, FP32-MFMA attention, the whole FP32 exponent
+ * range), and those results are returned: outputs are finite wherever the
+ * reference's are. */
 int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B,
                 int32_t S_max, uint32_t flags, const cih_outputs *out);
 

@@ -9,8 +9,9 @@
  * contracts a*b+c, and glibc's expf/sqrtf/powf/cosf/sinf are the same calls
  * Rust's f32 methods make on Linux, so the scalar parts reproduce the
  * reference's arithmetic operation for operation.  The GEMM micro-kernel is
- * the AVX2+FMA path of dot_row_batch_m4 and the attention dot/axpy are the
- * 256-bit AVX paths (the code the reference dispatches to on an AVX2 host).
+ * the AVX2+FMA path of dot_row_batch_m4; the attention dot/axpy are the
+ * 256-bit AVX paths, or at head_dim 64 on a host with AVX-512F the 512-bit
+ * ones, as the reference dispatches at run time.
  */
 #define _GNU_SOURCE
 #include "cpu_ref.h"
@@ -488,6 +489,50 @@ static void axpy_head(float *out, const float *v, float p, int hd) {
     for (int i = 0; i < hd; i++) out[i] += p * v[i];
 }
 
+/* dot_product_head_avx512_d64 / accumulate_value_head_avx512_d64
+ * (lib.rs:3398-3434): what the reference runs at head_dim 64 when the host
+ * has AVX-512F (lib.rs:5113, 5457, 5816, 3452).  Dot: 16-wide products of
+ * q[0..16) * k[0..16), then three fused multiply-adds of the next 16-wide
+ * slices into the same accumulator, then _mm512_reduce_add_ps, whose order is
+ * the halving tree (lanes i + i+8, then i + i+4, i + i+2, then 0 + 1).  Axpy:
+ * one fused multiply-add per element, out = fma(p, v, out). */
+__attribute__((target("avx512f")))
+static float dot_head_d64_avx512(const float *q, const float *k) {
+    __m512 acc = _mm512_mul_ps(_mm512_loadu_ps(q), _mm512_loadu_ps(k));
+    acc = _mm512_fmadd_ps(_mm512_loadu_ps(q + 16), _mm512_loadu_ps(k + 16), acc);
+    acc = _mm512_fmadd_ps(_mm512_loadu_ps(q + 32), _mm512_loadu_ps(k + 32), acc);
+    acc = _mm512_fmadd_ps(_mm512_loadu_ps(q + 48), _mm512_loadu_ps(k + 48), acc);
+    float a[16], b[8], c[4], e[2];
+    _mm512_storeu_ps(a, acc);
+    for (int i = 0; i < 8; i++) b[i] = a[i] + a[i + 8];
+    for (int i = 0; i < 4; i++) c[i] = b[i] + b[i + 4];
+    for (int i = 0; i < 2; i++) e[i] = c[i] + c[i + 2];
+    return e[0] + e[1];
+}
+
+__attribute__((target("avx512f")))
+static void axpy_head_d64_avx512(float *out, const float *v, float p) {
+    const __m512 pv = _mm512_set1_ps(p);
+    for (int i = 0; i < 64; i += 16)
+        _mm512_storeu_ps(out + i, _mm512_fmadd_ps(pv, _mm512_loadu_ps(v + i), _mm512_loadu_ps(out + i)));
+}
+
+/* is_x86_feature_detected!("avx512f") at head_dim 64, as the reference
+ * decides per forward; cr_set_attention_isa(1) forces the 256-bit path. */
+static int g_force_avx = 0;
+void cr_set_attention_isa(int32_t avx_only) { g_force_avx = avx_only != 0; }
+int32_t cr_attention_uses_avx512(int32_t hd) {
+    return hd == 64 && !g_force_avx && __builtin_cpu_supports("avx512f");
+}
+
+static inline float dot_head_dispatch(int avx512, const float *q, const float *k, int hd) {
+    return avx512 ? dot_head_d64_avx512(q, k) : dot_head(q, k, hd);
+}
+static inline void axpy_head_dispatch(int avx512, float *out, const float *v, float p, int hd) {
+    if (avx512) axpy_head_d64_avx512(out, v, p);
+    else axpy_head(out, v, p, hd);
+}
+
 /* ------------------------------------------------------------------------ */
 /* The bidirectional forward: forward_bidirectional_parallel_ext (FP32,       */
 /* lib.rs:5097-5440), forward_bidirectional_q8 (5442-5788),                  */
@@ -518,6 +563,7 @@ int32_t cr_forward(const cr_config *cfg, const cr_weights *w, const int32_t *tok
     if (do_contacts && n_res > 1024) return -4; /* row_sums: [f32; 1024], lib.rs:5046 */
     if (do_contacts && !o->contact_w) return -1;
     const float inv_scale = 1.0f / sqrtf((float)hd);
+    const int avx512 = cr_attention_uses_avx512(hd);
 
     float *x = calloc((size_t)S * d, 4), *xb = calloc((size_t)S * d, 4);
     float *q = calloc((size_t)S * d, 4), *k = calloc((size_t)S * d, 4), *v = calloc((size_t)S * d, 4);
@@ -562,7 +608,8 @@ int32_t cr_forward(const cr_config *cfg, const cr_weights *w, const int32_t *tok
         for (int h = 0; h < H; h++) {
             for (int p = 0; p < S; p++) {
                 const float *qh = q + (int64_t)p * d + h * hd;
-                for (int t = 0; t < S; t++) att[t] = dot_head(qh, k + (int64_t)t * d + h * hd, hd) * inv_scale;
+                for (int t = 0; t < S; t++)
+                    att[t] = dot_head_dispatch(avx512, qh, k + (int64_t)t * d + h * hd, hd) * inv_scale;
                 cr_softmax(att, S);
                 if (do_contacts) memcpy(head_att + (int64_t)p * S, att, sizeof(float) * S);
                 if (o->attn) memcpy(o->attn + (((int64_t)l * H + h) * S + p) * S, att, sizeof(float) * S);
@@ -572,7 +619,7 @@ int32_t cr_forward(const cr_config *cfg, const cr_weights *w, const int32_t *tok
                 }
                 float *out = oa + (int64_t)p * d + h * hd;
                 memset(out, 0, sizeof(float) * hd);
-                for (int t = 0; t < S; t++) axpy_head(out, v + (int64_t)t * d + h * hd, att[t], hd);
+                for (int t = 0; t < S; t++) axpy_head_dispatch(avx512, out, v + (int64_t)t * d + h * hd, att[t], hd);
             }
             if (do_contacts)
                 cr_accumulate_head_apc(head_att, cl, S, n_res, o->contact_w[l * H + h]);
@@ -783,14 +830,17 @@ int32_t cr_forward_step(const cr_config *cfg, const cr_weights *w, int32_t token
         float *kc = s->key_cache + (int64_t)l * s->max_len * d, *vc = s->value_cache + (int64_t)l * s->max_len * d;
         memcpy(kc + (int64_t)pos * d, k, sizeof(float) * d);
         memcpy(vc + (int64_t)pos * d, v, sizeof(float) * d);
-        /* attention_head_avx1, lib.rs:3438-3483 (256-bit path) */
+        /* attention_head_avx1, lib.rs:3438-3483 (AVX-512 at head_dim 64 when
+         * the host has it, else the 256-bit path) */
+        const int avx512 = cr_attention_uses_avx512(hd);
         for (int h = 0; h < H; h++) {
             const float *qh = q + h * hd;
-            for (int t = 0; t <= pos; t++) att[t] = dot_head(qh, kc + (int64_t)t * d + h * hd, hd) * inv_scale;
+            for (int t = 0; t <= pos; t++)
+                att[t] = dot_head_dispatch(avx512, qh, kc + (int64_t)t * d + h * hd, hd) * inv_scale;
             cr_softmax(att, pos + 1);
             float *o = xb2 + h * hd;
             memset(o, 0, sizeof(float) * hd);
-            for (int t = 0; t <= pos; t++) axpy_head(o, vc + (int64_t)t * d + h * hd, att[t], hd);
+            for (int t = 0; t <= pos; t++) axpy_head_dispatch(avx512, o, vc + (int64_t)t * d + h * hd, att[t], hd);
         }
         cr_matmul_vec(dt, xb, xb2, mat_at(w->wo, dt, l, d, d), w->bo + (int64_t)l * d, d, d, nt);
         for (int i = 0; i < d; i++) x[i] += xb[i];

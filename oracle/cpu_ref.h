@@ -89,6 +89,12 @@ void cr_matmul_tiled(int32_t wdtype, float *out, const float *x, const void *w,
                      int32_t seq_len, int32_t num_threads);
 
 /* one sequence, one forward.  Returns 0 or a negative error code. */
+/* Attention micro-kernel choice: at head_dim 64 on an AVX-512F host the
+ * reference uses its 512-bit dot/axpy (lib.rs:3398-3434), else the 256-bit
+ * ones.  cr_set_attention_isa(1) forces the 256-bit path (0: as the host). */
+void cr_set_attention_isa(int32_t avx_only);
+int32_t cr_attention_uses_avx512(int32_t head_dim);
+
 int32_t cr_forward(const cr_config *cfg, const cr_weights *w, const int32_t *tokens,
                    int32_t seq_len, int32_t num_threads, const cr_outputs *out);
 

@@ -113,6 +113,9 @@ def lib():
                                   ctypes.c_float, ctypes.c_int32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32,
                                   _i32p, ctypes.c_int32]
         L.cr_generate.restype = ctypes.c_int32
+        L.cr_set_attention_isa.argtypes = [ctypes.c_int32]
+        L.cr_attention_uses_avx512.argtypes = [ctypes.c_int32]
+        L.cr_attention_uses_avx512.restype = ctypes.c_int32
         for name in ("cr_cosine_similarity", "cr_rmse"):
             getattr(L, name).argtypes = [_f32p, _f32p, ctypes.c_int64]
             getattr(L, name).restype = ctypes.c_float
@@ -392,6 +395,16 @@ def generate(cfg, weights, prompt_tokens, temperature=0.0, max_new_tokens=None, 
     if n < 0:
         raise RuntimeError(f"cr_generate failed with code {n}")
     return out[:n].copy()
+
+
+def set_attention_isa(avx_only):
+    """Force the reference's 256-bit attention dot/axpy (True) or let head_dim
+    64 take its AVX-512F path when the host has it (False, the default)."""
+    lib().cr_set_attention_isa(1 if avx_only else 0)
+
+
+def attention_uses_avx512(head_dim):
+    return bool(lib().cr_attention_uses_avx512(head_dim))
 
 
 def forward(cfg, weights, tokens, num_threads=1, contacts=None, attn=False, layer_hidden=False,

@@ -83,8 +83,13 @@ def write_codq(path, cfg, w, arch_id):
 
 
 def _create_from_file(path, quantize_to=-1):
+    """Status of cih_model_create_from_file; a model it creates is destroyed."""
     h = ctypes.c_void_p()
-    return C.lib().cih_model_create_from_file(path.encode(), quantize_to, None, 0.0, ctypes.byref(h))
+    rc = C.lib().cih_model_create_from_file(path.encode(), quantize_to, None, 0.0, ctypes.byref(h))
+    if rc == 0:
+        assert h.value
+        assert C.lib().cih_model_destroy(h) == 0
+    return rc
 
 
 def test_file_reader_errors(tmp_path):
@@ -111,8 +116,10 @@ def test_file_reader_errors(tmp_path):
 
 
 def test_file_reader_accepts_valid_files(tmp_path, w8m_path):
-    """Valid inputs parse completely; without a GPU the first failure is the
-    device check (CIH_ERR_HIP), after every format check has passed."""
+    """Valid inputs parse completely: without a GPU the first failure is the
+    device check (CIH_ERR_HIP), after every format check has passed; with a
+    GPU (CIH_EXPECT_GPU=1) every load succeeds and its model is destroyed.
+    The loads' numbers are checked against the oracle in test_gpu_loader.py."""
     cfg = ch.EsmConfig.esm2_8m()
     w = ch.EsmWeights.from_grouped_canonical(w8m_path, cfg)
     q8 = str(tmp_path / "m.q8")
@@ -122,7 +129,6 @@ def test_file_reader_accepts_valid_files(tmp_path, w8m_path):
     on_gpu = os.environ.get("CIH_EXPECT_GPU") == "1"
     for path, qt in ((w8m_path, -1), (w8m_path, 1), (w8m_path, 2), (q8, -1), (q4, -1)):
         rc = _create_from_file(path, qt)
-        if not on_gpu:
-            assert rc == -5, (path, qt, C.lib().cih_last_error())
+        assert rc == (0 if on_gpu else -5), (path, qt, C.lib().cih_last_error())
     # a Q8 file cannot be requantized to Q4
     assert _create_from_file(q8, 2) == -1

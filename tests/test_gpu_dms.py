@@ -54,3 +54,39 @@ def test_dms_8m_peptide(w8m_path):
     rows, rate = ch.run_pipeline_dms(PEPTIDE, m, chunk=16)
     assert len(rows) == len(PEPTIDE) and rows[0].pos == 1 and rows[0].wt == PEPTIDE[0] and rate > 0
     m.close()
+
+
+def test_config4_650m_q8_dms_full_shape():
+    """Config 4 at its real shape: ESM-2 650M Q8_0, a seeded 400-residue
+    protein, masked marginal over all 400 positions in chunks of 32 (12
+    batched forwards of 32 masked copies of L = 402 and one of 16,
+    pipeline.rs:76-315).  The oracle scores positions 0, 31, 32 (either side
+    of the first chunk boundary), 200 and 399 (the last, in the short chunk);
+    every row has its wild-type column exactly 0, finite deltas and an
+    entropy in [0, ln 20]."""
+    rng = np.random.default_rng(400)
+    cfg = ch.EsmConfig.esm2_650m()
+    w = ch.EsmWeights.random(cfg, seed=4000, bias_std=0.02).quantize_q8()
+    res = (4 + rng.integers(0, 20, 400)).astype(np.int32)
+    m = ch.GpuModel(cfg, w, max_batch=32, max_len=402, outputs=ch.OUT_LOGITS)
+    print("650M Q8_0 DMS, 400 residues, chunks of 32", flush=True)
+    got_d, got_e = m.dms(res, 0, 0, ch.DMS_MASKED_MARGINAL, 32)
+    m.close()
+    canon = "ACDEFGHIKLMNPQRSTVWY"
+    aa = "LAGVSERTIDPKQNFYMHWC"  # token ids 4..23
+    wt_col = np.array([canon.index(aa[t - 4]) for t in res])
+    assert np.all(got_d[np.arange(400), wt_col] == 0.0)
+    assert np.isfinite(got_d).all()
+    assert np.all((got_e >= 0.0) & (got_e <= np.log(20.0) + 1e-5))
+    _, wins = cr.dms_windows(400, 0, cfg.max_seq_len)
+    for p in (0, 31, 32, 200, 399):
+        ws, we = wins[p]
+        toks = np.concatenate([[0], res[ws:we], [2]]).astype(np.int32)
+        tp = p - ws + 1
+        wt = int(toks[tp])
+        toks[tp] = 32
+        logits = cr.forward(cfg, w, toks, 16, final_att=False, hidden=False)["logits"]
+        rd, re_ = cr.dms_score(logits[tp], wt)
+        ed, ee = float(np.abs(got_d[p] - rd).max()), abs(float(got_e[p]) - re_)
+        print(f"position {p}: deltas {ed:.2e} entropy {ee:.2e}", flush=True)
+        assert ed <= TOL and ee <= TOL

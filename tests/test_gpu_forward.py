@@ -8,7 +8,10 @@ Tolerances (FP32 accumulate throughout):
   attention P   max |gpu - oracle| <= 1e-5
   final_att     max |gpu - oracle| <= 1e-5
   contacts      max |gpu - oracle| <= 1e-4
-  argmax        identical wherever the oracle's top-1/top-2 margin > 2e-3
+  argmax        identical wherever the oracle's top-1/top-2 margin exceeds
+                twice the measured max |logit error| of that sequence (where
+                the argmax provably cannot change); at least 90% of the
+                positions must be compared, and the count is printed
 """
 import numpy as np
 import pytest
@@ -34,7 +37,21 @@ def quantized(w, dtype):
     return w if dtype == 0 else (w.quantize_q8() if dtype == 1 else w.quantize_q4())
 
 
-def check_batch(cfg, w, seqs, flags, contact=None, nthreads=8, margin=2e-3):
+def check_argmax(got_logits, ref_logits, tag):
+    """Argmax over all 33 ids (ties to the last index, as compute_top1_match_rate,
+    lib.rs:2300-2315) identical wherever the oracle's top-1/top-2 gap exceeds
+    twice the observed max logit error: a perturbation of at most e per logit
+    cannot reorder two logits more than 2e apart."""
+    e = float(np.abs(got_logits.astype(np.float64) - ref_logits).max())
+    top2 = np.sort(ref_logits, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 2.0 * e
+    last = lambda a: a.shape[1] - 1 - a[:, ::-1].argmax(1)  # noqa: E731
+    print(f"argmax {tag}: {int(clear.sum())}/{clear.size} positions compared (margin {2 * e:.1e})", flush=True)
+    assert clear.mean() >= 0.9, (tag, int(clear.sum()), clear.size)
+    assert np.array_equal(last(got_logits)[clear], last(ref_logits)[clear]), tag
+
+
+def check_batch(cfg, w, seqs, flags, contact=None, nthreads=8):
     model = ch.GpuModel(cfg, w, contact_head=contact, max_batch=len(seqs), max_len=max(len(s) for s in seqs),
                         outputs=flags)
     got = model.forward(seqs, flags)
@@ -59,11 +76,7 @@ def check_batch(cfg, w, seqs, flags, contact=None, nthreads=8, margin=2e-3):
             e = float(np.abs(g.astype(np.float64) - r).max())
             worst[name] = max(worst.get(name, 0.0), e)
             assert e <= TOL[name], (name, b, S, e)
-        # argmax exact where the oracle's decision is not a near tie
-        lr = ref["logits"]
-        top2 = np.sort(lr, axis=1)[:, -2:]
-        clear = (top2[:, 1] - top2[:, 0]) > margin
-        assert np.array_equal(got["logits"][b, :S].argmax(1)[clear], lr.argmax(1)[clear]), b
+        check_argmax(got["logits"][b, :S], ref["logits"], f"seq {b} (S={S})")
     print("worst abs errors:", {k: f"{v:.2e}" for k, v in worst.items()}, flush=True)
     model.close()
     return got
@@ -205,9 +218,7 @@ def test_forward_headline_shape(monkeypatch):
         e = float(np.abs(got[name][0].astype(np.float64) - ref[name]).max())
         print(name, f"{e:.2e}", flush=True)
         assert e <= TOL[name], (name, e)
-    top2 = np.sort(ref["logits"], axis=1)[:, -2:]
-    clear = (top2[:, 1] - top2[:, 0]) > 2e-3
-    assert np.array_equal(got["logits"][0].argmax(1)[clear], ref["logits"].argmax(1)[clear])
+    check_argmax(got["logits"][0], ref["logits"], "650M Q8 headline seq 0")
     monkeypatch.setenv("CIH_SPLITK", "0")
     monkeypatch.setenv("CIH_FORWARD_GRAPH", "0")  # a replayed graph keeps the splits it was captured with
     unsplit = m.forward(seqs, flags)
@@ -355,3 +366,94 @@ def test_attention_key_split(case, monkeypatch):
         e = float(np.abs(res["1"][k][-1, :n].astype(np.float64) - ref[k]).max())
         print(case, k, f"{e:.2e}", flush=True)
         assert e <= TOL[k], (case, k, e)
+
+
+def test_device_io_token_validation():
+    """With CIH_IO_DEVICE the token ids are checked on the device: an id
+    outside [0, vocab) returns CIH_ERR_TOKEN (as the host path does) instead
+    of being computed with a clamped id; the next valid forward on the same
+    workspace (and the same captured graph) succeeds and matches the host
+    path."""
+    from codon_hip.devmem import Hip
+    rng = np.random.default_rng(90)
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=90, bias_std=0.02).quantize_q8()
+    S, B = 40, 2
+    flags = ch.OUT_LOGITS
+    m = ch.GpuModel(cfg, w, max_batch=B, max_len=S, outputs=flags | ch.IO_DEVICE)
+    hip = Hip()
+    d_tok, d_log = hip.malloc(B * S * 4), hip.malloc(B * S * cfg.vocab_size * 4)
+    seqs = [rand_tokens(rng, S - 2), rand_tokens(rng, 25)]
+    toks = np.zeros((B, S), np.int32)
+    for b, s in enumerate(seqs):
+        toks[b, :len(s)] = s
+    lens = [len(s) for s in seqs]
+    try:
+        for bad in (40, -1, 33):
+            t = toks.copy()
+            t[1, 7] = bad
+            hip.h2d(d_tok, t)
+            with pytest.raises(ch.CihError, match="TOKEN"):
+                m.forward_device(d_tok, lens, S, flags, {"logits": d_log})
+        hip.h2d(d_tok, toks)
+        for _ in range(2):
+            m.forward_device(d_tok, lens, S, flags, {"logits": d_log})
+            got = np.zeros((B, S, cfg.vocab_size), np.float32)
+            hip.d2h(got, d_log)
+            m2 = ch.GpuModel(cfg, w, max_batch=B, max_len=S, outputs=flags)
+            ref = m2.forward(seqs, flags)
+            m2.close()
+            for b in range(B):
+                assert np.array_equal(got[b, :lens[b]], ref["logits"][b, :lens[b]])
+    finally:
+        hip.free(d_tok)
+        hip.free(d_log)
+        m.close()
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_limb_overflow_runs_full_range(dtype):
+    """An activation the f16 limbs cannot hold: layer 0's LN1 output is
+    ~7e4 in one column (bias 7e4) whose Q, K and V weights are zero, so the
+    reference's result does not depend on it, while the f16 hi limb is inf
+    and inf * 0 = NaN in the MFMA.  The forward detects the non-finite
+    residual and runs again with the full-range kernels: results match the
+    oracle at the usual tolerances, with the default f16-limb hand-off and
+    with the FP32 one (CIH_ACT=f32, split inside the GEMM)."""
+    rng = np.random.default_rng(91 + dtype)
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=91, bias_std=0.02)
+    d, c = cfg.dim, 37
+    b1 = np.array(w.ln_1_bias, np.float32)
+    b1[c] = 7.0e4
+    w.ln_1_bias = b1
+    for name in ("wq", "wk", "wv"):
+        a = np.array(getattr(w, name), np.float32).reshape(cfg.n_layers, d, d)
+        a[0, :, c] = 0.0
+        setattr(w, name, a.ravel())
+    w = quantized(w, dtype)
+    seqs = [rand_tokens(rng, n) for n in (60, 33)]
+    check_batch(cfg, w, seqs, ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT)
+
+
+def test_graph_key_follows_kernel_switches(monkeypatch):
+    """A captured forward is keyed by the kernel switches read while it was
+    enqueued: with graphs on, CIH_ATT=fp32 after a default forward of the same
+    shape runs the FP32-MFMA attention (rounding differs), and unsetting it
+    replays the default graph bit for bit."""
+    rng = np.random.default_rng(92)
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=92, bias_std=0.02).quantize_q8()
+    seqs = [rand_tokens(rng, 70), rand_tokens(rng, 50)]
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN
+    monkeypatch.setenv("CIH_FORWARD_GRAPH", "1")
+    m = ch.GpuModel(cfg, w, max_batch=2, max_len=72, outputs=flags)
+    a = m.forward(seqs, flags)
+    monkeypatch.setenv("CIH_ATT", "fp32")
+    b = m.forward(seqs, flags)
+    monkeypatch.delenv("CIH_ATT")
+    c = m.forward(seqs, flags)
+    m.close()
+    diff = float(np.abs(a["hidden"] - b["hidden"]).max())
+    assert 0.0 < diff <= 1e-3, diff
+    assert np.array_equal(a["hidden"], c["hidden"]) and np.array_equal(a["logits"], c["logits"])

@@ -1,10 +1,16 @@
 """GPU model residency: weight files loaded straight to the device and FP32
 weights quantized there.
 
-* The device quantizer equals the host one (quantize_slice_to_q8 / _q4,
-  lib.rs:670-673, 1085-1088, itself pinned against the reference's
-  known-answer tests) byte for byte, including zero blocks, NaN, infinities,
-  exact .5 ties and equal-magnitude maxima of opposite sign.
+* The device quantizer equals the oracle's quantizers (quantize_slice_to_q8
+  / _q4, lib.rs:670-673, 1085-1088, pinned against the reference's
+  known-answer tests) and the host one byte for byte, including zero blocks,
+  NaN, infinities, subnormals, values near 1e37, exact .5 ties and
+  equal-magnitude maxima of opposite sign.
+* The shipped ESM-2 8M weights file (grouped_canonical_v1), loaded through
+  cih_model_create_from_file as FP32 and quantized to Q8_0 / Q4_0 on the
+  device, agrees with the oracle's forward of the same weights (logits
+  <= 1e-3, last-layer map <= 1e-5, contacts <= 1e-4) and reconstructs the
+  published 39/39 peptide (docs/benchmarks_v1.6.0.md:61-62).
 * A model loaded from a file (CODQ Q8_0 / Q4_0 / FP32, headerless
   grouped_canonical_v1, sequential_hf) produces bit-identical logits and
   hidden states to the same weights handed over as host tensors, and an FP32
@@ -17,6 +23,8 @@ import numpy as np
 import pytest
 
 import codon_hip as ch
+import cpu_ref as cr
+from conftest import PEPTIDE, decode
 
 pytestmark = pytest.mark.gpu
 FLAGS = ch.OUT_LOGITS | ch.OUT_HIDDEN
@@ -56,12 +64,14 @@ def test_device_quantizer_bit_exact(dtype):
     rng = np.random.default_rng(7 + dtype)
     x = np.concatenate([special_blocks(), rng.standard_normal(32 * 40000).astype(np.float32) * 0.05,
                         rng.standard_normal(32 * 1000).astype(np.float32) * 1e4])
+    oracle = cr.quantize_q8(x) if dtype == ch.DTYPE_Q8_0 else cr.quantize_q4(x)
     host = ch.quantize_slice_to_q8(x) if dtype == ch.DTYPE_Q8_0 else ch.quantize_slice_to_q4(x)
     dev = ch.quantize_on_device(dtype, x)
     bb = 36 if dtype == ch.DTYPE_Q8_0 else 20
-    bad = np.nonzero((host.reshape(-1, bb) != dev.reshape(-1, bb)).any(axis=1))[0]
-    print(f"dtype {dtype}: {x.size // 32} blocks, {bad.size} differ", flush=True)
-    assert bad.size == 0, bad[:10]
+    for name, ref in (("oracle", oracle), ("host", host)):
+        bad = np.nonzero((ref.reshape(-1, bb) != dev.reshape(-1, bb)).any(axis=1))[0]
+        print(f"dtype {dtype}: {x.size // 32} blocks, {bad.size} differ from the {name} quantizer", flush=True)
+        assert bad.size == 0, (name, bad[:10])
 
 
 def write_grouped(path, w, header_cfg=None):
@@ -179,3 +189,32 @@ def test_load_without_lm_head(tmp_path):
     assert_same_outputs(m_file, m_host, seqs, "no LM head")
     m_file.close()
     m_host.close()
+
+
+@pytest.mark.parametrize("quantize_to", [-1, ch.DTYPE_Q8_0, ch.DTYPE_Q4_0])
+def test_shipped_8m_file_vs_oracle(w8m_path, quantize_to):
+    cfg = ch.EsmConfig.esm2_8m()
+    w = ch.EsmWeights.from_grouped_canonical(w8m_path, cfg)
+    if quantize_to == ch.DTYPE_Q8_0:
+        w = w.quantize_q8()
+    elif quantize_to == ch.DTYPE_Q4_0:
+        w = w.quantize_q4()
+    contact = cfg.contact_head_weights()
+    flags = ch.OUT_LOGITS | ch.OUT_FINAL_ATT | ch.OUT_CONTACTS
+    m = ch.GpuModel.from_file(w8m_path, quantize_to=quantize_to, contact_head=contact, max_batch=2, max_len=64,
+                              outputs=flags)
+    assert m.dtype == (ch.DTYPE_FP32 if quantize_to < 0 else quantize_to)
+    toks = ch.Tokenizer.encode(PEPTIDE)
+    other = np.concatenate([[0], 4 + np.random.default_rng(8).integers(0, 20, 60), [2]]).astype(np.int32)
+    got = m.forward([toks, other], flags)
+    m.close()
+    for b, t in enumerate((toks, other)):
+        S = len(t)
+        ref = cr.forward(cfg, w, t, 8, contacts=contact)
+        el = float(np.abs(got["logits"][b, :S] - ref["logits"]).max())
+        ea = float(np.abs(got["final_att"][b, :S, :S] - ref["final_att"]).max())
+        ec = float(np.abs(got["contacts"][b, :S - 2, :S - 2] - ref["contacts"]).max())
+        print(f"8M file quantize_to={quantize_to} seq {b}: logits {el:.2e} final_att {ea:.2e} contacts {ec:.2e}",
+              flush=True)
+        assert el <= 1e-3 and ea <= 1e-5 and ec <= 1e-4
+    assert decode(got["logits"][0, 1:len(toks) - 1].argmax(1)) == PEPTIDE

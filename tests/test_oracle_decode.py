@@ -19,10 +19,10 @@ KV cache, SimpleRng, sample, generate_sequence*; src/lib.rs:3506-4233,
 """
 import numpy as np
 import pytest
-from scipy.special import erf
 
 import codon_hip as ch
 import cpu_ref as cr
+from ref64 import forward64
 
 
 # ---- SimpleRng --------------------------------------------------------------
@@ -162,64 +162,13 @@ def test_reference_cosines_at_position0(w8m_all):
     assert cos(lg["fp32"], lg["q4"]) > 0.85
 
 
-def causal_forward64(cfg, w, tokens):
-    """Float64 causal ESM-2 from the mathematics: token i attends to 0..i."""
-    d, F, L, H, V = cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.n_heads, cfg.vocab_size
-    hd = d // H
-    f64 = lambda a: np.asarray(a, np.float64)  # noqa: E731
-    emb = f64(w.token_embedding_table).reshape(V, d)
-    n = len(tokens)
-    x = np.stack([np.zeros(d) if t == 32 else emb[t] * np.float64(np.float32(0.88)) for t in tokens])
-
-    def ln(v, g, b):
-        mu = v.mean(-1, keepdims=True)
-        var = ((v - mu) ** 2).mean(-1, keepdims=True)
-        return g * (v - mu) / np.sqrt(var + 1e-5) + b
-
-    gelu = lambda v: 0.5 * v * (1 + erf(v / np.sqrt(2)))  # noqa: E731
-    half = hd // 2
-    freq = 1.0 / 10000.0 ** (np.arange(half) * 2 / hd)
-    ang = np.arange(n)[:, None] * freq[None, :]
-    c, s = np.cos(ang), np.sin(ang)
-
-    def rope(t):
-        t = t.reshape(n, H, hd)
-        a, b = t[..., :half], t[..., half:]
-        return np.concatenate([a * c[:, None] - b * s[:, None], b * c[:, None] + a * s[:, None]], -1)
-
-    mat = lambda name, l, o, i: f64(getattr(w, name)).reshape(L, o, i)[l]  # noqa: E731
-    vec = lambda name, l, o: f64(getattr(w, name)).reshape(L, o)[l]  # noqa: E731
-    causal = np.tril(np.ones((n, n), bool))
-    for l in range(L):
-        h = ln(x, vec("ln_1_weight", l, d), vec("ln_1_bias", l, d))
-        q = rope(h @ mat("wq", l, d, d).T + vec("bq", l, d))
-        k = rope(h @ mat("wk", l, d, d).T + vec("bk", l, d))
-        v = (h @ mat("wv", l, d, d).T + vec("bv", l, d)).reshape(n, H, hd)
-        sc = np.einsum("qhe,khe->hqk", q, k) / np.sqrt(hd)
-        sc = np.where(causal[None], sc, -np.inf)
-        p = np.exp(sc - sc.max(-1, keepdims=True))
-        p /= p.sum(-1, keepdims=True)
-        o = np.einsum("hqk,khe->qhe", p, v).reshape(n, d)
-        x = x + o @ mat("wo", l, d, d).T + vec("bo", l, d)
-        h = ln(x, vec("ln_2_weight", l, d), vec("ln_2_bias", l, d))
-        h = gelu(h @ mat("fc1_weight", l, F, d).T + vec("fc1_bias", l, F))
-        x = x + h @ mat("fc2_weight", l, d, F).T + vec("fc2_bias", l, d)
-    x = ln(x, f64(w.ln_f_weight), f64(w.ln_f_bias))
-    cw = f64(w.classifier_weights)
-    lnw, lnb = cw[:d], cw[d:2 * d]
-    dw, db = cw[2 * d:2 * d + d * d].reshape(d, d), cw[2 * d + d * d:3 * d + d * d]
-    decw = cw[3 * d + d * d:3 * d + d * d + V * d].reshape(V, d)
-    decb = cw[3 * d + d * d + V * d:]
-    return ln(gelu(x @ dw.T + db), lnw, lnb) @ decw.T + decb
-
-
 def test_kv_cache_positions_against_float64_causal(w8m_all):
     cfg, ws = w8m_all
     w = ws["fp32"]
     toks = [0, 20, 5, 32, 11, 11, 23, 4, 17, 9, 30, 12]
     rs = cr.RunState(cfg, w, max_len=16, num_threads=4)
     steps = np.stack([rs.step(t, p) for p, t in enumerate(toks)])
-    ref = causal_forward64(cfg, w, toks)
+    ref = forward64(cfg, w, toks, causal=True)["logits"]
     err = float(np.abs(steps - ref).max())
     print(f"AR oracle vs float64 causal, 12 positions: {err:.2e}")
     assert err <= 1e-4
