@@ -32,6 +32,7 @@ EXPORTED = [
     "cih_quantize_q4", "cih_dequantize_q8", "cih_dequantize_q4", "cih_tokenize", "cih_log_softmax_canonical",
     "cih_profile_enable", "cih_profile_read", "cih_last_error", "cih_abi_version", "cih_dms",
     "cih_decoder_create", "cih_decoder_destroy", "cih_decoder_reset", "cih_decode", "cih_generate",
+    "cih_matmul_tiled_noalloc",
 ]
 
 DMS_MASKED_MARGINAL, DMS_WILDTYPE_MARGINAL = 0, 1
@@ -99,6 +100,7 @@ def lib():
         "cih_generate": [vp, i32, vp, vp, vp, f32, i32, vp, i32, vp, i32, vp, ctypes.POINTER(ctypes.c_double),
                          ctypes.POINTER(ctypes.c_double)],
         "cih_matmul_tiled": [i32, vp, vp, vp, vp, i32, i32, i32],
+        "cih_matmul_tiled_noalloc": [i32, vp, vp, vp, vp, i32, i32, i32, vp],
         "cih_dequantize_device": [i32, vp, i64, vp],
         "cih_quantize_device": [i32, vp, i64, vp],
         "cih_quantize_q8": [vp, i64, vp],

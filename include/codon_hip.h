@@ -221,6 +221,23 @@ int cih_dms(cih_model *m, const int32_t *residues, int32_t n, int32_t window, in
 int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w,
                      const float *bias, int32_t in_dim, int32_t out_dim, int32_t seq_len);
 
+/* No counterpart in the reference: a variant of cih_matmul_tiled for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  out, x, w and bias are
+ * DEVICE pointers (w 4-byte aligned, x 16-byte aligned; w in the same
+ * reference layout as above); the call is enqueued on `stream` (a
+ * hipStream_t; NULL = the null stream) and returns without waiting.  It
+ * calls no allocator: the repacked weight matrix and the partial sums of a
+ * k-split live in one fixed device array per GPU (48 MiB, held from the time
+ * the library's code is loaded on that GPU until the process ends), so a
+ * matrix whose repacked form exceeds 32 MiB returns CIH_ERR_CAPACITY (650M
+ * FC1 in Q8_0 is 7.4 MB; a 3B FC1 in Q8_0 29.5 MB).  Every call on one GPU
+ * uses the same array: calls that overlap on one GPU (other streams, other
+ * threads) race; calls in order on one stream do not.  Results equal
+ * cih_matmul_tiled's bit for bit. */
+int cih_matmul_tiled_noalloc(int32_t dtype, float *out, const float *x, const void *w, const float *bias,
+                             int32_t in_dim, int32_t out_dim, int32_t seq_len, void *stream);
+
 /* Dequantizes nblocks blocks on the GPU with the decode routine the GEMMs
  * use (BlockQ8_0/BlockQ4_0::dequantize_to, lib.rs:663-667, 1074-1082). */
 int cih_dequantize_device(int32_t dtype, const void *blocks, int64_t nblocks, float *out);
