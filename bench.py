@@ -94,6 +94,17 @@ def physical_cores():
     return os.cpu_count() or 1
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, w, tokens, budget_s, contacts=None):
     """The oracle (the reference's CPU algorithm: row-partitioned 4-token FMA
     GEMMs on a thread pool, serial attention) over whole sequences of the same
@@ -123,8 +134,10 @@ def cpu_baseline(cfg, w, tokens, budget_s, contacts=None):
             break
     what = f"first 256 residues of {done} sequence(s)" if cut else f"{done} sequence(s)"
     return {"value": res / el, "unit": "residues/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
             "sample": f"{what} of the same workload (L={len(tokens[0])}) run serially with "
-                      f"{threads} threads in {el:.1f} s"}
+                      f"{threads} threads in {el:.1f} s (threads = min(16, physical cores): 16 is the "
+                      f"CPU share one GPU's job gets on this host)"}
 
 
 def load_bench(args, ch):
@@ -392,7 +405,9 @@ def main():
     if "maps" in args.outputs:
         flags |= ch.OUT_ATTN
     contact = cfg.contact_head_weights() if flags & ch.OUT_CONTACTS else None
-    model = ch.GpuModel(cfg, w, contact_head=contact, max_batch=B, max_len=S, outputs=flags | ch.IO_DEVICE)
+    # reserved for host-pointer outputs too (staging buffers), so that the
+    # same model also times a short host-I/O pass after the timed one
+    model = ch.GpuModel(cfg, w, contact_head=contact, max_batch=B, max_len=S, outputs=flags)
     hip = Hip()
     d_tok = hip.malloc(toks.nbytes)
     d_log = hip.malloc(B * S * cfg.vocab_size * 4)
@@ -472,6 +487,15 @@ def main():
     logits = np.empty((B, S, cfg.vocab_size), np.float32)
     hip.d2h(logits, d_log)
     assert np.isfinite(logits).all()
+    # Host-pointer I/O (tokens from host memory, outputs copied back over
+    # PCIe inside each call): reported beside the line, never as its value.
+    # (Skipped when every layer's maps are exported: gigabytes per call.)
+    seqs = [toks[b, :lens[b]] for b in range(B)]
+    host_steps = 0 if flags & ch.OUT_ATTN else min(args.steps, 5)
+    t3 = time.perf_counter()
+    for _ in range(host_steps):
+        model.forward(seqs, flags)
+    el_host = time.perf_counter() - t3
 
     residues = int((lens - 2).sum())
     value = residues * args.steps / el
@@ -498,7 +522,12 @@ def main():
         "config": {"workload": f"ESM-2 {args.model} {wname} bidirectional forward, B={B}, {lens_desc}, "
                                f"seeded N(0,0.02) weights{' quantized in-tree' if args.dtype != 'fp32' else ''}, "
                                f"uniform 20-AA tokens, {outs_desc} to HBM",
-                   "batch": B, "seq_len": S, "residues_per_step": residues, "parallelism": "single GPU"},
+                   "batch": B, "seq_len": S, "residues_per_step": residues, "parallelism": "single GPU",
+                   "io": "tokens read from and outputs written to HBM (CIH_IO_DEVICE): the timed region holds "
+                         "no host transfer"},
+        "host_io": ({"value": round(residues * host_steps / el_host, 1), "unit": "residues/s",
+                     "ms_per_step": round(el_host * 1e3 / host_steps, 3), "steps": host_steps,
+                     "note": "host-pointer tokens and outputs, PCIe copies inside each call"} if host_steps else None),
         "roofline": ({"bound": "hbm", "kernel": kname,
                       "achieved": round(achieved, 1), "peak": peak, "unit": "GB/s",
                       "frac": round(achieved / peak, 4),

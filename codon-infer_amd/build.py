@@ -49,7 +49,28 @@ def build(verbose=True):
     os.replace(tmp, OUT)
     if verbose:
         print("built", OUT)
+    build_capi(verbose)
     return OUT
+
+
+CAPI_SRC = os.path.join(HERE, "capi", "pipeline.c")
+CAPI_OUT = os.path.join(HERE, "capi", "pipeline")
+
+
+def build_capi(verbose=True):
+    """The C caller of the ABI (capi/pipeline.c), compiled as C99 against
+    include/codon_hip.h with gcc and linked to the library next to it."""
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no C compiler for capi/pipeline.c")
+    cmd = [cc, "-O2", "-std=c99", "-D_POSIX_C_SOURCE=200809L", "-Wall", "-Wextra", "-Werror", CAPI_SRC, "-o",
+           CAPI_OUT + ".tmp", "-L" + os.path.dirname(OUT), "-lcodon_hip", "-Wl,-rpath,$ORIGIN/../codon_hip", "-lm"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(CAPI_OUT + ".tmp", CAPI_OUT)
+    if verbose:
+        print("built", CAPI_OUT)
 
 
 if __name__ == "__main__":

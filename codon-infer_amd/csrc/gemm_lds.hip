@@ -379,6 +379,7 @@ int tile_choice(int M, int N) {
 template <int EPI>
 hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
     const char *e = getenv("CIH_GEMM_TILE_N");
+    if (const char *eg = getenv("CIH_GEMM_TILE_N_GELU"); eg && EPI == EPI_GELU_H2) e = eg;
     const int bn = e ? atoi(e) : tile_choice(M, W.N);
     if (bn == 320) return launch_t<EPI, 1, 5, 4, 2>(W, X, bias, Y, ldy, M, st);
     if (bn == 256) return launch_t<EPI, 2, 2, 2, 4>(W, X, bias, Y, ldy, M, st);

@@ -132,3 +132,37 @@ def test_file_reader_accepts_valid_files(tmp_path, w8m_path):
         assert rc == (0 if on_gpu else -5), (path, qt, C.lib().cih_last_error())
     # a Q8 file cannot be requantized to Q4
     assert _create_from_file(q8, 2) == -1
+
+
+def test_capi_driver_builds_and_reports_errors(w8m_path):
+    """The C caller (capi/pipeline.c) is built with the library; without a
+    device it stops at the first HIP call with the library's message."""
+    import subprocess
+    drv = os.path.join(REPO, "codon-infer_amd", "capi", "pipeline")
+    assert os.path.exists(drv)
+    r = subprocess.run([drv], capture_output=True, text=True)
+    assert r.returncode == 2 and "usage" in r.stderr
+    if os.environ.get("CIH_EXPECT_GPU") != "1":
+        r = subprocess.run([drv, "dms", w8m_path, "LAGV", "0", "0", "0", "2"], capture_output=True, text=True)
+        assert r.returncode == 1 and "cih_model_create_from_file failed (-5)" in r.stderr, r.stderr
+
+
+def test_rust_ffi_declares_every_entry_point():
+    """rust/codon-hip-sys/src/lib.rs declares exactly the functions of
+    include/codon_hip.h, with the same number of parameters (no cargo in
+    this image, so this is the check that the binding tracks the header)."""
+    with open(os.path.join(REPO, "include", "codon_hip.h")) as f:
+        header = f.read()
+    with open(os.path.join(REPO, "rust", "codon-hip-sys", "src", "lib.rs")) as f:
+        rust = f.read()
+    c_funcs = {}
+    for m in re.finditer(r"\b(?:int|const char \*)\s*(cih_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", header):
+        args = [a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        c_funcs[m.group(1)] = len(args)
+    r_funcs = {}
+    for m in re.finditer(r"pub fn (cih_[a-z0-9_]+)\(([^)]*)\)", rust):
+        args = [a for a in m.group(2).split(",") if a.strip()]
+        r_funcs[m.group(1)] = len(args)
+    assert c_funcs and c_funcs == r_funcs, (set(c_funcs) ^ set(r_funcs),
+                                            {k: (c_funcs.get(k), r_funcs.get(k)) for k in c_funcs
+                                             if c_funcs.get(k) != r_funcs.get(k)})
