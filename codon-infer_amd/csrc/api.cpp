@@ -40,7 +40,7 @@ std::string kernel_switches() {
     static const char *const names[] = {"CIH_ATT",     "CIH_ATT_QB", "CIH_ATT_SPLIT", "CIH_SPLITK",
                                         "CIH_QGEMM",   "CIH_ACT",    "CIH_LIMBS",     "CIH_GEMV",
                                         "CIH_GEMV_NB", "CIH_GEMM_LDS", "CIH_GEMM_TILE", "CIH_GEMM_TILE_N",
-                                        "CIH_GEMM_TILE_N_GELU"};
+                                        "CIH_GEMM_TILE_N_GELU", "CIH_ATT_IMG"};
     std::string s = g_full_range ? "R|" : "|";
     for (const char *n : names) {
         const char *v = getenv(n);
@@ -248,6 +248,13 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
     }
     const bool need_P = flags & (CIH_OUT_CONTACTS | CIH_OUT_FINAL_ATT | CIH_OUT_ATTN);
     if (good && need_P) good = ok(dalloc(ws.P, B * H * S * S, dl));
+    if (good && attention_img_supported((int)m->hd)) {
+        // tile images for every (tile row, head): at most B ceil(S / 32) tile rows;
+        // zeroed once, so dims past hd stay zero (nothing writes them)
+        const size_t img = B * ((S + 31) / 32) * H * kv_image_bytes((int)m->hd);
+        good = ok(dalloc(ws.kv_img, img, dl)) && ok(dalloc(ws.kv_tb, B, dl)) && ok(dalloc(ws.kv_pk, T, dl)) &&
+               ok(dalloc(ws.kv_pos, T, dl)) && ok(hipMemset(ws.kv_img, 0, img));
+    }
     if (good && (flags & CIH_OUT_CONTACTS))
         good = ok(dalloc(ws.M, B * n * n, dl)) && ok(dalloc(ws.r, L * H * B * n, dl)) &&
                ok(dalloc(ws.coef, L * H * B, dl)) && ok(dalloc(ws.rowsum, B * H * S, dl)) &&
@@ -355,6 +362,32 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         }
     }
     const int epi_fc1 = af == AF_X3 ? EPI_GELU_X3 : (af == AF_H2 ? EPI_GELU_H2 : EPI_GELU);
+    // K/V tile images: the QKV projection's epilogue rotates K, splits K and V
+    // into f16 limbs and lays them out as attention's LDS tiles, once per
+    // key; attention copies them (CIH_ATT_IMG=0: K/V as FP32 rows, staged by
+    // attention itself).  Needs the LDS GEMM for the projection and the
+    // f16-limb attention.
+    // Other projections (GEMV, register-staged GEMMs, FP32 weights) write FP32
+    // rows and a prep kernel builds the same images from them, so that every
+    // batch shape runs the same attention kernel on the same bytes.
+    bool use_img = false, epi_img = false;
+    int tile_rows = 0;
+    {
+        const char *ie = getenv("CIH_ATT_IMG"), *ae = getenv("CIH_ATT");
+        use_img = ws.kv_img && L > 0 && !(ie && !std::strcmp(ie, "0")) && !(ae && !std::strcmp(ae, "fp32")) &&
+                  !full_range_mode() && attention_img_supported((int)m->hd);
+        epi_img = use_img && af == AF_H2 && gemm_lds_applies(m->layers[0].wqkv, af, T, EPI_NONE);
+        for (int b = 0; b < B; b++) tile_rows += (lens[b] + 31) / 32;
+    }
+    const int epi_qkv = m->hd == 16 ? EPI_QKV16 : (m->hd == 32 ? EPI_QKV32 : EPI_QKV64);
+    QkvOut qo;
+    qo.pk = ws.kv_pk;
+    qo.pos = ws.kv_pos;
+    qo.rc = ws.rope_c;
+    qo.rs = ws.rope_s;
+    qo.img = ws.kv_img;
+    qo.d = d;
+    qo.H = H;
 
     m->prof.used = 0;
     // the contact accumulator and the status word are cleared outside the
@@ -369,6 +402,10 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
         HIPCHK(launch_embed(ws.tokens, sm, m->emb.fmt, m->emb.q, m->emb.sc, d, V, ws.x, st, ws.flag));
     }
+    if (use_img) {
+        ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T);
+        HIPCHK(launch_kv_setup(sm, (int)m->hd, H, ws.kv_tb, ws.kv_pk, ws.kv_pos, ws.kv_img, st));
+    }
 
     for (int l = 0; l < L; l++) {
         const Layer &ly = m->layers[l];
@@ -376,7 +413,17 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
             HIPCHK(launch_layernorm(ws.x, ly.ln1w, ly.ln1b, ws.xb, af, T, d, st));
         }
-        HIPCHK(gemm(m, ly.wqkv, ws.xb, d, af, ly.bqkv, ws.qkv, 3 * d, T, EPI_NONE));
+        if (epi_img) {
+            const double bytes = wbytes(ly.wqkv) + 4.0 * T * d + 4.0 * T * 3 * d;
+            ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * T * ly.wqkv.N * ly.wqkv.K, bytes);
+            HIPCHK(launch_gemm_lds(ly.wqkv, ws.xb, ly.bqkv, ws.qkv, 3 * d, T, epi_qkv, st, &qo));
+        } else {
+            HIPCHK(gemm(m, ly.wqkv, ws.xb, d, af, ly.bqkv, ws.qkv, 3 * d, T, EPI_NONE));
+            if (use_img) {
+                ProfScope ps(m, CIH_KC_OTHER, 0, 16.0 * T * d);
+                HIPCHK(launch_kv_prep(ws.qkv, d, H, sm, ws.kv_tb, tile_rows, ws.rope_c, ws.rope_s, ws.kv_img, st));
+            }
+        }
         // probabilities: straight into the attention-map output when exported
         float *P = nullptr;
         int64_t pb = 0, ph = SS;
@@ -392,8 +439,13 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             double fl = 0;
             for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
             ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
-            HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, af, P, pb, ph,
-                                    want_contacts && m->nz[l] > 0 ? ws.rowsum : nullptr, ws.attp, ws.attp_floats, st));
+            float *rsum = want_contacts && m->nz[l] > 0 ? ws.rowsum : nullptr;
+            if (use_img)
+                HIPCHK(launch_attention_img(ws.qkv, d, H, sm, ws.kv_tb, ws.kv_img, ws.rope_c, ws.rope_s, ws.ao, af, P,
+                                            pb, ph, rsum, ws.attp, ws.attp_floats, st));
+            else
+                HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, af, P, pb, ph, rsum, ws.attp,
+                                        ws.attp_floats, st));
         }
         if (want_contacts && m->nz[l] > 0) {
             ProfScope ps(m, CIH_KC_OTHER, 0, 0);

@@ -44,6 +44,7 @@
 #include <type_traits>
 
 #include "kernels.h"
+#include "kv_image.h"
 
 namespace cih {
 
@@ -51,6 +52,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
 
 // Stores a lane's 16 probabilities (keys k0 + 8g + e, g = 0..3, e = 0..3) of
 // one query row: 16-byte stores where a group is whole and aligned.
@@ -319,6 +321,18 @@ __device__ __forceinline__ void split8(const float *v, f16x8 &hi, f16x8 &lo) {
     }
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void split8_mix(const float *v, f16x8 &hi, f16x8 &lo) {
+    uint4 h, l;
+    h.x = split_pair(v[0], v[1], l.x);
+    h.y = split_pair(v[2], v[3], l.y);
+    h.z = split_pair(v[4], v[5], l.z);
+    h.w = split_pair(v[6], v[7], l.w);
+    hi = __builtin_bit_cast(f16x8, h);
+    lo = __builtin_bit_cast(f16x8, l);
+}
+
 // Work items: (sequence, head, query block) tasks, task = (b * H + h) * nq + qb,
 // one workgroup each for the first nfull; every later task is split into
 // nsplit ranges of whole 32-key tiles (one workgroup each, ONEPASS only)
@@ -332,6 +346,8 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                                                      long long pb, long long ph, float inv_scale,
                                                      float *__restrict__ rowsum, int H, int nq, int nfull, int nsplit,
                                                      float *__restrict__ part) {
+    // no FMA contraction: the staged and the image kernel round alike
+#pragma clang fp contract(off)
     constexpr int HALF = HD / 2;
     constexpr int HDP = (HD + 15) / 16 * 16;  // dims padded to whole 16-wide k-chunks
     constexpr int NC = HDP / 16;
@@ -394,8 +410,8 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
             for (int e = 0; e < 8; e++) {
                 const int dim = 16 * c + 8 * hh + e;
                 float r = 0.0f;
-                if (dim < HALF) r = qrow[dim] * cs[dim] - qrow[dim + HALF] * sn[dim];
-                else if (dim < HD) r = qrow[dim] * cs[dim - HALF] + qrow[dim - HALF] * sn[dim - HALF];
+                if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
+                else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
                 v[e] = r;
             }
             split8(v, qh[c], ql[c]);
@@ -413,10 +429,10 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
             const float4 k1 = *reinterpret_cast<const float4 *>(krow + c + HALF);
             const float4 cs = *reinterpret_cast<const float4 *>(rc + (size_t)kk * HALF + c);
             const float4 sn = *reinterpret_cast<const float4 *>(rsn + (size_t)kk * HALF + c);
-            const float r0[4] = {k0.x * cs.x - k1.x * sn.x, k0.y * cs.y - k1.y * sn.y, k0.z * cs.z - k1.z * sn.z,
-                                 k0.w * cs.w - k1.w * sn.w};
-            const float r1[4] = {k1.x * cs.x + k0.x * sn.x, k1.y * cs.y + k0.y * sn.y, k1.z * cs.z + k0.z * sn.z,
-                                 k1.w * cs.w + k0.w * sn.w};
+            const float r0[4] = {rot_lo(k0.x, k1.x, cs.x, sn.x), rot_lo(k0.y, k1.y, cs.y, sn.y),
+                                 rot_lo(k0.z, k1.z, cs.z, sn.z), rot_lo(k0.w, k1.w, cs.w, sn.w)};
+            const float r1[4] = {rot_hi(k1.x, k0.x, cs.x, sn.x), rot_hi(k1.y, k0.y, cs.y, sn.y),
+                                 rot_hi(k1.z, k0.z, cs.z, sn.z), rot_hi(k1.w, k0.w, cs.w, sn.w)};
             f16x4 h0, l0, h1, l1;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -467,8 +483,8 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     // (register 8c + e = key 16c + 8(e/4) + 4hh + e%4), A = V^T read in that key order
     auto pv = [&](f32x16 (&oacc)[DT], const float (&p)[16]) {
         f16x8 phi[2], plo[2];
-        split8(p, phi[0], plo[0]);
-        split8(p + 8, phi[1], plo[1]);
+        split8_mix(p, phi[0], plo[0]);
+        split8_mix(p + 8, phi[1], plo[1]);
 #pragma unroll
         for (int t = 0; t < DT; t++) {
             const int row = cur * VBUF + (t * 32 + li) * V_LD;
@@ -492,8 +508,10 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     if constexpr (ONEPASS) {
         // One pass, online softmax (see k_attention) in base 2: scores are
         // pre-scaled by log2(e) / sqrt(hd) so every exponential is one
-        // v_exp_f32.  Whole tiles skip the key mask; the output accumulators
-        // are rescaled only when some lane's running max moved.
+        // v_exp_f32.  Whole tiles skip the key mask.  The exponent offset m
+        // follows the running max lazily (it moves only when a score exceeds
+        // it by more than 8, so p <= 256), which leaves the accumulators
+        // unscaled on most tiles; o / l is unchanged.
         const float sl2 = inv_scale * 1.44269504088896340736f;
         float m = -INFINITY, l = 0.0f;
         auto tile = [&](int kt0, auto masked) {
@@ -515,23 +533,26 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 sv[q] = v;
                 tmax = fmaxf(tmax, v);
             }
-            // key kt0 (< kend) sits in half 0, so the combined tile max is finite
-            const float mn = fmaxf(m, fmaxf(tmax, __shfl_xor(tmax, 32)));
-            const float corr = __builtin_amdgcn_exp2f(m - mn);
-            float p[16], sum = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                p[q] = __builtin_amdgcn_exp2f(sv[q] - mn);
-                sum += p[q];
-            }
-            l = l * corr + sum;
-            m = mn;
-            if (__ballot(corr != 1.0f)) {
+            // key kt0 (< kend) sits in half 0, so the combined tile max is finite;
+            // the offset m moves only when a score exceeds it by more than 8
+            const float tm = fmaxf(tmax, __shfl_xor(tmax, 32));
+            if (__ballot(tm > m + 8.0f)) {
+                const float mn = tm > m + 8.0f ? tm : m;
+                const float corr = __builtin_amdgcn_exp2f(m - mn);
+                l *= corr;
+                m = mn;
 #pragma unroll
                 for (int t = 0; t < DT; t++)
 #pragma unroll
                     for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
             }
+            float p[16], sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                p[q] = __builtin_amdgcn_exp2f(sv[q] - m);
+                sum += p[q];
+            }
+            l += sum;
             pv(oacc, p);
         };
         int kt0 = kbeg;
@@ -602,8 +623,8 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                     f16x4 h0, l0, h1, l1;
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        const float r0 = k0[e] * cs[e] - k1[e] * sn[e];
-                        const float r1 = k1[e] * cs[e] + k0[e] * sn[e];
+                        const float r0 = rot_lo(k0[e], k1[e], cs[e], sn[e]);
+                        const float r1 = rot_hi(k1[e], k0[e], cs[e], sn[e]);
                         h0[e] = (_Float16)r0;
                         l0[e] = (_Float16)(r0 - (float)h0[e]);
                         h1[e] = (_Float16)r1;
@@ -755,6 +776,360 @@ __global__ __launch_bounds__(256) void k_attention_merge(const float *__restrict
         *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + row * d + h * HD + c) = v;
 }
 
+// 16 bytes global -> LDS by the load unit: lane l writes LDS bytes
+// [lds_base + 16 l, +16).  Issued from inline assembly so that the compiler,
+// which cannot see these LDS writes, does not wait for them at every LDS read
+// (the kernels wait with explicit vmcnt counts before their barriers).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; listing it keeps values out of it here
+__device__ __forceinline__ void dma16(const void *g, unsigned lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Attention over K/V tile images (kv_image.h): the same tasks, key split,
+// arithmetic and outputs as k_attention_h, but a key tile is staged by a flat
+// copy of its image (global_load_lds, issued one tile ahead into the other of
+// two LDS stages) instead of being rotated, split and transposed here; one
+// barrier per tile.  The one-pass softmax keeps its exponent offset m until
+// a score exceeds it by more than 8 (base-2 units), so the accumulators are
+// rescaled rarely and p <= 256 (the normalisation is unchanged: o / l with o
+// and l under the same offset).
+template <int HD, bool ONEPASS, int NTH>
+__global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_img(
+    const float *__restrict__ qkv, int d, const int *__restrict__ cu, const int *__restrict__ lens, int S_max,
+    const int *__restrict__ tb, const unsigned char *__restrict__ img, const float *__restrict__ rc,
+    const float *__restrict__ rsn, void *__restrict__ out, int out_fmt, float *__restrict__ P, long long pb,
+    long long ph, float inv_scale, float *__restrict__ rowsum, int H, int nq, int nfull, int nsplit,
+    float *__restrict__ part) {
+    // no FMA contraction: the staged and the image kernel round alike
+#pragma clang fp contract(off)
+    using I = KvImg<HD>;
+    constexpr int HALF = I::HALF, HDP = I::HDP, NC = HDP / 16, VW = I::VW, DT = VW / 32, TB = I::TB;
+    constexpr int NWV = NTH / 64;
+    constexpr int NJ = TB / 1024, JPW = (NJ + NWV - 1) / NWV;             // whole tile
+    constexpr int NJK = I::VOFF / 1024, JPWK = (NJK + NWV - 1) / NWV;     // K rows only
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * TB];
+
+    int task = blockIdx.x, ks = 0, ns = 1;
+    if (task >= nfull) {
+        const int t = task - nfull;
+        task = nfull + t / nsplit;
+        ks = t % nsplit;
+        ns = nsplit;
+    }
+    const int qb = task % nq, h = (task / nq) % H, b = task / nq / H;
+    const int len = lens[b], base = cu[b];
+    const int qblk = qb * (NTH / 2);
+    if (qblk >= len) return;
+    const int ntile_all = (len + 31) / 32, per = (ntile_all + ns - 1) / ns;
+    const int t0 = min(ks * per, ntile_all), t1 = min((ks + 1) * per, ntile_all);  // tiles [t0, t1)
+    const int kend = min(t1 * 32, len);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, hh = lane >> 5;
+    const size_t ld = (size_t)3 * d;
+    const float sl2 = inv_scale * 1.44269504088896340736f;
+
+    // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs
+    const int qi = qblk + wave * 32 + li;
+    const int qc = min(qi, len - 1);
+    f16x8 qh[NC], ql[NC];
+    {
+        const float *qrow = qkv + (size_t)(base + qc) * ld + h * HD;
+        const float *cs = rc + (size_t)qc * HALF, *sn = rsn + (size_t)qc * HALF;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int dim = 16 * c + 8 * hh + e;
+                float r = 0.0f;
+                if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
+                else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
+                v[e] = r;
+            }
+            split8_mix(v, qh[c], ql[c]);
+        }
+    }
+
+    // image of key tile t (absolute within the sequence) of this head
+    const unsigned char *himg = img + ((size_t)tb[b] * H + h) * TB;
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds);
+    // Copies tile t into stage stg: instruction j (1 KiB) is issued by wave j % NWV.
+    auto dma = [&](int t, int stg, auto with_v) __attribute__((always_inline)) {
+        constexpr int nj = decltype(with_v)::value ? NJ : NJK, jpw = decltype(with_v)::value ? JPW : JPWK;
+        const unsigned char *src = himg + (size_t)t * H * TB + lane * 16;
+#pragma unroll
+        for (int i = 0; i < jpw; i++) {
+            const int j = i * NWV + wave;
+            if (j < nj) dma16(src + j * 1024, __builtin_amdgcn_readfirstlane(lds0 + stg * TB + j * 1024));
+        }
+    };
+    // S^T tile (32 keys x 32 queries) from stage st
+    auto scores = [&](const unsigned char *st, f32x16 &acc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[q] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int dim = 16 * c + 8 * hh;
+            const f16x8 kh = *reinterpret_cast<const f16x8 *>(st + li * I::KRP + I::kchunk(li, I::klc(dim, 0)) * 16);
+            const f16x8 kl = *reinterpret_cast<const f16x8 *>(st + li * I::KRP + I::kchunk(li, I::klc(dim, 1)) * 16);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[c], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[c], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[c], acc, 0, 0, 0);
+        }
+    };
+    // O^T += V^T P^T: register 8c + e of lane half hh holds key 16c + 8(e/4) + 4hh + e%4
+    auto pv = [&](const unsigned char *st, f32x16 (&oacc)[DT], const float (&p)[16]) __attribute__((always_inline)) {
+        f16x8 phi[2], plo[2];
+        split8_mix(p, phi[0], plo[0]);
+        split8_mix(p + 8, phi[1], plo[1]);
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            const int row = t * 32 + li;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const unsigned char *vr = st + I::VOFF + row * 128;
+                const f16x8 vh = *reinterpret_cast<const f16x8 *>(vr + I::vchunk(row, 2 * c + hh) * 16);
+                const f16x8 vl = *reinterpret_cast<const f16x8 *>(vr + I::vchunk(row, 4 + 2 * c + hh) * 16);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, phi[c], oacc[t], 0, 0, 0);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, plo[c], oacc[t], 0, 0, 0);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, phi[c], oacc[t], 0, 0, 0);
+            }
+        }
+    };
+    // One sweep over tiles [t0, t1): tile t + 1 is copied while tile t is
+    // computed.  Before the barrier a wave waits for its own copies of tile
+    // t; after it, every wave's copies have landed and every wave is done
+    // with the stage tile t + 1 goes to.
+    // Whole tiles run in one loop, a partial last tile after it (one inlined
+    // copy of the body per loop keeps the register allocation of each).
+    auto sweep = [&](auto with_v, auto body) __attribute__((always_inline)) {
+        __syncthreads();  // a previous sweep's reads of the stages are done
+        if (t0 < t1) dma(t0, 0, with_v);
+        auto step = [&](int t, auto masked) __attribute__((always_inline)) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (t + 1 < t1) dma(t + 1, (t - t0 + 1) & 1, with_v);
+            body(lds + ((t - t0) & 1) * TB, t * 32, masked);
+        };
+        const int tw = t1 > t0 && kend < t1 * 32 ? t1 - 1 : t1;  // past the whole tiles (an empty range: t1)
+        for (int t = t0; t < tw; t++) step(t, std::false_type{});
+        if (tw < t1) step(tw, std::true_type{});
+    };
+
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
+    float out_scale;
+    if constexpr (ONEPASS) {
+        float m = -INFINITY, l = 0.0f;
+        sweep(std::true_type{}, [&](const unsigned char *st, int kt0, auto masked) __attribute__((always_inline)) {
+            f32x16 acc;
+            scores(st, acc);
+            float sv[16];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                float v = acc[q] * sl2;
+                if constexpr (decltype(masked)::value) {
+                    const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                    v = key < kend ? v : -INFINITY;
+                }
+                sv[q] = v;
+                tmax = fmaxf(tmax, v);
+            }
+            // key kt0 (< kend) sits in half 0, so the combined tile max is finite
+            const float tm = fmaxf(tmax, __shfl_xor(tmax, 32));
+            if (__ballot(tm > m + 8.0f)) {
+                const float mn = tm > m + 8.0f ? tm : m;
+                const float corr = __builtin_amdgcn_exp2f(m - mn);
+                l *= corr;
+                m = mn;
+#pragma unroll
+                for (int t = 0; t < DT; t++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
+            }
+            float p[16], sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                p[q] = __builtin_amdgcn_exp2f(sv[q] - m);
+                sum += p[q];
+            }
+            l += sum;
+            pv(st, oacc, p);
+        });
+        const float lt = l + __shfl_xor(l, 32);
+        if (ns > 1) {
+            // split task: unnormalized output, exponent offset (base 2) and sum
+            if (qi < len) {
+                float *pr = part + ((size_t)(blockIdx.x - nfull) * (NTH / 2) + wave * 32 + li) * (HD + 2);
+#pragma unroll
+                for (int t = 0; t < DT; t++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int dd = t * 32 + 8 * g + 4 * hh;
+                        if (dd >= HD) continue;
+                        *reinterpret_cast<float2 *>(pr + dd) = make_float2(oacc[t][4 * g], oacc[t][4 * g + 1]);
+                        *reinterpret_cast<float2 *>(pr + dd + 2) = make_float2(oacc[t][4 * g + 2], oacc[t][4 * g + 3]);
+                    }
+                if (hh == 0) *reinterpret_cast<float2 *>(pr + HD) = make_float2(m, lt);
+            }
+            return;
+        }
+        out_scale = 1.0f / lt;
+    } else {
+        // pass 1 (K limbs only): running max / sum of exp per lane
+        float m = -INFINITY, l = 0.0f;
+        sweep(std::false_type{}, [&](const unsigned char *st, int kt0, auto) __attribute__((always_inline)) {
+            f32x16 acc;
+            scores(st, acc);
+            float sv[16];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
+                tmax = fmaxf(tmax, sv[q]);
+            }
+            const float mn = fmaxf(m, tmax);
+            if (mn != -INFINITY) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) sum += __builtin_amdgcn_exp2f(sv[q] - mn);
+                l = l * __builtin_amdgcn_exp2f(m - mn) + sum;
+                m = mn;
+            }
+        });
+        const float mo = __shfl_xor(m, 32), lo = __shfl_xor(l, 32);
+        const float mx = fmaxf(m, mo);
+        const float inv_sum = 1.0f / (l * __builtin_amdgcn_exp2f(m - mx) + lo * __builtin_amdgcn_exp2f(mo - mx));
+        // pass 2: normalized probabilities, optional export, P.V
+        float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+        float rs = 0.0f;
+        sweep(std::true_type{}, [&](const unsigned char *st, int kt0, auto) __attribute__((always_inline)) {
+            f32x16 acc;
+            scores(st, acc);
+            float p[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - mx) * inv_sum : 0.0f;
+            }
+            if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
+            if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
+            pv(st, oacc, p);
+        });
+        write_rowsum(rowsum, rs, b, h, H, S_max, qi, len, hh);
+        out_scale = 1.0f;
+    }
+    if (qi < len) {
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int dd = t * 32 + 8 * g + 4 * hh;
+                if (dd >= HD) continue;
+                const float4 v = make_float4(oacc[t][4 * g] * out_scale, oacc[t][4 * g + 1] * out_scale,
+                                             oacc[t][4 * g + 2] * out_scale, oacc[t][4 * g + 3] * out_scale);
+                if (out_fmt == AF_X3)
+                    x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                else if (out_fmt == AF_H2)
+                    h2_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+                else
+                    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d + h * HD +
+                                                dd) = v;
+            }
+    }
+}
+
+// Per-forward set-up of the tile images, one workgroup per sequence b:
+// tb[b] = sum of ceil(len / 32) over the sequences before b; pk = 32 tb[b] +
+// position and pos = position for its tokens; the padding keys (positions
+// len..) of its last tile are zeroed in every head's image, both limbs, so
+// that masked keys multiply zeros whatever an earlier batch left there.
+template <int HD>
+__global__ __launch_bounds__(256) void k_kv_setup(const int *__restrict__ cu, const int *__restrict__ lens, int H,
+                                                  int *__restrict__ tb, int *__restrict__ pk, int *__restrict__ pos,
+                                                  unsigned char *__restrict__ img) {
+    using I = KvImg<HD>;
+    const int b = blockIdx.x;
+    __shared__ int s_first;
+    if (threadIdx.x == 0) {
+        int f = 0;
+        for (int i = 0; i < b; i++) f += (lens[i] + 31) / 32;
+        s_first = f;
+        tb[b] = f;
+    }
+    __syncthreads();
+    const int first = s_first, len = lens[b], base = cu[b];
+    for (int t = threadIdx.x; t < len; t += 256) {
+        pk[base + t] = first * 32 + t;
+        pos[base + t] = t;
+    }
+    const int pad = (32 - len % 32) % 32;
+    if (pad == 0 || len == 0) return;
+    const int last = first + (len - 1) / 32, k0 = len % 32;
+    // (head, limb, padding key, dim) of K (HDP dims) and V (VW dims)
+    const int per = 2 * pad * (I::HDP + I::VW);
+    for (int idx = threadIdx.x; idx < H * per; idx += 256) {
+        const int h = idx / per, r = idx % per;
+        const int limb = r / (pad * (I::HDP + I::VW)), r2 = r % (pad * (I::HDP + I::VW));
+        unsigned char *t = img + ((size_t)last * H + h) * I::TB;
+        if (r2 < pad * I::HDP) {
+            const int key = k0 + r2 / I::HDP, dim = r2 % I::HDP;
+            *reinterpret_cast<_Float16 *>(t + I::koff(key, dim, limb)) = (_Float16)0.0f;
+        } else {
+            const int r3 = r2 - pad * I::HDP, key = k0 + r3 / I::VW, dim = r3 % I::VW;
+            *reinterpret_cast<_Float16 *>(t + I::voff(key, dim, limb)) = (_Float16)0.0f;
+        }
+    }
+}
+
+// Tile images from FP32 Q|K|V rows, for projections that did not write them
+// in their epilogue (GEMV, the register-staged GEMMs, FP32 weights): the
+// same rotation and split as the LDS GEMM's QKV epilogue, so both give the
+// same bytes.  One workgroup per (tile row, head); consecutive threads take
+// consecutive dims of a key (coalesced reads).  Padding keys are left to
+// k_kv_setup.
+template <int HD>
+__global__ __launch_bounds__(256) void k_kv_prep(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
+                                                 const int *__restrict__ lens, const int *__restrict__ tb, int B,
+                                                 const float *__restrict__ rc, const float *__restrict__ rsn,
+                                                 unsigned char *__restrict__ img, int H) {
+    using I = KvImg<HD>;
+    constexpr int HALF = HD / 2;
+    const int tr = blockIdx.x / H, h = blockIdx.x % H;
+    // the sequence owning tile row tr: the last b with tb[b] <= tr
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tb[mid] <= tr) lo = mid;
+        else hi = mid - 1;
+    }
+    const int b = lo, kt0 = (tr - tb[b]) * 32, len = lens[b];
+    const size_t ld = (size_t)3 * d;
+    const float *base = qkv + (size_t)(cu[b] + kt0) * ld + h * HD;
+    unsigned char *t = img + ((size_t)tr * H + h) * I::TB;
+    const int nk = min(32, len - kt0);
+    for (int idx = threadIdx.x; idx < nk * HD; idx += 256) {
+        const int key = idx / HD, j = idx % HD, jj = j < HALF ? j : j - HALF;
+        const float *k = base + (size_t)key * ld + d;
+        const size_t ti = (size_t)(kt0 + key) * HALF + jj;
+        const float c = rc[ti], s = rsn[ti];
+        const float r = j < HALF ? rot_lo(k[j], k[j + HALF], c, s) : rot_hi(k[j], k[j - HALF], c, s);
+        const _Float16 rh = (_Float16)r, rl = (_Float16)(r - (float)rh);
+        *reinterpret_cast<_Float16 *>(t + I::koff(key, j, 0)) = rh;
+        *reinterpret_cast<_Float16 *>(t + I::koff(key, j, 1)) = rl;
+        const float v = base[(size_t)key * ld + 2 * d + j];
+        const _Float16 vh = (_Float16)v, vl = (_Float16)(v - (float)vh);
+        *reinterpret_cast<_Float16 *>(t + I::voff(key, j, 0)) = vh;
+        *reinterpret_cast<_Float16 *>(t + I::voff(key, j, 1)) = vl;
+    }
+}
+
 // Rows of partial results the key split may use: one row per query of a
 // workgroup slot, two rounds of 256-query (or four of 128-query) slots.
 size_t attention_part_floats(int hd) { return (size_t)device_cus() * 512 * (hd + 2); }
@@ -830,6 +1205,95 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
 #undef CIH_ATT
 #undef CIH_ATT_H
 #undef CIH_ATT_K
+    return hipGetLastError();
+}
+
+bool attention_img_supported(int hd) { return hd == 16 || hd == 32 || hd == 64; }
+
+size_t kv_image_bytes(int hd) {
+    return hd == 16 ? KvImg<16>::TB : (hd == 32 ? KvImg<32>::TB : (hd == 64 ? KvImg<64>::TB : 0));
+}
+
+hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos, unsigned char *img, hipStream_t st) {
+    if (sm.B <= 0) return hipSuccess;
+#define CIH_KVS(HDV) hipLaunchKernelGGL((k_kv_setup<HDV>), dim3(sm.B), dim3(256), 0, st, sm.cu, sm.lens, H, tb, pk, pos, img)
+    switch (hd) {
+    case 16: CIH_KVS(16); break;
+    case 32: CIH_KVS(32); break;
+    case 64: CIH_KVS(64); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef CIH_KVS
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_prep(const float *qkv, int d, int H, SeqMeta sm, const int *tb, int tile_rows, const float *rope_cos,
+                          const float *rope_sin, unsigned char *img, hipStream_t st) {
+    if (tile_rows <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)tile_rows * H;
+#define CIH_KVP(HDV)                                                                                              \
+    hipLaunchKernelGGL((k_kv_prep<HDV>), dim3(grid), dim3(256), 0, st, qkv, d, sm.cu, sm.lens, tb, sm.B, rope_cos, \
+                       rope_sin, img, H)
+    switch (d / H) {
+    case 16: CIH_KVP(16); break;
+    case 32: CIH_KVP(32); break;
+    case 64: CIH_KVP(64); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef CIH_KVP
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_img(const float *qkv, int d, int H, SeqMeta sm, const int *tb, const unsigned char *img,
+                                const float *rope_cos, const float *rope_sin, void *out, int out_fmt, float *P,
+                                int64_t pb, int64_t ph, float *rowsum, float *part, size_t part_floats, hipStream_t st) {
+    if (rowsum && !P) return hipErrorInvalidValue;
+    if ((out_fmt == AF_X3 || out_fmt == AF_H2) && d % 32) return hipErrorInvalidValue;
+    const int hd = d / H;
+    if (!attention_img_supported(hd) || d != hd * H) return hipErrorInvalidValue;
+    const float inv_scale = 1.0f / sqrtf((float)hd);
+    // query blocks and key split as in launch_attention
+    const char *qe = getenv("CIH_ATT_QB");
+    bool wide = (long)((sm.S_max + 255) / 256) * H * sm.B >= 512;
+    if (qe && !strcmp(qe, "128")) wide = false;
+    if (qe && !strcmp(qe, "256")) wide = true;
+    const int QB = wide ? 256 : 128, nq = (sm.S_max + QB - 1) / QB;
+    const int tasks = sm.B * H * nq;
+    int nfull = tasks, nsplit = 1;
+    const char *se = getenv("CIH_ATT_SPLIT"), *ke = getenv("CIH_SPLITK");
+    const bool split_ok = !P && part && !(se && !strcmp(se, "0")) && !(ke && !strcmp(ke, "0"));
+    const int slots = 2 * device_cus() * (wide ? 1 : 2);
+    if (split_ok && tasks < slots) {
+        int ns = std::min(slots / tasks, (sm.S_max + 31) / 32 / 2);
+        while (ns > 1 && (size_t)tasks * ns * QB * (hd + 2) > part_floats) ns--;
+        if (ns > 1) {
+            nfull = 0;
+            nsplit = ns;
+        }
+    }
+    const int grid = nfull + (tasks - nfull) * nsplit;
+#define CIH_ATI(HDV, ONE, NTH)                                                                                   \
+    hipLaunchKernelGGL((k_attention_img<HDV, ONE, NTH>), dim3(grid), dim3(NTH), 0, st, qkv, d, sm.cu, sm.lens,    \
+                       sm.S_max, tb, img, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph,      \
+                       inv_scale, rowsum, H, nq, nfull, nsplit, part)
+#define CIH_ATI_HD(HDV)                                                                                          \
+    if (P && wide) CIH_ATI(HDV, false, 512);                                                                      \
+    else if (P) CIH_ATI(HDV, false, 256);                                                                         \
+    else if (wide) CIH_ATI(HDV, true, 512);                                                                       \
+    else CIH_ATI(HDV, true, 256);                                                                                 \
+    if (nsplit > 1) {                                                                                             \
+        const long n = (long)(tasks - nfull) * QB * (HDV / 4);                                                    \
+        hipLaunchKernelGGL((k_attention_merge<HDV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part,   \
+                           tasks - nfull, nsplit, nfull, H, nq, QB, sm.cu, sm.lens, d, out, out_fmt);             \
+    }
+    switch (hd) {
+    case 16: CIH_ATI_HD(16) break;
+    case 32: CIH_ATI_HD(32) break;
+    case 64: CIH_ATI_HD(64) break;
+    default: return hipErrorInvalidValue;
+    }
+#undef CIH_ATI_HD
+#undef CIH_ATI
     return hipGetLastError();
 }
 

@@ -28,7 +28,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "kernels.h"
+#include "kv_image.h"
 #include "x3.h"
 
 namespace cih {
@@ -59,14 +63,241 @@ template <int RT, int CT, int WM, int WN> struct LdsTile {
     static_assert(BN % NW == 0 && SL <= 64 && OCC * 3 * STAGE <= 160 * 1024, "tile");
 };
 
+// f(integral_constant<int, I>) for each I of the sequence, in order
+template <int... Is, class F>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, Is...>, F &&f) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+
+// Epilogue of the QKV projection when attention reads K/V tile images
+// (kv_image.h).  acc holds v = x.W^T + b; lane (li, hh) of wave (wm, wn) has
+// column n0 + (wn CT + c) 32 + li and rows m0 + (wm RT + r) 32 + 8g + 4hh + e
+// (register q = 4g + e).  Q columns ([0, d)) are stored as FP32 like
+// EPI_NONE.  A K column (dim j of head h) is rotated with its partner dim
+// j +- HD/2 by rot_lo / rot_hi (kv_image.h), as attention's prep kernel
+// rotates, and split into f16 limbs (hi = f16(r), lo = f16(r - hi)); a V
+// column is split.  The partner is the neighbouring column tile (hd 64;
+// through LDS when the two tiles belong to different waves) or lane
+// li ^ HD/2 (hd 32, 16).  Each 32 x 32 tile of limbs is rearranged in a
+// wave-private LDS patch into the image's 128-byte lines (a key's 32 dims of
+// both limbs, or a dim's 32 keys of both limbs) and stored a whole line per 8
+// lanes.  V goes this way when the 32 rows are exactly one key tile, element
+// by element otherwise (a sequence starting inside the 32 rows).
+template <int HD, int RT, int CT, int WM, int WN, bool PREF>
+__device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned char *lds, const unsigned char *pre,
+                                             int m0, int n0, int wm, int wn, int lane, int M, int N,
+                                             float *__restrict__ Y, int ldy, const QkvOut &qo) {
+    using I = KvImg<HD>;
+    constexpr int HALF = HD / 2, BM = WM * RT * 32;
+    // per-row data: from the LDS copy (PREF: [BM] pk, [BM] pos, [2][BM][HALF] cos / sin) or from memory
+    const int *s_pk = reinterpret_cast<const int *>(pre);
+    const float *s_rope = reinterpret_cast<const float *>(pre + BM * 8);
+    auto pk_of = [&](int row) __attribute__((always_inline)) { return PREF ? s_pk[row - m0] : qo.pk[row]; };
+    static_assert(HD != 64 || CT % 2 == 0 || WN == 2, "hd-64 column pairs: within a wave or across two waves");
+    const int li = lane & 31, hh = lane >> 5, d = qo.d;
+    // hd 64 with an odd number of column tiles per wave: wave wn = 0 holds dims
+    // 0..31 of the head its last tile starts, wave 1 dims 32..63 in its first
+    float xpart[RT][16];
+    if constexpr (HD == 64 && CT % 2 == 1) {
+        float *xch = reinterpret_cast<float *>(lds);
+        const int mine = wn == 0 ? CT - 1 : 0;
+        const int col0 = n0 + (wn * CT + mine) * 32;
+        const bool kcol = col0 >= d && col0 < 2 * d;
+        __syncthreads();  // every wave is done with the operand stages
+        if (kcol)
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    xch[(((wn * WM + wm) * RT + r) * 16 + q) * 64 + lane] = wn == 0 ? acc[r][CT - 1][q] : acc[r][0][q];
+        __syncthreads();
+        if (kcol)
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) xpart[r][q] = xch[((((1 - wn) * WM + wm) * RT + r) * 16 + q) * 64 + lane];
+    }
+    const bool has_k = n0 + (wn * CT + CT) * 32 > d && n0 + wn * CT * 32 < 2 * d;  // this wave has K columns
+    constexpr int PP = 144;  // bytes per patch row: 128 + 16 (spreads the rows over the banks)
+    if constexpr (!(HD == 64 && CT % 2 == 1)) __syncthreads();  // every wave is done with the operand stages
+    unsigned char *patch = lds + (HD == 64 && CT % 2 == 1 ? 2 * WM * RT * 16 * 64 * 4 : 0) + (wm * WN + wn) * 32 * PP;
+    // P = parity of wn CT: hd-64 partner tiles are compile-time indices (ct ^ 1)
+    auto tiles = [&](auto P) __attribute__((always_inline)) {
+        constexpr int PAR = decltype(P)::value;
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const int row0 = m0 + (wm * RT + r) * 32;
+            // this lane's rows: padded key index and position
+            int pk[16], pos[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int row = row0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                pk[q] = row < M ? pk_of(row) : -1;
+                pos[q] = PREF || !(row < M && has_k) ? 0 : qo.pos[row];
+            }
+            // the 32 rows are one whole key tile (slots 0..31 in order)
+            const bool tile_rows = row0 + 31 < M && (pk_of(row0) & 31) == 0 && pk_of(row0 + 31) == pk_of(row0) + 31;
+            static_for(std::make_integer_sequence<int, CT>{}, [&](auto C) __attribute__((always_inline)) {
+                constexpr int c = decltype(C)::value;
+                const int ct = wn * CT + c;  // column tile within the workgroup
+                const int col0 = n0 + ct * 32, col = col0 + li;
+                if (col0 >= N) return;
+                if (col0 < d) {  // Q: FP32 rows
+#pragma unroll
+                    for (int q = 0; q < 16; q++) {
+                        const int row = row0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                        if (row < M) Y[(size_t)row * ldy + col] = acc[r][c][q];
+                    }
+                    return;
+                }
+                const bool is_k = col0 < 2 * d;
+                const int hc = col - (is_k ? d : 2 * d);
+                const int h = hc / HD, j = hc % HD;
+                float v[16];
+#pragma unroll
+                for (int q = 0; q < 16; q++) v[q] = acc[r][c][q];
+                if (is_k) {
+                    // fma(k_j, cos, -+(k_partner sin)): rot_lo below HD/2, rot_hi above, same rounding
+                    const int jj = j < HALF ? j : j - HALF;
+                    const float sgn = j < HALF ? -1.0f : 1.0f;
+                    constexpr int pc = ((c + PAR) ^ 1) - PAR;  // partner tile in this wave, if in [0, CT)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) {
+                        float vp;
+                        if constexpr (HD == 64) {
+                            if constexpr (pc < 0 || pc >= CT) vp = xpart[r][q];
+                            else vp = acc[r][pc][q];
+                        } else {
+                            vp = __shfl_xor(v[q], HALF);
+                        }
+                        float cs, sn;
+                        if constexpr (PREF) {
+                            const int rw = (wm * RT + r) * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                            cs = s_rope[rw * HALF + jj];
+                            sn = s_rope[(BM + rw) * HALF + jj];
+                        } else {
+                            const size_t t = (size_t)pos[q] * HALF + jj;
+                            cs = qo.rc[t];
+                            sn = qo.rs[t];
+                        }
+                        v[q] = __builtin_fmaf(v[q], cs, sgn * (vp * sn));
+                    }
+                }
+                // limbs, two rows to a register (registers q, q + 1)
+                unsigned hi2[8], lo2[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) hi2[i] = split_pair(v[2 * i], v[2 * i + 1], lo2[i]);
+                // Whole 128-byte image lines go out through the wave's patch (rows of
+                // PP bytes: [limb][32] f16 and 16 bytes of padding), 8 lanes per line.
+                unsigned char *pb = reinterpret_cast<unsigned char *>(patch);
+                // A wave's LDS operations complete in order; the compiler only must not
+                // move patch accesses across this point (a memory fence would also wait
+                // for the global stores in flight).
+                auto wave_sync = [&]() __attribute__((always_inline)) {
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                };
+                if (is_k) {
+                    // patch row = key row of the tile: [limb][32 tile dims]
+#pragma unroll
+                    for (int q = 0; q < 16; q++) {
+                        const int rl = 8 * (q >> 2) + 4 * hh + (q & 3);
+                        *reinterpret_cast<unsigned short *>(pb + rl * PP + li * 2) =
+                            (unsigned short)(hi2[q >> 1] >> (16 * (q & 1)));
+                        *reinterpret_cast<unsigned short *>(pb + rl * PP + 64 + li * 2) =
+                            (unsigned short)(lo2[q >> 1] >> (16 * (q & 1)));
+                    }
+                    wave_sync();
+#pragma unroll
+                    for (int it = 0; it < 4; it++) {
+                        const int rl = it * 8 + (lane >> 3), q = lane & 7, row = row0 + rl;
+                        if (row >= M) continue;
+                        const int p = pk_of(row), slot = p & 31;
+                        unsigned char *base = qo.img + (size_t)(p >> 5) * qo.H * I::TB + slot * I::KRP;
+                        int hdx, src, dst;  // head within the tile's first, patch chunk, line byte offset
+                        if constexpr (HD == 64) {
+                            // tile = group g of one head; physical chunk (g*8 + ls) ^ (slot & 15)
+                            const int g = ((col0 - d) % 64) / 32, ls = q ^ (slot & 7);
+                            hdx = 0;
+                            src = (ls >> 2) * 64 + (ls & 3) * 16;
+                            dst = ((g ^ ((slot >> 3) & 1)) * 8 + q) * 16;
+                        } else if constexpr (HD == 32) {
+                            const int ls = q ^ ((slot ^ (slot >> 1)) & 7);
+                            hdx = 0;
+                            src = (ls >> 2) * 64 + (ls & 3) * 16;
+                            dst = q * 16;
+                        } else {
+                            // two heads of 16 dims: 4 chunks each, [limb][2 chunks]
+                            hdx = q >> 2;
+                            const int ls = (q & 3) ^ ((slot ^ (slot >> 2)) & 3);
+                            src = (ls >> 1) * 64 + hdx * 32 + (ls & 1) * 16;
+                            dst = (q & 3) * 16;
+                        }
+                        const int hk = (col0 - d) / HD + hdx;
+                        *reinterpret_cast<uint4 *>(base + (size_t)hk * I::TB + dst) =
+                            *reinterpret_cast<const uint4 *>(pb + rl * PP + src);
+                    }
+                    wave_sync();
+                    return;
+                }
+                if (tile_rows) {
+                    // patch row = dim of the tile: [limb][32 key positions]; a lane's keys
+                    // 8g + 4hh + {0..3} are positions vpos(8g + 4hh) + {0..3}
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int off = li * PP + I::vpos(8 * g + 4 * hh) * 2;
+                        *reinterpret_cast<uint2 *>(pb + off) = make_uint2(hi2[2 * g], hi2[2 * g + 1]);
+                        *reinterpret_cast<uint2 *>(pb + off + 64) = make_uint2(lo2[2 * g], lo2[2 * g + 1]);
+                    }
+                    wave_sync();
+                    unsigned char *tb0 = qo.img + (size_t)(pk_of(row0) >> 5) * qo.H * I::TB + I::VOFF;
+#pragma unroll
+                    for (int it = 0; it < 4; it++) {
+                        const int dl = it * 8 + (lane >> 3), q = lane & 7;
+                        const int hc2 = col0 - 2 * d + dl, hv = hc2 / HD, jv = hc2 % HD;
+                        const int ls = q ^ ((jv ^ (jv >> 1)) & 7);  // logical chunk: limb * 4 + position / 8
+                        *reinterpret_cast<uint4 *>(tb0 + (size_t)hv * I::TB + jv * 128 + q * 16) =
+                            *reinterpret_cast<const uint4 *>(pb + dl * PP + (ls >> 2) * 64 + (ls & 3) * 16);
+                    }
+                    wave_sync();
+                    return;
+                }
+                // V rows of a tile that starts or ends a sequence: element by element
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int p = pk[q];
+                    if (p < 0) continue;
+                    unsigned char *t = qo.img + ((size_t)(p >> 5) * qo.H + h) * I::TB;
+                    *reinterpret_cast<unsigned short *>(t + I::voff(p & 31, j, 0)) =
+                        (unsigned short)(hi2[q >> 1] >> (16 * (q & 1)));
+                    *reinterpret_cast<unsigned short *>(t + I::voff(p & 31, j, 1)) =
+                        (unsigned short)(lo2[q >> 1] >> (16 * (q & 1)));
+                }
+            });
+        }
+    };
+    if constexpr (HD == 64 && CT % 2 == 1) {
+        if (wn & 1) tiles(std::integral_constant<int, 1>{});
+        else tiles(std::integral_constant<int, 0>{});
+    } else {
+        tiles(std::integral_constant<int, 0>{});
+    }
+}
+
 template <int EPI, int RT, int CT, int WM, int WN>
 __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned short *__restrict__ W16, const float *__restrict__ Wsc,
-    const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K) {
+    const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo) {
     using T = LdsTile<RT, CT, WM, WN>;
     constexpr int BM = T::BM, BN = T::BN, NW = T::NW, SA = T::SA, SB = T::SB, STAGE = T::STAGE, NA = T::NA,
                   NB = T::NB, SL = T::SL;
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[3 * STAGE];
+    // QKV epilogue with one workgroup per CU: the rows' padded key indices,
+    // positions and RoPE table rows are fetched into LDS behind the k loop
+    constexpr bool QKV = EPI == EPI_QKV16 || EPI == EPI_QKV32 || EPI == EPI_QKV64;
+    constexpr int QHALF = EPI == EPI_QKV16 ? 8 : (EPI == EPI_QKV32 ? 16 : 32);
+    constexpr bool PREF = QKV && T::OCC == 1;
+    constexpr int XTRA = PREF ? BM * 8 + 2 * BM * QHALF * 4 : 0;
+    static_assert(3 * STAGE + XTRA <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[3 * STAGE + XTRA];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -239,6 +470,25 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     // so every wave issues the same instructions and the counts hold.
     request(0, 0);
     request(min(1, KB - 1), 1);
+    if constexpr (PREF) {
+        int *s_pk = reinterpret_cast<int *>(lds + 3 * STAGE), *s_pos = s_pk + BM;
+        if (tid < BM) {
+            const int row = m0 + tid;
+            s_pk[tid] = row < M ? qo.pk[row] : -1;
+            s_pos[tid] = row < M ? qo.pos[row] : 0;
+        }
+        if (n0 < 2 * qo.d && n0 + BN > qo.d) {  // K columns: cos rows, then sin rows, [2][BM][QHALF]
+            constexpr int CPRR = QHALF / 4, NCH = 2 * BM * CPRR, NJ = NCH / 64;
+            static_assert(NCH % 64 == 0, "whole 1 KiB loads");
+            for (int j = wave; j < NJ; j += NW) {
+                const int c = j * 64 + lane, tbl = c / (BM * CPRR), rem = c % (BM * CPRR);
+                const int row = min(m0 + rem / CPRR, M - 1);
+                const float *src = (tbl ? qo.rs : qo.rc) + (size_t)qo.pos[row] * QHALF + (rem % CPRR) * 4;
+                __builtin_amdgcn_global_load_lds((glb_ptr_t *)src, (lds_ptr_t *)(lds + 3 * STAGE + BM * 8 + j * 1024),
+                                                 16, 0, 0);
+            }
+        }
+    }
     for (int kb = 0;;) {
         sync();
         request(min(kb + 2, KB - 1), 2);
@@ -290,6 +540,11 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                 if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
                 acc[r][c][q] = v;
             }
+    if constexpr (EPI == EPI_QKV16 || EPI == EPI_QKV32 || EPI == EPI_QKV64) {
+        qkv_epilogue<EPI == EPI_QKV16 ? 16 : (EPI == EPI_QKV32 ? 32 : 64), RT, CT, WM, WN, PREF>(
+            acc, lds, lds + 3 * STAGE, m0, n0, wm, wn, lane, M, N, reinterpret_cast<float *>(Yv), ldy, qo);
+        return;
+    }
     auto store = [&](bool guard) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < CT; c++) {
@@ -335,11 +590,12 @@ __global__ __launch_bounds__(256) void k_expand_f16(const unsigned char *__restr
 }
 
 template <int EPI, int RT, int CT, int WM, int WN>
-hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
+hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
+                    const QkvOut &qo) {
     using T = LdsTile<RT, CT, WM, WN>;
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
     hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN>), dim3(tiles), dim3(T::THREADS), 0, st,
-                       reinterpret_cast<const unsigned short *>(X), W.q16, W.sc, bias, Y, ldy, M, W.N, W.K);
+                       reinterpret_cast<const unsigned short *>(X), W.q16, W.sc, bias, Y, ldy, M, W.N, W.K, qo);
     return hipGetLastError();
 }
 
@@ -377,14 +633,17 @@ int tile_choice(int M, int N) {
 }
 
 template <int EPI>
-hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st) {
+hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
+                      const QkvOut &qo) {
     const char *e = getenv("CIH_GEMM_TILE_N");
     if (const char *eg = getenv("CIH_GEMM_TILE_N_GELU"); eg && EPI == EPI_GELU_H2) e = eg;
     const int bn = e ? atoi(e) : tile_choice(M, W.N);
-    if (bn == 320) return launch_t<EPI, 1, 5, 4, 2>(W, X, bias, Y, ldy, M, st);
-    if (bn == 256) return launch_t<EPI, 2, 2, 2, 4>(W, X, bias, Y, ldy, M, st);
-    if (bn == 160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st);
-    return launch_t<EPI, 2, 2, 2, 2>(W, X, bias, Y, ldy, M, st);
+    if (bn == 320) return launch_t<EPI, 1, 5, 4, 2>(W, X, bias, Y, ldy, M, st, qo);
+    if (bn == 256) return launch_t<EPI, 2, 2, 2, 4>(W, X, bias, Y, ldy, M, st, qo);
+    if constexpr (EPI < EPI_QKV16) {  // 160-column tiles would split heads between workgroups
+        if (bn == 160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st, qo);
+    }
+    return launch_t<EPI, 2, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
 }
 
 }  // namespace
@@ -412,13 +671,22 @@ bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi) {
 }
 
 hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
-                           hipStream_t st) {
+                           hipStream_t st, const QkvOut *qo) {
     if (!W.q16 || W.K % 32 || W.K <= 0 || M <= 0 || W.N <= 0) return hipErrorInvalidValue;
     if (epi == EPI_GELU_H2 && W.N % 32) return hipErrorInvalidValue;
+    if (epi >= EPI_QKV16) {
+        const int hd = epi == EPI_QKV16 ? 16 : (epi == EPI_QKV32 ? 32 : 64);
+        if (!qo || !qo->img || !qo->pk || !qo->pos || qo->d <= 0 || qo->d % 32 || W.N != 3 * qo->d ||
+            qo->d != qo->H * hd)
+            return hipErrorInvalidValue;
+    }
     switch (epi) {
-    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st);
-    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st);
-    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st);
+    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st, QkvOut());
+    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st, QkvOut());
+    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st, QkvOut());
+    case EPI_QKV16: return launch_epi<EPI_QKV16>(W, X, bias, Y, ldy, M, st, *qo);
+    case EPI_QKV32: return launch_epi<EPI_QKV32>(W, X, bias, Y, ldy, M, st, *qo);
+    case EPI_QKV64: return launch_epi<EPI_QKV64>(W, X, bias, Y, ldy, M, st, *qo);
     default: return hipErrorInvalidValue;
     }
 }

@@ -17,7 +17,29 @@ enum WFmt { WF_F32 = 0, WF_Q8 = 1, WF_Q4 = 2 };
 
 // GEMM epilogue applied to v = acc + bias[n]; EPI_GELU_X3 / EPI_GELU_H2 write
 // gelu(v) in the limb formats of x3.h (for the next quantized GEMM).
-enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_GELU_X3 = 3, EPI_GELU_H2 = 4 };
+// EPI_QKV16/32/64 (LDS GEMM only): the QKV projection of heads of 16/32/64
+// dims; Q columns go to Y as FP32, K (rotated) and V columns to the tile
+// images of kv_image.h described by a QkvOut.
+enum Epi {
+    EPI_NONE = 0,
+    EPI_GELU = 1,
+    EPI_RESIDUAL = 2,
+    EPI_GELU_X3 = 3,
+    EPI_GELU_H2 = 4,
+    EPI_QKV16 = 5,
+    EPI_QKV32 = 6,
+    EPI_QKV64 = 7
+};
+
+// Destination of the K/V columns of an EPI_QKV* projection.
+struct QkvOut {
+    const int *pk = nullptr;   // [T] padded key index of each packed token: 32 * tile row + slot
+    const float *rc = nullptr; // RoPE cos / sin tables [max_len][hd/2]
+    const float *rs = nullptr;
+    const int *pos = nullptr;  // [T] position of each token in its sequence
+    unsigned char *img = nullptr;
+    int d = 0, H = 0;
+};
 
 // erf_f32 (src/lib.rs:3485-3491, Abramowitz & Stegun 7.1.26, |error| <= 1.5e-7)
 // and gelu(x) = 0.5 x (1 + erf(x / sqrt 2)) (src/lib.rs:3493-3498).  Same
@@ -117,7 +139,7 @@ hipError_t launch_gemv_partials(const DevMatrix &W, const float *X, int ldx, int
 // CIH_GEMM_LDS=0 never, =force whenever the formats allow.
 bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi);
 hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
-                           hipStream_t st);
+                           hipStream_t st, const QkvOut *qo = nullptr);
 // W.q16 from W.q (quantized W, k-block-major), on stream st.
 hipError_t launch_expand_f16(const DevMatrix &W, unsigned short *q16, hipStream_t st);
 
@@ -181,6 +203,26 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
                             const float *rope_sin, void *out, int out_fmt, float *P, int64_t pb, int64_t ph,
                             float *rowsum, float *part, size_t part_floats, hipStream_t st);
 size_t attention_part_floats(int hd);
+
+// The same attention with K and V taken from the tile images of kv_image.h
+// (written by an EPI_QKV* projection; Q still from qkv's Q columns).  tb: [B]
+// first tile row of each sequence.  hd 16, 32 or 64.
+hipError_t launch_attention_img(const float *qkv, int d, int H, SeqMeta sm, const int *tb, const unsigned char *img,
+                                const float *rope_cos, const float *rope_sin, void *out, int out_fmt, float *P,
+                                int64_t pb, int64_t ph, float *rowsum, float *part, size_t part_floats, hipStream_t st);
+
+// Per-forward set-up of the tile images: tb[b] = first tile row of sequence
+// b, pk / pos of every packed token, and the padding keys of each sequence's
+// last tile zeroed in every head's image (so masked keys multiply finite
+// zeros).  Tile rows used: kv_tile_rows(lens).
+hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos, unsigned char *img, hipStream_t st);
+// Tile images from FP32 Q|K|V rows (any projection), tile_rows = sum over
+// sequences of ceil(len / 32); after launch_kv_setup.  Same bytes as the
+// EPI_QKV* epilogue.
+hipError_t launch_kv_prep(const float *qkv, int d, int H, SeqMeta sm, const int *tb, int tile_rows, const float *rope_cos,
+                          const float *rope_sin, unsigned char *img, hipStream_t st);
+bool attention_img_supported(int hd);
+size_t kv_image_bytes(int hd);  // bytes of one (tile row, head) image
 
 // final_att[b][p][t] = sum_h P_h[p][t] * (1/H), h ascending
 hipError_t launch_head_mean(const float *P, int64_t pb, int64_t ph, int H, SeqMeta sm, float *final_att,

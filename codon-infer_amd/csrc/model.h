@@ -52,6 +52,9 @@ struct Workspace {
     PartialBuf part;                                    // partial sums of k-split GEMMs / GEMVs
     float *attp = nullptr;                              // partial results of key-split attention
     size_t attp_floats = 0;
+    // K/V tile images (kv_image.h) written by the QKV projection's epilogue
+    unsigned char *kv_img = nullptr;
+    int *kv_tb = nullptr, *kv_pk = nullptr, *kv_pos = nullptr;  // [maxB], [T], [T]
     int *dms_meta = nullptr;                            // [max(maxB, maxS)][2] scored row, wild type
     float *dms_out = nullptr;                           // [max(maxB, maxS)][21] deltas, entropy
     // device staging of outputs for host-pointer calls (padded layouts)
