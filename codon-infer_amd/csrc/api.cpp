@@ -368,15 +368,19 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     // attention itself).  Needs the LDS GEMM for the projection and the
     // f16-limb attention.
     // Other projections (GEMV, register-staged GEMMs, FP32 weights) write FP32
-    // rows and a prep kernel builds the same images from them, so that every
-    // batch shape runs the same attention kernel on the same bytes.
+    // rows; from 2048 tokens on a prep kernel builds the same images from them,
+    // below that attention stages K/V itself (one launch less).  All paths
+    // give the same bits, so results do not depend on the batch they are in.
+    // CIH_ATT_IMG=prep: images by the prep kernel at any size.
     bool use_img = false, epi_img = false;
     int tile_rows = 0;
     {
         const char *ie = getenv("CIH_ATT_IMG"), *ae = getenv("CIH_ATT");
+        const bool prep_only = ie && !std::strcmp(ie, "prep");
         use_img = ws.kv_img && L > 0 && !(ie && !std::strcmp(ie, "0")) && !(ae && !std::strcmp(ae, "fp32")) &&
                   !full_range_mode() && attention_img_supported((int)m->hd);
-        epi_img = use_img && af == AF_H2 && gemm_lds_applies(m->layers[0].wqkv, af, T, EPI_NONE);
+        epi_img = use_img && !prep_only && af == AF_H2 && gemm_lds_applies(m->layers[0].wqkv, af, T, EPI_NONE);
+        if (!epi_img && !prep_only && T < 2048) use_img = false;
         for (int b = 0; b < B; b++) tile_rows += (lens[b] + 31) / 32;
     }
     const int epi_qkv = m->hd == 16 ? EPI_QKV16 : (m->hd == 32 ? EPI_QKV32 : EPI_QKV64);

@@ -180,7 +180,7 @@ __device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned cha
                             cs = qo.rc[t];
                             sn = qo.rs[t];
                         }
-                        v[q] = __builtin_fmaf(v[q], cs, sgn * (vp * sn));
+                        v[q] = opaque(__builtin_fmaf(v[q], cs, sgn * (vp * sn)));
                     }
                 }
                 // limbs, two rows to a register (registers q, q + 1)

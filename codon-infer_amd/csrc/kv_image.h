@@ -36,8 +36,15 @@ namespace cih {
 // attention (staged or from images), so that all of them give the same bits:
 //   lower dim j:       fma(x_j, cos, -(x_{j+hd/2} sin))
 //   upper dim j+hd/2:  fma(x_{j+hd/2}, cos, x_j sin)
-__device__ __forceinline__ float rot_lo(float x, float xp, float c, float s) { return __builtin_fmaf(x, c, -(xp * s)); }
-__device__ __forceinline__ float rot_hi(float x, float xp, float c, float s) { return __builtin_fmaf(x, c, xp * s); }
+// The result passes an empty asm so that the compiler cannot fuse the FMA with
+// a following f16 conversion (v_fma_mix rounds once, from the exact value, and
+// so can round a tie differently from f16(f32 result)).
+__device__ __forceinline__ float opaque(float r) {
+    asm("" : "+v"(r));
+    return r;
+}
+__device__ __forceinline__ float rot_lo(float x, float xp, float c, float s) { return opaque(__builtin_fmaf(x, c, -(xp * s))); }
+__device__ __forceinline__ float rot_hi(float x, float xp, float c, float s) { return opaque(__builtin_fmaf(x, c, xp * s)); }
 
 // hi = f16(v), lo = f16(v - hi) for a pair of floats, packed two f16 to a
 // register: one v_cvt_pk_f16_f32 and two v_fma_mix (lo = f16(fma(hi, -1, v));
