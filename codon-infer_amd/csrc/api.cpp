@@ -40,7 +40,7 @@ std::string kernel_switches() {
     static const char *const names[] = {"CIH_ATT",     "CIH_ATT_QB", "CIH_ATT_SPLIT", "CIH_SPLITK",
                                         "CIH_QGEMM",   "CIH_ACT",    "CIH_LIMBS",     "CIH_GEMV",
                                         "CIH_GEMV_NB", "CIH_GEMM_LDS", "CIH_GEMM_TILE", "CIH_GEMM_TILE_N",
-                                        "CIH_GEMM_TILE_N_GELU", "CIH_ATT_IMG"};
+                                        "CIH_GEMM_TILE_N_GELU", "CIH_ATT_IMG", "CIH_GEMV16", "CIH_GEMV16_KW"};
     std::string s = g_full_range ? "R|" : "|";
     for (const char *n : names) {
         const char *v = getenv(n);
@@ -131,6 +131,8 @@ hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, co
     ProfScope ps(m, W.fmt == WF_F32 ? CIH_KC_GEMM_FP32 : CIH_KC_GEMM_QUANT, flops, bytes);
     if (use_gemv(M, a_fmt, epi))
         return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, pb, m->stream);
+    if (gemv16_applies(W, a_fmt, M, epi))
+        return launch_gemv16(W, (const unsigned short *)X, M, bias, Y, ldy, epi, &pb, m->stream);
     return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, &pb, m->stream);
 }
 
@@ -350,7 +352,8 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     // FP32, no conversion in the GEMM).  CIH_ACT=f32 hands over FP32 (split in
     // the GEMM), CIH_ACT=x3 the three-limb bf16 form; CIH_LIMBS=bf16x3 and
     // CIH_QGEMM=fp32 imply FP32 hand-off.  Batches of at most GEMV_MAX_M
-    // tokens take the GEMV, which reads FP32.
+    // tokens take the f16-MFMA GEMV (k_gemv16), which reads limbs too; with
+    // any of those switches, CIH_GEMV16=0 or in full range the FP32 GEMV.
     int af = AF_F32;
     {
         const char *qpath = getenv("CIH_QGEMM"), *apath = getenv("CIH_ACT"), *lpath = getenv("CIH_LIMBS");
@@ -359,9 +362,27 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         if (m->dtype != DT_FP32 && !fp32_gemm && T > GEMV_MAX_M) {
             if ((apath && !std::strcmp(apath, "x3")) || full_range_mode()) af = AF_X3;
             else if (!(apath && !std::strcmp(apath, "f32")) && !bf16) af = AF_H2;
+        } else if (m->dtype != DT_FP32 && !fp32_gemm && !apath && !bf16 && !full_range_mode() && L > 0 &&
+                   gemv16_applies(m->layers[0].wqkv, AF_H2, T, EPI_NONE) &&
+                   gemv16_applies(m->layers[0].wo, AF_H2, T, EPI_NONE) &&
+                   gemv16_applies(m->layers[0].w1, AF_H2, T, EPI_NONE) &&
+                   gemv16_applies(m->layers[0].w2, AF_H2, T, EPI_NONE) && d % 32 == 0 && F % 32 == 0) {
+            af = AF_H2;  // few tokens: the f16-MFMA GEMV (k_gemv16) reads limbs
         }
     }
     const int epi_fc1 = af == AF_X3 ? EPI_GELU_X3 : (af == AF_H2 ? EPI_GELU_H2 : EPI_GELU);
+    // Few tokens (af == AF_H2 at T <= GEMV_MAX_M: the f16-MFMA GEMV): each
+    // projection leaves split-K partial sums in one half of the partial
+    // buffer, and the kernel after it adds them (attention: the QKV splits;
+    // the residual LayerNorm: Wo's, and FC2's of the layer before; FC2: FC1's,
+    // with bias and GELU), so a layer is LN, QKV, attention, Wo, LN, FC1, FC2
+    // with no separate reductions.  FC2's splits stay pending until the next
+    // LayerNorm (or a per-layer hidden-state export).
+    const bool few = af == AF_H2 && T <= GEMV_MAX_M;
+    const size_t part_half = ws.part.floats / 2 / 64 * 64;
+    float *const part_a = ws.part.part, *const part_b = ws.part.part + part_half;
+    int pend_splits = 0;  // FC2 splits waiting in part_a
+    const float *pend_bias = nullptr;
     // K/V tile images: the QKV projection's epilogue rotates K, splits K and V
     // into f16 limbs and lays them out as attention's LDS tiles, once per
     // key; attention copies them (CIH_ATT_IMG=0: K/V as FP32 rows, staged by
@@ -413,6 +434,86 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
 
     for (int l = 0; l < L; l++) {
         const Layer &ly = m->layers[l];
+        // probabilities: straight into the attention-map output when exported
+        float *P = nullptr;
+        int64_t pb = 0, ph = SS;
+        const bool need_P = want_attn || want_contacts || (want_final && l == L - 1);
+        if (want_attn) {
+            P = t_attn + (size_t)l * H * SS;
+            pb = (int64_t)L * H * SS;
+        } else if (need_P) {
+            P = ws.P;
+            pb = (int64_t)H * SS;
+        }
+        if (few) {
+            {
+                ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
+                HIPCHK(launch_residual_layernorm(ws.x, pend_splits ? part_a : nullptr, pend_splits, pend_bias,
+                                                 ly.ln1w, ly.ln1b, ws.xb, AF_H2, T, d, st));
+            }
+            int sq = 0;
+            {
+                ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * T * ly.wqkv.N * ly.wqkv.K,
+                             wbytes(ly.wqkv) + 4.0 * T * d + 4.0 * T * 3 * d);
+                HIPCHK(launch_gemv16_partials(ly.wqkv, (const unsigned short *)ws.xb, T, part_b, part_half, &sq, st));
+            }
+            if (!need_P && m->hd % 8 == 0 && m->hd <= FEW_MAX_HD) {
+                double fl = 0;
+                for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
+                ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
+                HIPCHK(launch_attention_few(part_b, sq, T, ly.bqkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, AF_H2, st));
+            } else {
+                {
+                    ProfScope ps(m, CIH_KC_OTHER, 0, 4.0 * sq * T * 3 * d);
+                    HIPCHK(launch_gemv16_fold(part_b, sq, T, 3 * d, ly.bqkv, ws.qkv, 3 * d, EPI_NONE, st));
+                }
+                double fl = 0;
+                for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
+                ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
+                float *rsum = want_contacts && m->nz[l] > 0 ? ws.rowsum : nullptr;
+                HIPCHK(launch_attention(ws.qkv, d, H, sm, ws.rope_c, ws.rope_s, ws.ao, af, P, pb, ph, rsum, ws.attp,
+                                        ws.attp_floats, st));
+            }
+            if (want_contacts && m->nz[l] > 0) {
+                ProfScope ps(m, CIH_KC_OTHER, 0, 0);
+                HIPCHK(launch_apc_layer(P, pb, ph, H, l, m->d_contact_w, m->d_heads + (size_t)l * H, m->nz[l], sm,
+                                        ws.rowsum, ws.colpart, ws.M, ws.r, st));
+            }
+            if (want_final && l == L - 1) {
+                ProfScope ps(m, CIH_KC_OTHER, 0, 0);
+                HIPCHK(launch_head_mean(P, pb, ph, H, sm, t_final, st));
+            }
+            int so = 0, s1 = 0, s2 = 0;
+            {
+                ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * T * ly.wo.N * ly.wo.K, wbytes(ly.wo) + 8.0 * T * d);
+                HIPCHK(launch_gemv16_partials(ly.wo, (const unsigned short *)ws.ao, T, part_a, part_half, &so, st));
+            }
+            {
+                ProfScope ps(m, CIH_KC_OTHER, 0, 4.0 * so * T * d + 12.0 * T * d);
+                HIPCHK(launch_residual_layernorm(ws.x, part_a, so, ly.bo, ly.ln2w, ly.ln2b, ws.xb, AF_H2, T, d, st));
+            }
+            {
+                ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * T * ly.w1.N * ly.w1.K, wbytes(ly.w1) + 4.0 * T * (d + F));
+                HIPCHK(launch_gemv16_partials(ly.w1, (const unsigned short *)ws.xb, T, part_b, part_half, &s1, st));
+            }
+            {
+                // FC2 forms GELU(FC1 + b1) from FC1's splits while staging its operand
+                ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * T * ly.w2.N * ly.w2.K,
+                             wbytes(ly.w2) + 4.0 * s1 * T * F + 4.0 * T * d);
+                HIPCHK(launch_gemv16_gelu_partials(ly.w2, part_b, s1, ly.b1, T, part_a, part_half, &s2, st));
+            }
+            pend_splits = s2;
+            pend_bias = ly.b2;
+            if (want_layer) {
+                {
+                    ProfScope ps(m, CIH_KC_OTHER, 0, 4.0 * s2 * T * d + 8.0 * T * d);
+                    HIPCHK(launch_gemv16_fold(part_a, s2, T, d, ly.b2, ws.x, d, EPI_RESIDUAL, st));
+                }
+                pend_splits = 0;
+                HIPCHK(launch_scatter_rows(ws.x, d, sm, t_layer + (size_t)l * S_max * d, (int64_t)L * S_max * d, st));
+            }
+            continue;
+        }
         {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
             HIPCHK(launch_layernorm(ws.x, ly.ln1w, ly.ln1b, ws.xb, af, T, d, st));
@@ -427,17 +528,6 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
                 ProfScope ps(m, CIH_KC_OTHER, 0, 16.0 * T * d);
                 HIPCHK(launch_kv_prep(ws.qkv, d, H, sm, ws.kv_tb, tile_rows, ws.rope_c, ws.rope_s, ws.kv_img, st));
             }
-        }
-        // probabilities: straight into the attention-map output when exported
-        float *P = nullptr;
-        int64_t pb = 0, ph = SS;
-        const bool need_P = want_attn || want_contacts || (want_final && l == L - 1);
-        if (want_attn) {
-            P = t_attn + (size_t)l * H * SS;
-            pb = (int64_t)L * H * SS;
-        } else if (need_P) {
-            P = ws.P;
-            pb = (int64_t)H * SS;
         }
         {
             double fl = 0;
@@ -478,7 +568,11 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     // |x| < 65504 only, and an overflow there makes the residual non-finite.
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-        HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, AF_F32, T, d, st, ws.flag));
+        if (pend_splits)
+            HIPCHK(launch_residual_layernorm(ws.x, part_a, pend_splits, pend_bias, m->lnfw, m->lnfb, ws.ao, AF_F32, T,
+                                             d, st, ws.flag));
+        else
+            HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, AF_F32, T, d, st, ws.flag));
     }
     if (want_hidden) HIPCHK(launch_scatter_rows(ws.ao, d, sm, t_hidden, (int64_t)S_max * d, st));
     if (want_logits || keep_logits) {
@@ -709,12 +803,20 @@ int cih_matmul_tiled(int32_t dtype, float *out, const float *x, const void *w, c
     if (!rc && dalloc(dy, (size_t)seq_len * out_dim, tmp.allocs) != hipSuccess)
         rc = set_error(CIH_ERR_HIP, "allocation failed");
     PartialBuf gs;
+    // a few rows of quantized weights: limbs (in the partial-sum buffer) and the f16-MFMA GEMV
+    const bool g16 = dtype != DT_FP32 && gemv16_applies(tmp.emb, AF_H2, seq_len, EPI_NONE);
     const bool gv = use_gemv(seq_len, AF_F32, EPI_NONE);
-    gs.floats = std::max(gemv_part_floats(out_dim, in_dim), SPLITK_PART_FLOATS);
+    gs.floats = std::max({gemv_part_floats(out_dim, in_dim), SPLITK_PART_FLOATS, (size_t)seq_len * in_dim});
     if (!rc && dalloc(gs.part, gs.floats, tmp.allocs) != hipSuccess) rc = set_error(CIH_ERR_HIP, "allocation failed");
     if (!rc) {
-        hipError_t e = gv ? launch_gemv(tmp.emb, dx, in_dim, seq_len, db, dy, out_dim, EPI_NONE, gs, nullptr)
-                          : launch_gemm(tmp.emb, dx, in_dim, AF_F32, db, dy, out_dim, seq_len, EPI_NONE, &gs, nullptr);
+        unsigned short *xh = reinterpret_cast<unsigned short *>(gs.part);
+        hipError_t e = g16   ? launch_to_h2(dx, seq_len, in_dim, xh, nullptr)
+                       : gv  ? launch_gemv(tmp.emb, dx, in_dim, seq_len, db, dy, out_dim, EPI_NONE, gs, nullptr)
+                             : launch_gemm(tmp.emb, dx, in_dim, AF_F32, db, dy, out_dim, seq_len, EPI_NONE, &gs, nullptr);
+        if (g16 && e == hipSuccess) {
+            PartialBuf rest{gs.part + (size_t)seq_len * in_dim, gs.floats - (size_t)seq_len * in_dim};
+            e = launch_gemv16(tmp.emb, xh, seq_len, db, dy, out_dim, EPI_NONE, &rest, nullptr);
+        }
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e == hipSuccess) e = hipMemcpy(out, dy, (size_t)seq_len * out_dim * 4, hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = set_error(CIH_ERR_HIP, "GEMM failed: %s", hipGetErrorString(e));

@@ -1,0 +1,265 @@
+// Kernels of the few-token forward (at most GEMV_MAX_M tokens in the batch),
+// which consume the split-K partial sums of the f16-MFMA GEMV (k_gemv16)
+// themselves instead of a separate reduction:
+//
+//   k_rln       residual + LayerNorm: x += bias + (sum of the splits of the
+//               previous projection), then out = LN(x) (the projection's
+//               residual epilogue and layer_norm, lib.rs:2556-2562)
+//   k_attn_few  the QKV splits + bias, RoPE, scores, softmax and P.V of one
+//               (sequence, head) in FP32 (attention of lib.rs:5206-5301 without
+//               a probability export)
+//
+// Partial sums are added in split order (fold_splits), so results do not
+// depend on scheduling.
+#include <cmath>
+
+#include "kernels.h"
+#include "x3.h"
+
+namespace cih {
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int FEW_THREADS = 256;
+constexpr int RLN_MAX_THREADS = 1024;
+
+// sum over the workgroup's waves (added in order); red: one float per wave
+__device__ __forceinline__ float wg_sum(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();  // red free from a previous use
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    float r = red[0];
+    for (int i = 1; i < nw; i++) r += red[i];
+    return r;
+}
+
+}  // namespace
+
+// One workgroup per row; thread t owns column quads t, t + blockDim, ... (Q of
+// them), so that every partial sum of a row is requested at once.  part (may
+// be null): [S][rows][d] partial sums of the projection whose residual is
+// added, with bias pb.
+template <int Q, int OF>
+__global__ __launch_bounds__(RLN_MAX_THREADS) void k_rln(float *__restrict__ x, const float *__restrict__ part, int S,
+                                                         const float *__restrict__ pb, const float *__restrict__ w,
+                                                         const float *__restrict__ b, void *__restrict__ out,
+                                                         int rows, int d, int *__restrict__ flag) {
+    __shared__ float red[RLN_MAX_THREADS / 64];
+    const int row = blockIdx.x, n4 = d >> 2, nt = blockDim.x;
+    f32x4 *xr = reinterpret_cast<f32x4 *>(x + (size_t)row * d);
+    f32x4 v[Q], g[Q], be[Q];
+#pragma unroll
+    for (int i = 0; i < Q; i++) {
+        const int c = min((int)threadIdx.x + nt * i, n4 - 1);  // past the row: re-read, masked below
+        v[i] = xr[c];
+        g[i] = reinterpret_cast<const f32x4 *>(w)[c];
+        be[i] = reinterpret_cast<const f32x4 *>(b)[c];
+    }
+    if (part) {
+        const size_t stride = (size_t)rows * d;
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const int c = min((int)threadIdx.x + nt * i, n4 - 1);
+            const f32x4 acc = fold_splits4(part + (size_t)row * d + 4 * c, S, stride);
+            const f32x4 bb = reinterpret_cast<const f32x4 *>(pb)[c];
+            v[i] = v[i] + (acc + bb);
+            if ((int)threadIdx.x + nt * i < n4) xr[c] = v[i];
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < Q; i++)
+        if ((int)threadIdx.x + nt * i < n4) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float mean = wg_sum(s, red) / (float)d;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < Q; i++) {
+        const f32x4 t = v[i] - mean;
+        if ((int)threadIdx.x + nt * i < n4) q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+    }
+    const float var = wg_sum(q, red) / (float)d;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+    if (flag && threadIdx.x == 0 && !(__builtin_isfinite(mean) && __builtin_isfinite(var)))
+        atomicOr(flag, FLAG_NONFINITE);
+#pragma unroll
+    for (int i = 0; i < Q; i++) {
+        const int c = threadIdx.x + nt * i;
+        if (c >= n4) break;
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+        if constexpr (OF == AF_H2)
+            h2_store4(reinterpret_cast<unsigned short *>(out), row, 4 * c, d, make_float4(y.x, y.y, y.z, y.w));
+        else
+            reinterpret_cast<f32x4 *>(out)[(size_t)row * n4 + c] = y;
+    }
+}
+
+template <int OF>
+static hipError_t launch_rln_t(float *x, const float *part, int S, const float *pbias, const float *w, const float *b,
+                               void *out, int rows, int d, int *flag, hipStream_t st) {
+    const int n4 = d / 4;
+    const int q = (n4 + RLN_MAX_THREADS - 1) / RLN_MAX_THREADS;
+    const int nt = (n4 + q - 1) / q;
+    const dim3 grid(rows), blk((nt + 63) / 64 * 64);
+#define CIH_RLN(QV) hipLaunchKernelGGL((k_rln<QV, OF>), grid, blk, 0, st, x, part, S, pbias, w, b, out, rows, d, flag)
+    if (q <= 1) CIH_RLN(1);
+    else if (q <= 2) CIH_RLN(2);
+    else return hipErrorInvalidValue;
+#undef CIH_RLN
+    return hipGetLastError();
+}
+
+hipError_t launch_residual_layernorm(float *x, const float *part, int S, const float *pbias, const float *w,
+                                     const float *b, void *out, int out_fmt, int rows, int d, hipStream_t st,
+                                     int *flag) {
+    if (rows <= 0) return hipSuccess;
+    if (d % 32 || d > 8 * RLN_MAX_THREADS || (part && (S < 1 || !pbias)) || (out_fmt != AF_H2 && out_fmt != AF_F32))
+        return hipErrorInvalidValue;
+    return out_fmt == AF_H2 ? launch_rln_t<AF_H2>(x, part, S, pbias, w, b, out, rows, d, flag, st)
+                            : launch_rln_t<AF_F32>(x, part, S, pbias, w, b, out, rows, d, flag, st);
+}
+
+// One workgroup per (sequence, head), n <= GEMV_MAX_M tokens.  q, k, v of the
+// head: the QKV splits in order + bias (part: [S][T][3d]); RoPE (apply_rope,
+// lib.rs:3533-3552, products rounded one by one); scores (q . k) / sqrt(hd),
+// softmax (lib.rs:3500-3504: max, exp(s - max), * 1/sum; the row's max and
+// sum over a shuffle tree) and out = P V, all FP32; out in H2 limbs (the Wo
+// GEMV's operand) or FP32.  A thread takes one item of the head's columns of
+// all T rows (nothing waits for the sequence's offset before the loads): a
+// q or k dim-quad pair (4j..4j+3 and its RoPE partners + hd/2), rotated in
+// registers, or a v quad; every split is requested at once, four floats per
+// load, with the bias.
+constexpr int ATTF_THREADS = 512;
+template <int OF>
+__global__ __launch_bounds__(ATTF_THREADS) void k_attn_few(const float *__restrict__ part, int S, int T,
+                                                           const float *__restrict__ bias, int d, int hd,
+                                                           const int *__restrict__ cu, const int *__restrict__ lens,
+                                                           int S_max, const float *__restrict__ rc,
+                                                           const float *__restrict__ rs, float inv_scale,
+                                                           void *__restrict__ out) {
+    constexpr int RW = FEW_MAX_HD + 4;  // padded rows: the 8 key rows of a score read hit distinct banks
+    __shared__ float qkv[3][GEMV_MAX_M][RW];
+    __shared__ float p[GEMV_MAX_M][GEMV_MAX_M];
+    const int b = blockIdx.x, h = blockIdx.y;
+    const int half = hd / 2, hq = hd / 4, pq = hd / 8;  // quads per row, pairs per row
+    const size_t stride = (size_t)T * 3 * d;
+    const int len = lens[b], r0 = cu[b];
+    // items: [0, 2 T pq) q/k pairs (which, row, pair), then T hq v quads
+    const int nqk = 2 * T * pq, nitem = nqk + T * hq;
+    const int it = min((int)threadIdx.x, nitem - 1);  // past the end: re-read, unused
+    const bool pair = it < nqk;
+    int which, r, j;  // j: first dim of the (lower) quad
+    if (pair) {
+        which = it / (T * pq);
+        const int rem = it - which * T * pq;
+        r = rem / pq;
+        j = 4 * (rem - r * pq);
+    } else {
+        which = 2;
+        const int rem = it - nqk;
+        r = rem / hq;
+        j = 4 * (rem - r * hq);
+    }
+    const float *src = part + (size_t)r * 3 * d + which * d + h * hd + j;
+    const int up = pair ? half : 0;  // the partner quad
+    fold4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < S; s0 += FOLD_CHUNK) {
+        fold4_t v0[FOLD_CHUNK], v1[FOLD_CHUNK];
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++) {
+            const bool in = s0 + u < S;
+            v0[u] = in ? *reinterpret_cast<const fold4_t *>(src + (size_t)(s0 + u) * stride) : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            v1[u] = in && pair ? *reinterpret_cast<const fold4_t *>(src + up + (size_t)(s0 + u) * stride)
+                               : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++) {
+            a0 += v0[u];
+            a1 += v1[u];
+        }
+    }
+    const float *bp = bias + which * d + h * hd + j;
+    a0 += *reinterpret_cast<const fold4_t *>(bp);
+    if (pair) a1 += *reinterpret_cast<const fold4_t *>(bp + up);
+    const int n = min(len, GEMV_MAX_M), pos = r - r0;
+    if (pair && pos >= 0 && pos < n) {
+        const fold4_t c = *reinterpret_cast<const fold4_t *>(rc + (size_t)pos * half + j);
+        const fold4_t sn = *reinterpret_cast<const fold4_t *>(rs + (size_t)pos * half + j);
+        fold4_t lo, hi;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            lo[t] = __fsub_rn(__fmul_rn(a0[t], c[t]), __fmul_rn(a1[t], sn[t]));
+            hi[t] = __fadd_rn(__fmul_rn(a1[t], c[t]), __fmul_rn(a0[t], sn[t]));
+        }
+        a0 = lo;
+        a1 = hi;
+    }
+    if ((int)threadIdx.x < nitem) {
+        *reinterpret_cast<fold4_t *>(&qkv[which][r][j]) = a0;
+        if (pair) *reinterpret_cast<fold4_t *>(&qkv[which][r][j + half]) = a1;
+    }
+    if (n <= 0) return;  // uniform: no barrier follows for this workgroup
+    __syncthreads();
+    // scores and softmax: lane 8 i + j of wave 0 holds (query i, key j); a
+    // row's lanes meet through shuffles
+    if (threadIdx.x < 64) {
+        const int i = threadIdx.x >> 3, j = threadIdx.x & 7;
+        const bool live = i < n && j < n;
+        const f32x4 *qr = reinterpret_cast<const f32x4 *>(qkv[0][r0 + min(i, n - 1)]);
+        const f32x4 *kr = reinterpret_cast<const f32x4 *>(qkv[1][r0 + min(j, n - 1)]);
+        float a = 0.0f;
+#pragma unroll 8
+        for (int k = 0; k < hq; k++) {
+            const f32x4 x = qr[k], y = kr[k];
+            a = fmaf(x.x, y.x, a);
+            a = fmaf(x.y, y.y, a);
+            a = fmaf(x.z, y.z, a);
+            a = fmaf(x.w, y.w, a);
+        }
+        const float sc = live ? a * inv_scale : -INFINITY;
+        float mx = sc;
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float e = live ? expf(sc - mx) : 0.0f;
+        float sum = e;
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o);
+        p[i][j] = e * (1.0f / sum);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < n * hd; e += ATTF_THREADS) {
+        const int i = e / hd, j = e - i * hd;
+        float a = 0.0f;
+#pragma unroll
+        for (int t = 0; t < GEMV_MAX_M; t++)
+            if (t < n) a = fmaf(p[i][t], qkv[2][r0 + t][j], a);
+        if constexpr (OF == AF_H2) h2_store(static_cast<unsigned short *>(out), r0 + i, h * hd + j, d, a);
+        else static_cast<float *>(out)[(size_t)(r0 + i) * d + h * hd + j] = a;
+    }
+}
+
+hipError_t launch_attention_few(const float *part, int S, int T, const float *bias, int d, int H, const SeqMeta &sm,
+                                const float *rope_c, const float *rope_s, void *out, int out_fmt, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    const int hd = H > 0 ? d / H : 0;
+    if (T > GEMV_MAX_M || !part || S < 1 || !bias || hd <= 0 || hd * H != d || hd % 8 || hd > FEW_MAX_HD ||
+        (out_fmt == AF_H2 && d % 32) || (out_fmt != AF_H2 && out_fmt != AF_F32))
+        return hipErrorInvalidValue;
+    const float inv_scale = 1.0f / sqrtf((float)hd);
+    const dim3 grid(sm.B, H), blk(ATTF_THREADS);
+    if (out_fmt == AF_H2)
+        hipLaunchKernelGGL(k_attn_few<AF_H2>, grid, blk, 0, st, part, S, T, bias, d, hd, sm.cu, sm.lens, sm.S_max,
+                           rope_c, rope_s, inv_scale, out);
+    else
+        hipLaunchKernelGGL(k_attn_few<AF_F32>, grid, blk, 0, st, part, S, T, bias, d, hd, sm.cu, sm.lens, sm.S_max,
+                           rope_c, rope_s, inv_scale, out);
+    return hipGetLastError();
+}
+
+}  // namespace cih

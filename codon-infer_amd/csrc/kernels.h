@@ -59,6 +59,36 @@ __device__ __forceinline__ float erf_as(float x) {
 }
 __device__ __forceinline__ float gelu_as(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f)); }
 
+// Sum of S partial results p[0], p[stride], ... in split order (twenty loads
+// in flight, then added one by one): the same bits whatever launched the
+// splits.  fold_splits4: the same for four consecutive floats (16-byte loads).
+constexpr int FOLD_CHUNK = 20;
+__device__ __forceinline__ float fold_splits(const float *__restrict__ p, int S, size_t stride) {
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += FOLD_CHUNK) {
+        float v[FOLD_CHUNK];
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++) v[u] = s0 + u < S ? p[(size_t)(s0 + u) * stride] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++) acc += v[u];
+    }
+    return acc;
+}
+typedef float fold4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ fold4_t fold_splits4(const float *__restrict__ p, int S, size_t stride) {
+    fold4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < S; s0 += FOLD_CHUNK) {
+        fold4_t v[FOLD_CHUNK];
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++)
+            v[u] = s0 + u < S ? *reinterpret_cast<const fold4_t *>(p + (size_t)(s0 + u) * stride)
+                              : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++) acc += v[u];
+    }
+    return acc;
+}
+
 struct DevMatrix {
     int fmt = WF_F32;
     int N = 0, K = 0;          // out_dim, in_dim
@@ -131,6 +161,33 @@ hipError_t launch_gemv(const DevMatrix &W, const float *X, int ldx, int M, const
 hipError_t launch_gemv_partials(const DevMatrix &W, const float *X, int ldx, int M, const PartialBuf &pb, int *splits,
                                 hipStream_t st);
 
+// Few-token quantized GEMM on f16 MFMA: X (M <= GEMV_MAX_M rows) in H2 limbs
+// ([M][K/32][64] f16), W Q8_0 / Q4_0 with N % 16 == 0; workgroups of 64
+// columns and kw k-blocks, K split across `splits` workgroups.  CIH_GEMV16=0:
+// gemv16_applies is false.
+bool gemv16_applies(const DevMatrix &W, int a_fmt, int M, int epi);
+struct Gemv16Grid { int kw = 0, splits = 0; };
+constexpr size_t GEMV16_SPLIT_MAX_FLOATS = (size_t)1 << 21;
+Gemv16Grid gemv16_grid(int N, int K);
+// partial sums [*splits][M][N] (no bias) for a consumer that adds them in split order
+hipError_t launch_gemv16_partials(const DevMatrix &W, const unsigned short *X, int M, float *part, size_t part_floats,
+                                  int *splits, hipStream_t st);
+// the same with activations GELU(sum of the aS splits of apart + abias) formed
+// while staging (apart: [aS][M][W.K], the FC1 projection's partial sums)
+hipError_t launch_gemv16_gelu_partials(const DevMatrix &W, const float *apart, int aS, const float *abias, int M,
+                                       float *part, size_t part_floats, int *splits, hipStream_t st);
+// Y = epi(sum of the S splits of part + bias): EPI_NONE / EPI_RESIDUAL / EPI_GELU
+// (FP32 Y, row stride ldy) or EPI_GELU_H2 (Y in H2 limbs, N columns)
+hipError_t launch_gemv16_fold(const float *part, int S, int M, int N, const float *bias, void *Y, int ldy, int epi,
+                              hipStream_t st);
+// the whole GEMM: partials in pb and the fold, or (more than
+// GEMV16_SPLIT_MAX_FLOATS partial sums) one workgroup per 64 columns over the
+// whole K with the epilogue applied there
+hipError_t launch_gemv16(const DevMatrix &W, const unsigned short *X, int M, const float *bias, void *Y, int ldy,
+                         int epi, const PartialBuf *pb, hipStream_t st);
+// FP32 [M][K] (16-byte aligned, K % 32 == 0) -> H2 limbs [M][K/32][64]
+hipError_t launch_to_h2(const float *x, int M, int K, unsigned short *out, hipStream_t st);
+
 // The same GEMM for activations in f16 limbs (AF_H2) and W.q16 present, with
 // operands copied global -> LDS by the load unit (no staging registers).
 // Epilogues EPI_NONE / EPI_RESIDUAL / EPI_GELU_H2.  gemm_lds_applies says
@@ -172,6 +229,19 @@ struct SeqMeta {
 // forward, read after it).
 constexpr int FLAG_BAD_TOKEN = 1;  // a token id outside [0, V) (device-pointer input)
 constexpr int FLAG_NONFINITE = 2;  // a LayerNorm row with a non-finite mean or variance
+
+// Few-token forward (few.hip).  x += pbias + (sum of the S splits of part,
+// [S][rows][d]; part may be null), then out = LayerNorm(x) as FP32 or H2
+// limbs; flag as launch_layernorm.
+hipError_t launch_residual_layernorm(float *x, const float *part, int S, const float *pbias, const float *w,
+                                     const float *b, void *out, int out_fmt, int rows, int d, hipStream_t st,
+                                     int *flag = nullptr);
+// Attention of T <= GEMV_MAX_M packed tokens from the QKV projection's splits
+// (part [S][T][3d]) + bias: RoPE, softmax(q k / sqrt(hd)) v in FP32 per
+// (sequence, head); out [T][d] in FP32 or H2 limbs.  hd % 8 == 0, <= FEW_MAX_HD.
+constexpr int FEW_MAX_HD = 128;
+hipError_t launch_attention_few(const float *part, int S, int T, const float *bias, int d, int H, const SeqMeta &sm,
+                                const float *rope_c, const float *rope_s, void *out, int out_fmt, hipStream_t st);
 
 // Full-range mode: quantized GEMMs take three bf16 limbs and attention the
 // FP32-MFMA kernel, which cover the whole FP32 exponent range (the f16 limbs

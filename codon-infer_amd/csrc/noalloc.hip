@@ -81,11 +81,22 @@ extern "C" int cih_matmul_tiled_noalloc(int32_t dtype, float *out, const float *
     W.sc = dtype == DT_FP32 ? nullptr : reinterpret_cast<const float *>(base + sc_off);
     pb.part = reinterpret_cast<float *>(base + NOALLOC_WEIGHT_BYTES);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool g16 = dtype != DT_FP32 && gemv16_applies(W, AF_H2, seq_len, EPI_NONE);
+    if (g16 && (size_t)seq_len * in_dim * sizeof(float) > NOALLOC_PART_BYTES)
+        return set_error(CIH_ERR_CAPACITY, "%d rows of %d limbs need more than the %zu bytes available", seq_len,
+                         in_dim, NOALLOC_PART_BYTES);
     hipError_t e = launch_load_matrix(static_cast<const uint8_t *>(w), W.fmt, out_dim, W, 0, st);
-    if (e == hipSuccess)
+    if (e == hipSuccess && g16) {
+        // as cih_matmul_tiled: limbs in the partial-sum region, then the f16-MFMA GEMV
+        unsigned short *xh = reinterpret_cast<unsigned short *>(pb.part);
+        e = launch_to_h2(x, seq_len, in_dim, xh, st);
+        PartialBuf rest{pb.part + (size_t)seq_len * in_dim, NOALLOC_PART_BYTES / sizeof(float) - (size_t)seq_len * in_dim};
+        if (e == hipSuccess) e = launch_gemv16(W, xh, seq_len, bias, out, out_dim, EPI_NONE, &rest, st);
+    } else if (e == hipSuccess) {
         e = use_gemv(seq_len, AF_F32, EPI_NONE)
                 ? launch_gemv(W, x, in_dim, seq_len, bias, out, out_dim, EPI_NONE, pb, st)
                 : launch_gemm(W, x, in_dim, AF_F32, bias, out, out_dim, seq_len, EPI_NONE, &pb, st);
+    }
     if (e != hipSuccess) return set_error(CIH_ERR_HIP, "GEMM failed: %s", hipGetErrorString(e));
     return CIH_OK;
 }

@@ -228,14 +228,20 @@ def test_forward_headline_shape(monkeypatch):
     m.close()
 
 
-@pytest.mark.parametrize("gemv", ["on", "off"])
+@pytest.mark.parametrize("gemv", ["on", "fp32", "off"])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
 def test_forward_few_tokens(dtype, gemv, monkeypatch):
-    """Batches of at most 8 tokens in total run every linear layer on the
-    weight-streaming GEMV (CIH_GEMV=0: on the MFMA GEMMs); all outputs, with
-    a <mask>, a sequence with no residues (BOS, EOS) and contacts."""
+    """Batches of at most 8 tokens in total run every layer projection on
+    the few-token f16-MFMA GEMV with limb hand-off (quantized weights), or
+    on the FP32 weight-streaming GEMV (FP32 weights; CIH_GEMV16=0), or on
+    the MFMA GEMMs (CIH_GEMV=0); all outputs, with a <mask>, a sequence with
+    no residues (BOS, EOS) and contacts."""
     if gemv == "off":
         monkeypatch.setenv("CIH_GEMV", "0")
+    if gemv == "fp32":
+        if dtype == 0:
+            pytest.skip("FP32 weights always take the FP32 GEMV")
+        monkeypatch.setenv("CIH_GEMV16", "0")
     rng = np.random.default_rng(21 + dtype)
     cfg = ch.EsmConfig(128, 512, 2, 4)
     w = quantized(ch.EsmWeights.random(cfg, seed=5 + dtype, bias_std=0.02), dtype)

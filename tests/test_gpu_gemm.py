@@ -58,19 +58,31 @@ def test_gemm_matches_oracle(dtype, N, K, path, monkeypatch):
 
 # (N, K) chosen to cover every GEMV grid shape: one split (K <= 128), one
 # block per wave (1280x1280), two (1280x5120), four (5120x5120), a split with
-# a partly filled last wave (K = 480), columns not a multiple of 64 (33, 1000).
-GEMV_SHAPES = [(96, 64), (33, 320), (1280, 1280), (1280, 5120), (5120, 5120), (480, 480), (1000, 480), (3840, 1280)]
+# a partly filled last wave (K = 480), columns not a multiple of 64 (33, 1000);
+# for the f16-MFMA GEMV: one wave with clamped blocks (K = 64), a partly
+# filled last wave (K = 480), 16 waves (K = 5120), two rounds of 16 waves
+# (K = 10240), columns not a multiple of 16 (33, FP32 GEMV instead).
+GEMV_SHAPES = [(96, 64), (33, 320), (1280, 1280), (1280, 5120), (5120, 5120), (480, 480), (1000, 480), (3840, 1280),
+               (64, 10240)]
 
 
+@pytest.mark.parametrize("path", ["default", "fp32"])
 @pytest.mark.parametrize("dtype", [0, 1, 2])
 @pytest.mark.parametrize("N,K", GEMV_SHAPES)
-def test_gemv_matches_oracle(dtype, N, K):
+def test_gemv_matches_oracle(dtype, N, K, path, monkeypatch):
+    """At most 8 rows: quantized weights with N % 16 == 0 take the f16-MFMA
+    GEMV on limbs (k_gemv16: one workgroup per 16 columns over the whole K),
+    the others and CIH_GEMV16=0 the FP32 weight-streaming GEMV."""
+    if path == "fp32":
+        if dtype == 0:
+            pytest.skip("FP32 weights always take the FP32 GEMV")
+        monkeypatch.setenv("CIH_GEMV16", "0")
     rng = np.random.default_rng(N * 3 + K + dtype)
     w, wd = _weights(dtype, N, K, rng)
     bias = rng.standard_normal(N, dtype=np.float32) * np.float32(0.02)
     for M in range(1, 9):
         x = rng.standard_normal(M * K, dtype=np.float32)
-        print(f"gemv dtype={dtype} M={M} N={N} K={K}", flush=True)
+        print(f"gemv {path} dtype={dtype} M={M} N={N} K={K}", flush=True)
         got = ch.matmul_tiled(dtype, x, w, bias, K, N)
         ref = cr.matmul_tiled(dtype, x, w, bias, K, N, num_threads=8)
         scale = np.abs(x.reshape(M, K)).astype(np.float64) @ np.abs(wd.reshape(N, K)).astype(np.float64).T
