@@ -249,7 +249,9 @@ def decode_bench(args, ch):
         "config": {"workload": f"ESM-2 {args.model} {args.dtype} autoregressive decode, {n} stream(s), 16-token "
                                f"prompts, positions {P + args.warmup}..{P + args.warmup + K - 1}, seeded weights",
                    "streams": n, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv (weights streamed once per step for all streams)",
+        "roofline": {"bound": "hbm", "kernel": ("k_gemv16 split-K GEMV on f16 MFMA" if args.dtype != "fp32" and n <= 8
+                                                and os.environ.get("CIH_GEMV16") != "0" else "k_gemv")
+                                               + " (weights streamed once per step for all streams)",
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "timing": TIMING},
@@ -458,9 +460,13 @@ def main():
     fp32_path = os.environ.get("CIH_QGEMM") == "fp32"
     wname = {"q8": "Q8_0", "q4": "Q4_0", "fp32": "FP32"}[args.dtype]
     if gemv:
-        # weight-streaming GEMV: algorithmic bytes = Q8_0 weights + activations in/out
+        # weight streaming: algorithmic bytes = quantized weights + activations in/out
         achieved = q["bytes"] / (q["total_ms"] * 1e-3) / 1e9 if q["total_ms"] > 0 else 0.0
-        kname, peak, limbs = f"k_gemv<{wname}> weight streaming (QKV, Wo, FC1, FC2)", PEAK_HBM_GBS, None
+        if not fp32_model and os.environ.get("CIH_GEMV16") != "0" and not fp32_path:
+            kname = f"k_gemv16<{wname}> split-K GEMV on f16 MFMA (QKV, Wo, FC1, FC2)"
+        else:
+            kname = f"k_gemv<{wname}> weight streaming (QKV, Wo, FC1, FC2)"
+        peak, limbs = PEAK_HBM_GBS, None
     else:
         achieved = q["flops"] / (q["total_ms"] * 1e-3) / 1e12 if q["total_ms"] > 0 else 0.0
         if fp32_path or fp32_model:

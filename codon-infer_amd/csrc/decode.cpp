@@ -46,6 +46,23 @@ void destroy(cih_decoder *dc) {
     delete dc;
 }
 
+// A step of at most GEMV_MAX_M rows of a quantized model runs its layer
+// projections on the f16-MFMA GEMV, with the activations handed over as f16
+// limbs and the split-K partial sums added by the next kernel (the fused
+// attention: QKV's; the residual LayerNorm: Wo's and FC2's; FC2: FC1's).
+bool step_gemv16(const cih_decoder *dc, int n) {
+    const cih_model *m = dc->m;
+    if (n > GEMV_MAX_M || full_range_mode() || m->layers.empty() || m->cfg.dim % 32 || m->cfg.hidden_dim % 32)
+        return false;
+    const Layer &ly = m->layers[0];
+    return gemv16_applies(ly.wqkv, AF_H2, n, EPI_NONE) && gemv16_applies(ly.wo, AF_H2, n, EPI_NONE) &&
+           gemv16_applies(ly.w1, AF_H2, n, EPI_NONE) && gemv16_applies(ly.w2, AF_H2, n, EPI_NONE);
+}
+
+// Steps whose activations travel as f16 limbs (|x| < 65504) report a residual
+// that is no longer finite, and run again in full range.
+bool step_limbs(const cih_decoder *dc, int n) { return n > GEMV_MAX_M ? !full_range_mode() : step_gemv16(dc, n); }
+
 // The rows' forward from the staged device tokens / rows: embedding
 // (constant 0.88 scale, <mask> -> 0), the layers with cached causal
 // attention, final LN and LM head -> dc->logits.  Kernel launches only, so
@@ -65,7 +82,59 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
     // algorithmic attention work of the rows: keys 0..pos of their slot
     double keys = 0;
     for (int i = 0; i < n; i++) keys += dc->h_meta[dc->max_rows + 2 * i + 1] + 1;
-    for (int l = 0; l < L; l++) {
+    const bool g16 = step_gemv16(dc, n);
+    const size_t part_half = dc->part.floats / 2 / 64 * 64;
+    float *const part_a = dc->part.part, *const part_b = dc->part.part + part_half;
+    int pend_splits = 0;  // FC2 splits waiting in part_a
+    const float *pend_bias = nullptr;
+    for (int l = 0; l < L && g16; l++) {
+        const Layer &ly = m->layers[l];
+        const unsigned short *xbh = reinterpret_cast<const unsigned short *>(dc->xb);
+        {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
+            HIPCHK(launch_residual_layernorm(dc->x, pend_splits ? part_a : nullptr, pend_splits, pend_bias, ly.ln1w,
+                                             ly.ln1b, dc->xb, AF_H2, n, d, st));
+        }
+        int sq = 0, so = 0, s1 = 0;
+        {
+            ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * n * ly.wqkv.N * d, wbytes(ly.wqkv) + 4.0 * n * d + 4.0 * n * ly.wqkv.N);
+            HIPCHK(launch_gemv16_partials(ly.wqkv, xbh, n, part_b, part_half, &sq, st));
+        }
+        float *kc = dc->kc + l * layer, *vc = dc->vc + l * layer;
+        {
+            ProfScope ps(m, CIH_KC_ATTENTION, 4.0 * keys * d, 8.0 * keys * d + 24.0 * n * d);
+            if (fused) {
+                HIPCHK(launch_decode_attention_fused(dc->qkv, part_b, sq, ly.bqkv, d, H, dc->d_rows, n, dc->max_len,
+                                                     dc->rope_c, dc->rope_s, kc, vc, dc->slot_stride, dc->ao, st,
+                                                     AF_H2));
+            } else {
+                HIPCHK(launch_gemv16_fold(part_b, sq, n, 3 * d, ly.bqkv, dc->qkv, 3 * d, EPI_NONE, st));
+                HIPCHK(launch_rope_kv(dc->qkv, d, m->hd, dc->d_rows, n, dc->rope_c, dc->rope_s, kc, vc,
+                                      dc->slot_stride, st));
+                HIPCHK(launch_decode_attention(dc->qkv, d, H, dc->d_rows, n, dc->max_len, kc, vc, dc->slot_stride,
+                                               dc->ao, st, AF_H2));
+            }
+        }
+        {
+            ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * n * d * d, wbytes(ly.wo) + 8.0 * n * d);
+            HIPCHK(launch_gemv16_partials(ly.wo, reinterpret_cast<const unsigned short *>(dc->ao), n, part_a,
+                                          part_half, &so, st));
+        }
+        {
+            ProfScope ps(m, CIH_KC_OTHER, 0, 4.0 * so * n * d + 12.0 * n * d);
+            HIPCHK(launch_residual_layernorm(dc->x, part_a, so, ly.bo, ly.ln2w, ly.ln2b, dc->xb, AF_H2, n, d, st));
+        }
+        {
+            ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * n * F * d, wbytes(ly.w1) + 4.0 * n * (d + F));
+            HIPCHK(launch_gemv16_partials(ly.w1, xbh, n, part_b, part_half, &s1, st));
+        }
+        {
+            ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * n * F * d, wbytes(ly.w2) + 4.0 * s1 * n * F + 4.0 * n * d);
+            HIPCHK(launch_gemv16_gelu_partials(ly.w2, part_b, s1, ly.b1, n, part_a, part_half, &pend_splits, st));
+            pend_bias = ly.b2;
+        }
+    }
+    for (int l = 0; l < L && !g16; l++) {
         const Layer &ly = m->layers[l];
         {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
@@ -109,8 +178,12 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
         // more rows than the GEMV takes go through GEMMs on f16 limbs: the
         // final LayerNorm reports a residual that overflowed them
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
-        HIPCHK(launch_layernorm(dc->x, m->lnfw, m->lnfb, dc->ao, AF_F32, n, d, st,
-                                n > GEMV_MAX_M && !full_range_mode() ? dc->d_flag : nullptr));
+        int *flag = step_limbs(dc, n) ? dc->d_flag : nullptr;
+        if (pend_splits)
+            HIPCHK(launch_residual_layernorm(dc->x, part_a, pend_splits, pend_bias, m->lnfw, m->lnfb, dc->ao, AF_F32, n,
+                                             d, st, flag));
+        else
+            HIPCHK(launch_layernorm(dc->x, m->lnfw, m->lnfb, dc->ao, AF_F32, n, d, st, flag));
     }
     // project_lm_head_* (lib.rs:3952-4015): dense + GELU, LN, decoder; or the
     // tied embedding without bias
@@ -141,18 +214,21 @@ int run_rows(cih_decoder *dc, int n) {
     const bool fused = dc->unique;
     HIPCHK(hipMemcpyAsync(dc->d_tokens, dc->h_meta, (size_t)n * 4, hipMemcpyHostToDevice, st));
     HIPCHK(hipMemcpyAsync(dc->d_rows, dc->h_meta + dc->max_rows, (size_t)n * 8, hipMemcpyHostToDevice, st));
-    if (!use_graph(dc, n)) {
-        if (n <= GEMV_MAX_M) return enqueue_rows(dc, n, fused);
-        // rows through the f16-limb GEMMs: a non-finite residual (an
-        // overflowed limb) runs the rows again in full-range mode, rewriting
-        // the same cache positions
-        int *h_flag = dc->h_meta + 3 * dc->max_rows;
-        HIPCHK(hipMemsetAsync(dc->d_flag, 0, sizeof(int), st));
-        if (int rc = enqueue_rows(dc, n, fused)) return rc;
+    // Rows whose activations travel as f16 limbs: a non-finite residual (an
+    // overflowed limb) runs the rows again in full-range mode, kernel by
+    // kernel, rewriting the same cache positions.
+    const bool limbs = step_limbs(dc, n);
+    int *h_flag = dc->h_meta + 3 * dc->max_rows;
+    auto check = [&]() -> int {
         HIPCHK(hipMemcpyAsync(h_flag, dc->d_flag, sizeof(int), hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
         if (*h_flag & FLAG_NONFINITE) return in_full_range([&] { return enqueue_rows(dc, n, fused); });
         return 0;
+    };
+    if (limbs) HIPCHK(hipMemsetAsync(dc->d_flag, 0, sizeof(int), st));
+    if (!use_graph(dc, n)) {
+        if (int rc = enqueue_rows(dc, n, fused)) return rc;
+        return limbs ? check() : 0;
     }
     auto key = std::make_tuple(n, fused, kernel_switches());
     auto it = dc->graphs.find(key);
@@ -172,7 +248,7 @@ int run_rows(cih_decoder *dc, int n) {
         it = dc->graphs.emplace(key, ex).first;
     }
     HIPCHK(hipGraphLaunch(it->second, st));
-    return 0;
+    return limbs ? check() : 0;
 }
 
 // Validates rows and stages them; rows of one slot must continue its

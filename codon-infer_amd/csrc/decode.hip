@@ -6,6 +6,7 @@
 #include <math.h>
 
 #include "kernels.h"
+#include "x3.h"
 
 namespace cih {
 
@@ -69,7 +70,7 @@ __device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_m
 // RoPE to its head's Q and K, writes K and V at pos into the cache for later
 // steps, and takes key pos from LDS rather than from the cache, so no
 // workgroup reads what another one writes.  Otherwise k_rope_kv has run.
-template <int HD, bool FUSED>
+template <int HD, bool FUSED, int OF>
 __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *__restrict__ qkv,
                                                                   const float *__restrict__ part, int splits,
                                                                   const float *__restrict__ bias, int d,
@@ -219,7 +220,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
         float o = gsum[t];
 #pragma unroll
         for (int k = 1; k < G; k++) o += gsum[k * HD + t];
-        out[(size_t)r * d + h * HD + t] = o;
+        if constexpr (OF == AF_H2) h2_store(reinterpret_cast<unsigned short *>(out), r, h * HD + t, d, o);
+        else out[(size_t)r * d + h * HD + t] = o;
     }
 }
 
@@ -240,15 +242,20 @@ hipError_t launch_rope_kv(float *qkv, int d, int hd, const int *rows, int n, con
 template <bool FUSED>
 static hipError_t launch_att(const float *qkv, const float *part, int splits, const float *bias, int d, int H,
                              const int *rows, int n, int max_len, const float *rc, const float *rs, float *kc,
-                             float *vc, int64_t slot_stride, float *out, hipStream_t st) {
+                             float *vc, int64_t slot_stride, float *out, int out_fmt, hipStream_t st) {
     const int hd = d / H;
     const float inv_scale = 1.0f / sqrtf((float)hd);
     const size_t lds = decode_attention_lds(hd, max_len);
     const dim3 grid(n, H), block(ATT_THREADS);
+    if (out_fmt != AF_F32 && (out_fmt != AF_H2 || d % 32)) return hipErrorInvalidValue;
 #define CIH_ATT_CASE(HDV)                                                                                           \
     case HDV:                                                                                                      \
-        hipLaunchKernelGGL((k_decode_attention<HDV, FUSED>), grid, block, lds, st, qkv, part, splits, bias, d,     \
-                           rows, rc, rs, kc, vc, slot_stride, inv_scale, out);                                     \
+        if (out_fmt == AF_H2)                                                                                      \
+            hipLaunchKernelGGL((k_decode_attention<HDV, FUSED, AF_H2>), grid, block, lds, st, qkv, part, splits,   \
+                               bias, d, rows, rc, rs, kc, vc, slot_stride, inv_scale, out);                        \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_decode_attention<HDV, FUSED, AF_F32>), grid, block, lds, st, qkv, part, splits,  \
+                               bias, d, rows, rc, rs, kc, vc, slot_stride, inv_scale, out);                        \
         break;
     switch (hd) {
         CIH_ATT_CASE(16)
@@ -263,20 +270,20 @@ static hipError_t launch_att(const float *qkv, const float *part, int splits, co
 
 hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *rows, int n, int max_len,
                                    const float *kc, const float *vc, int64_t slot_stride, float *out,
-                                   hipStream_t st) {
+                                   hipStream_t st, int out_fmt) {
     if (n <= 0) return hipSuccess;
     return launch_att<false>(qkv, nullptr, 0, nullptr, d, H, rows, n, max_len, nullptr, nullptr,
-                             const_cast<float *>(kc), const_cast<float *>(vc), slot_stride, out, st);
+                             const_cast<float *>(kc), const_cast<float *>(vc), slot_stride, out, out_fmt, st);
 }
 
 hipError_t launch_decode_attention_fused(float *qkv, const float *part, int splits, const float *bias, int d, int H,
                                          const int *rows, int n, int max_len, const float *rope_c,
                                          const float *rope_s, float *kc, float *vc, int64_t slot_stride, float *out,
-                                         hipStream_t st) {
+                                         hipStream_t st, int out_fmt) {
     if (n <= 0) return hipSuccess;
     if (part && (!bias || splits < 1)) return hipErrorInvalidValue;
     return launch_att<true>(qkv, part, splits, bias, d, H, rows, n, max_len, rope_c, rope_s, kc, vc, slot_stride, out,
-                            st);
+                            out_fmt, st);
 }
 
 }  // namespace cih

@@ -326,16 +326,17 @@ hipError_t launch_rope_kv(float *qkv, int d, int hd, const int *rows, int n, con
                           float *kc, float *vc, int64_t slot_stride, hipStream_t st);
 hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *rows, int n, int max_len,
                                    const float *kc, const float *vc, int64_t slot_stride, float *out,
-                                   hipStream_t st);
+                                   hipStream_t st, int out_fmt = AF_F32);
 // Both steps in one launch when every slot appears at most once among the
 // rows (one new token per sequence): each (row, head) workgroup rotates its
 // head's Q and K, writes K and V at pos, and attends with key pos from LDS.
 // With part != nullptr the rows' Q|K|V come as [splits][n][3d] GEMV partial
-// sums (launch_gemv_partials) plus bias, added in split order; qkv is unused.
+// sums (launch_gemv_partials, launch_gemv16_partials) plus bias; qkv is
+// unused.  out_fmt: out as FP32 rows or H2 limbs.
 hipError_t launch_decode_attention_fused(float *qkv, const float *part, int splits, const float *bias, int d, int H,
                                          const int *rows, int n, int max_len, const float *rope_c,
                                          const float *rope_s, float *kc, float *vc, int64_t slot_stride, float *out,
-                                         hipStream_t st);
+                                         hipStream_t st, int out_fmt = AF_F32);
 size_t decode_attention_lds(int hd, int max_len);  // dynamic LDS bytes per workgroup
 
 // Copies packed rows [T][width] into padded [B][S_max][width] (valid rows only).
