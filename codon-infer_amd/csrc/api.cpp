@@ -255,7 +255,8 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
         // zeroed once, so dims past hd stay zero (nothing writes them)
         const size_t img = B * ((S + 31) / 32) * H * kv_image_bytes((int)m->hd);
         good = ok(dalloc(ws.kv_img, img, dl)) && ok(dalloc(ws.kv_tb, B, dl)) && ok(dalloc(ws.kv_pk, T, dl)) &&
-               ok(dalloc(ws.kv_pos, T, dl)) && ok(hipMemset(ws.kv_img, 0, img));
+               ok(dalloc(ws.kv_pos, T, dl)) && ok(dalloc(ws.kv_ti, B * ((S + 31) / 32) * 4, dl)) &&
+               ok(hipMemset(ws.kv_img, 0, img));
     }
     if (good && (flags & CIH_OUT_CONTACTS))
         good = ok(dalloc(ws.M, B * n * n, dl)) && ok(dalloc(ws.r, L * H * B * n, dl)) &&
@@ -400,8 +401,13 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         const bool prep_only = ie && !std::strcmp(ie, "prep");
         use_img = ws.kv_img && L > 0 && !(ie && !std::strcmp(ie, "0")) && !(ae && !std::strcmp(ae, "fp32")) &&
                   !full_range_mode() && attention_img_supported((int)m->hd);
-        epi_img = use_img && !prep_only && af == AF_H2 && gemm_lds_applies(m->layers[0].wqkv, af, T, EPI_NONE);
-        if (!epi_img && !prep_only && T < 2048) use_img = false;
+        // the QKV epilogue has forms for head sizes 16, 32 and 64; head size 24 takes the prep kernel
+        epi_img = use_img && !prep_only && af == AF_H2 && (m->hd == 16 || m->hd == 32 || m->hd == 64) &&
+                  gemm_lds_applies(m->layers[0].wqkv, af, T, EPI_NONE);
+        // without the epilogue, images cost a prep kernel per layer: it pays
+        // from 2048 tokens on, except at head size 24 (35M B=8 ragged: prep
+        // 8.5 us, attention 41.2 -> 33.5 us per layer; net loss)
+        if (!epi_img && !prep_only && (T < 2048 || m->hd == 24)) use_img = false;
         for (int b = 0; b < B; b++) tile_rows += (lens[b] + 31) / 32;
     }
     const int epi_qkv = m->hd == 16 ? EPI_QKV16 : (m->hd == 32 ? EPI_QKV32 : EPI_QKV64);
@@ -429,7 +435,7 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     }
     if (use_img) {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T);
-        HIPCHK(launch_kv_setup(sm, (int)m->hd, H, ws.kv_tb, ws.kv_pk, ws.kv_pos, ws.kv_img, st));
+        HIPCHK(launch_kv_setup(sm, (int)m->hd, H, ws.kv_tb, ws.kv_pk, ws.kv_pos, ws.kv_ti, ws.kv_img, st));
     }
 
     for (int l = 0; l < L; l++) {
@@ -526,7 +532,7 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             HIPCHK(gemm(m, ly.wqkv, ws.xb, d, af, ly.bqkv, ws.qkv, 3 * d, T, EPI_NONE));
             if (use_img) {
                 ProfScope ps(m, CIH_KC_OTHER, 0, 16.0 * T * d);
-                HIPCHK(launch_kv_prep(ws.qkv, d, H, sm, ws.kv_tb, tile_rows, ws.rope_c, ws.rope_s, ws.kv_img, st));
+                HIPCHK(launch_kv_prep(ws.qkv, d, H, ws.kv_ti, tile_rows, ws.rope_c, ws.rope_s, ws.kv_img, st));
             }
         }
         {

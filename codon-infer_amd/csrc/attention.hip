@@ -1045,88 +1045,127 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     }
 }
 
-// Per-forward set-up of the tile images, one workgroup per sequence b:
-// tb[b] = sum of ceil(len / 32) over the sequences before b; pk = 32 tb[b] +
-// position and pos = position for its tokens; the padding keys (positions
-// len..) of its last tile are zeroed in every head's image, both limbs, so
-// that masked keys multiply zeros whatever an earlier batch left there.
+// Per-forward set-up of the tile images, one workgroup per (sequence b,
+// head h): tb[b] = sum of ceil(len / 32) over the sequences before b; pk =
+// 32 tb[b] + position and pos = position for its tokens, and the tile-row
+// table ti (head 0's workgroup); the padding keys (positions len..) of the
+// last tile are zeroed in head h's image, both limbs — the K rows as whole
+// 16-byte stores (they are contiguous), the V positions one by one — so that
+// masked keys multiply zeros whatever an earlier batch left there.
 template <int HD>
 __global__ __launch_bounds__(256) void k_kv_setup(const int *__restrict__ cu, const int *__restrict__ lens, int H,
                                                   int *__restrict__ tb, int *__restrict__ pk, int *__restrict__ pos,
-                                                  unsigned char *__restrict__ img) {
+                                                  int *__restrict__ ti, unsigned char *__restrict__ img) {
     using I = KvImg<HD>;
-    const int b = blockIdx.x;
+    const int b = blockIdx.x, h = blockIdx.y;
     __shared__ int s_first;
     if (threadIdx.x == 0) {
         int f = 0;
         for (int i = 0; i < b; i++) f += (lens[i] + 31) / 32;
         s_first = f;
-        tb[b] = f;
+        if (h == 0) tb[b] = f;
     }
     __syncthreads();
     const int first = s_first, len = lens[b], base = cu[b];
-    for (int t = threadIdx.x; t < len; t += 256) {
-        pk[base + t] = first * 32 + t;
-        pos[base + t] = t;
+    if (h == 0) {
+        for (int t = threadIdx.x; t < len; t += 256) {
+            pk[base + t] = first * 32 + t;
+            pos[base + t] = t;
+        }
+        for (int t = threadIdx.x; t < (len + 31) / 32; t += 256)
+            *reinterpret_cast<int4 *>(ti + 4 * (first + t)) = make_int4(base + 32 * t, min(32, len - 32 * t), 32 * t, b);
     }
     const int pad = (32 - len % 32) % 32;
     if (pad == 0 || len == 0) return;
     const int last = first + (len - 1) / 32, k0 = len % 32;
-    // (head, limb, padding key, dim) of K (HDP dims) and V (VW dims)
-    const int per = 2 * pad * (I::HDP + I::VW);
-    for (int idx = threadIdx.x; idx < H * per; idx += 256) {
-        const int h = idx / per, r = idx % per;
-        const int limb = r / (pad * (I::HDP + I::VW)), r2 = r % (pad * (I::HDP + I::VW));
-        unsigned char *t = img + ((size_t)last * H + h) * I::TB;
-        if (r2 < pad * I::HDP) {
-            const int key = k0 + r2 / I::HDP, dim = r2 % I::HDP;
-            *reinterpret_cast<_Float16 *>(t + I::koff(key, dim, limb)) = (_Float16)0.0f;
-        } else {
-            const int r3 = r2 - pad * I::HDP, key = k0 + r3 / I::VW, dim = r3 % I::VW;
-            *reinterpret_cast<_Float16 *>(t + I::voff(key, dim, limb)) = (_Float16)0.0f;
-        }
+    unsigned char *t = img + ((size_t)last * H + h) * I::TB;
+    // K rows k0..31: bytes [k0 KRP, 32 KRP) of the image
+    for (int i = threadIdx.x; i < pad * I::KRP / 16; i += 256)
+        *reinterpret_cast<uint4 *>(t + k0 * I::KRP + 16 * i) = make_uint4(0u, 0u, 0u, 0u);
+    // V: (limb, dim row, padding key)
+    for (int i = threadIdx.x; i < 2 * I::VW * pad; i += 256) {
+        const int limb = i / (I::VW * pad), r = i % (I::VW * pad), dim = r / pad, key = k0 + r % pad;
+        *reinterpret_cast<_Float16 *>(t + I::voff(key, dim, limb)) = (_Float16)0.0f;
     }
 }
 
 // Tile images from FP32 Q|K|V rows, for projections that did not write them
-// in their epilogue (GEMV, the register-staged GEMMs, FP32 weights): the
-// same rotation and split as the LDS GEMM's QKV epilogue, so both give the
-// same bytes.  One workgroup per (tile row, head); consecutive threads take
-// consecutive dims of a key (coalesced reads).  Padding keys are left to
-// k_kv_setup.
+// in their epilogue (GEMV, the register-staged GEMMs, FP32 weights, head size
+// 24): the same rotation and split as the LDS GEMM's QKV epilogue, so both
+// give the same bytes.  One wave per (tile row, head): lane k < 32 rotates
+// key k's K row and writes its 16-byte chunks (8 dims of one limb); lane
+// 32 + k splits key k's V row into LDS at its V^T position, and after a
+// barrier the wave writes the V^T chunks (8 key positions of one dim and
+// limb).  Padding keys are left to k_kv_setup, padding dims are zero from
+// the allocation.
 template <int HD>
-__global__ __launch_bounds__(256) void k_kv_prep(const float *__restrict__ qkv, int d, const int *__restrict__ cu,
-                                                 const int *__restrict__ lens, const int *__restrict__ tb, int B,
-                                                 const float *__restrict__ rc, const float *__restrict__ rsn,
-                                                 unsigned char *__restrict__ img, int H) {
+__global__ __launch_bounds__(64) void k_kv_prep(const float *__restrict__ qkv, int d, const int *__restrict__ ti,
+                                                const float *__restrict__ rc, const float *__restrict__ rsn,
+                                                unsigned char *__restrict__ img, int H) {
     using I = KvImg<HD>;
-    constexpr int HALF = HD / 2;
+    constexpr int HALF = HD / 2, NG = HD / 8;  // 8-dim groups of a row
+    __shared__ __attribute__((aligned(16))) unsigned short vt[2][HD][32];  // [limb][dim][position]
     const int tr = blockIdx.x / H, h = blockIdx.x % H;
-    // the sequence owning tile row tr: the last b with tb[b] <= tr
-    int lo = 0, hi = B - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tb[mid] <= tr) lo = mid;
-        else hi = mid - 1;
-    }
-    const int b = lo, kt0 = (tr - tb[b]) * 32, len = lens[b];
+    const int4 info = *reinterpret_cast<const int4 *>(ti + 4 * tr);  // first packed row, keys, first position
+    const int kt0 = info.z, nk = info.y;
     const size_t ld = (size_t)3 * d;
-    const float *base = qkv + (size_t)(cu[b] + kt0) * ld + h * HD;
+    const float *base = qkv + (size_t)info.x * ld + h * HD;
     unsigned char *t = img + ((size_t)tr * H + h) * I::TB;
-    const int nk = min(32, len - kt0);
-    for (int idx = threadIdx.x; idx < nk * HD; idx += 256) {
-        const int key = idx / HD, j = idx % HD, jj = j < HALF ? j : j - HALF;
-        const float *k = base + (size_t)key * ld + d;
-        const size_t ti = (size_t)(kt0 + key) * HALF + jj;
-        const float c = rc[ti], s = rsn[ti];
-        const float r = j < HALF ? rot_lo(k[j], k[j + HALF], c, s) : rot_hi(k[j], k[j - HALF], c, s);
-        const _Float16 rh = (_Float16)r, rl = (_Float16)(r - (float)rh);
-        *reinterpret_cast<_Float16 *>(t + I::koff(key, j, 0)) = rh;
-        *reinterpret_cast<_Float16 *>(t + I::koff(key, j, 1)) = rl;
-        const float v = base[(size_t)key * ld + 2 * d + j];
-        const _Float16 vh = (_Float16)v, vl = (_Float16)(v - (float)vh);
-        *reinterpret_cast<_Float16 *>(t + I::voff(key, j, 0)) = vh;
-        *reinterpret_cast<_Float16 *>(t + I::voff(key, j, 1)) = vl;
+    const int lane = threadIdx.x, key = lane & 31;
+    auto pack8 = [](const unsigned short (&v)[8]) __attribute__((always_inline)) {
+        return make_uint4(v[0] | (unsigned)v[1] << 16, v[2] | (unsigned)v[3] << 16, v[4] | (unsigned)v[5] << 16,
+                          v[6] | (unsigned)v[7] << 16);
+    };
+    if (lane < 32) {
+        if (key < nk) {
+            const float *k = base + (size_t)key * ld + d;
+            const float *c = rc + (size_t)(kt0 + key) * HALF, *sn = rsn + (size_t)(kt0 + key) * HALF;
+            float x[HD], cs[HALF], ss[HALF];
+#pragma unroll
+            for (int j = 0; j < HD; j += 4)
+                *reinterpret_cast<float4 *>(&x[j]) = *reinterpret_cast<const float4 *>(k + j);
+#pragma unroll
+            for (int j = 0; j < HALF; j += 4) {
+                *reinterpret_cast<float4 *>(&cs[j]) = *reinterpret_cast<const float4 *>(c + j);
+                *reinterpret_cast<float4 *>(&ss[j]) = *reinterpret_cast<const float4 *>(sn + j);
+            }
+#pragma unroll
+            for (int g = 0; g < NG; g++) {
+                unsigned short h8[8], l8[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int j = 8 * g + e;
+                    const float r = j < HALF ? rot_lo(x[j], x[j + HALF], cs[j], ss[j])
+                                             : rot_hi(x[j], x[j - HALF], cs[j - HALF], ss[j - HALF]);
+                    const _Float16 rh = (_Float16)r, rl = (_Float16)(r - (float)rh);
+                    h8[e] = __builtin_bit_cast(unsigned short, rh);
+                    l8[e] = __builtin_bit_cast(unsigned short, rl);
+                }
+                *reinterpret_cast<uint4 *>(t + I::koff(key, 8 * g, 0)) = pack8(h8);
+                *reinterpret_cast<uint4 *>(t + I::koff(key, 8 * g, 1)) = pack8(l8);
+            }
+        }
+    } else {
+        // key's V row into LDS at position vpos(key); keys past the tile's end are zero
+        const int p = I::vpos(key);
+        float x[HD];
+#pragma unroll
+        for (int j = 0; j < HD; j += 4)
+            *reinterpret_cast<float4 *>(&x[j]) = key < nk ? *reinterpret_cast<const float4 *>(base + (size_t)key * ld + 2 * d + j)
+                                                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int j = 0; j < HD; j++) {
+            const _Float16 vh = (_Float16)x[j], vl = (_Float16)(x[j] - (float)vh);
+            vt[0][j][p] = __builtin_bit_cast(unsigned short, vh);
+            vt[1][j][p] = __builtin_bit_cast(unsigned short, vl);
+        }
+    }
+    __syncthreads();
+    // V^T chunks: (limb, dim, positions 8q .. 8q + 7)
+    for (int i = lane; i < 2 * HD * 4; i += 64) {
+        const int limb = i / (HD * 4), r = (i >> 2) % HD, q = i & 3;
+        *reinterpret_cast<uint4 *>(t + I::voff(I::vpos(8 * q), r, limb)) =
+            *reinterpret_cast<const uint4 *>(&vt[limb][r][8 * q]);
     }
 }
 
@@ -1208,17 +1247,26 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     return hipGetLastError();
 }
 
-bool attention_img_supported(int hd) { return hd == 16 || hd == 32 || hd == 64; }
+bool attention_img_supported(int hd) { return hd == 16 || hd == 24 || hd == 32 || hd == 64; }
 
 size_t kv_image_bytes(int hd) {
-    return hd == 16 ? KvImg<16>::TB : (hd == 32 ? KvImg<32>::TB : (hd == 64 ? KvImg<64>::TB : 0));
+    switch (hd) {
+    case 16: return KvImg<16>::TB;
+    case 24: return KvImg<24>::TB;
+    case 32: return KvImg<32>::TB;
+    case 64: return KvImg<64>::TB;
+    default: return 0;
+    }
 }
 
-hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos, unsigned char *img, hipStream_t st) {
+hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos, int *ti, unsigned char *img,
+                           hipStream_t st) {
     if (sm.B <= 0) return hipSuccess;
-#define CIH_KVS(HDV) hipLaunchKernelGGL((k_kv_setup<HDV>), dim3(sm.B), dim3(256), 0, st, sm.cu, sm.lens, H, tb, pk, pos, img)
+#define CIH_KVS(HDV)                                                                                               \
+    hipLaunchKernelGGL((k_kv_setup<HDV>), dim3(sm.B, H), dim3(256), 0, st, sm.cu, sm.lens, H, tb, pk, pos, ti, img)
     switch (hd) {
     case 16: CIH_KVS(16); break;
+    case 24: CIH_KVS(24); break;
     case 32: CIH_KVS(32); break;
     case 64: CIH_KVS(64); break;
     default: return hipErrorInvalidValue;
@@ -1227,15 +1275,15 @@ hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos
     return hipGetLastError();
 }
 
-hipError_t launch_kv_prep(const float *qkv, int d, int H, SeqMeta sm, const int *tb, int tile_rows, const float *rope_cos,
+hipError_t launch_kv_prep(const float *qkv, int d, int H, const int *ti, int tile_rows, const float *rope_cos,
                           const float *rope_sin, unsigned char *img, hipStream_t st) {
     if (tile_rows <= 0) return hipSuccess;
     const unsigned grid = (unsigned)tile_rows * H;
 #define CIH_KVP(HDV)                                                                                              \
-    hipLaunchKernelGGL((k_kv_prep<HDV>), dim3(grid), dim3(256), 0, st, qkv, d, sm.cu, sm.lens, tb, sm.B, rope_cos, \
-                       rope_sin, img, H)
+    hipLaunchKernelGGL((k_kv_prep<HDV>), dim3(grid), dim3(64), 0, st, qkv, d, ti, rope_cos, rope_sin, img, H)
     switch (d / H) {
     case 16: CIH_KVP(16); break;
+    case 24: CIH_KVP(24); break;
     case 32: CIH_KVP(32); break;
     case 64: CIH_KVP(64); break;
     default: return hipErrorInvalidValue;
@@ -1288,6 +1336,7 @@ hipError_t launch_attention_img(const float *qkv, int d, int H, SeqMeta sm, cons
     }
     switch (hd) {
     case 16: CIH_ATI_HD(16) break;
+    case 24: CIH_ATI_HD(24) break;
     case 32: CIH_ATI_HD(32) break;
     case 64: CIH_ATI_HD(64) break;
     default: return hipErrorInvalidValue;

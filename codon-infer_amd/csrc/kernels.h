@@ -282,14 +282,15 @@ hipError_t launch_attention_img(const float *qkv, int d, int H, SeqMeta sm, cons
                                 int64_t pb, int64_t ph, float *rowsum, float *part, size_t part_floats, hipStream_t st);
 
 // Per-forward set-up of the tile images: tb[b] = first tile row of sequence
-// b, pk / pos of every packed token, and the padding keys of each sequence's
-// last tile zeroed in every head's image (so masked keys multiply finite
-// zeros).  Tile rows used: kv_tile_rows(lens).
-hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos, unsigned char *img, hipStream_t st);
+// b, pk / pos of every packed token, ti[tile row] = (first packed row, keys,
+// first position, sequence), and the padding keys of each sequence's last
+// tile zeroed in every head's image (so masked keys multiply finite zeros).
+hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos, int *ti, unsigned char *img,
+                           hipStream_t st);
 // Tile images from FP32 Q|K|V rows (any projection), tile_rows = sum over
-// sequences of ceil(len / 32); after launch_kv_setup.  Same bytes as the
-// EPI_QKV* epilogue.
-hipError_t launch_kv_prep(const float *qkv, int d, int H, SeqMeta sm, const int *tb, int tile_rows, const float *rope_cos,
+// sequences of ceil(len / 32); after launch_kv_setup (reads its ti).  Same
+// bytes as the EPI_QKV* epilogue.
+hipError_t launch_kv_prep(const float *qkv, int d, int H, const int *ti, int tile_rows, const float *rope_cos,
                           const float *rope_sin, unsigned char *img, hipStream_t st);
 bool attention_img_supported(int hd);
 size_t kv_image_bytes(int hd);  // bytes of one (tile row, head) image

@@ -55,6 +55,7 @@ struct Workspace {
     // K/V tile images (kv_image.h) written by the QKV projection's epilogue
     unsigned char *kv_img = nullptr;
     int *kv_tb = nullptr, *kv_pk = nullptr, *kv_pos = nullptr;  // [maxB], [T], [T]
+    int *kv_ti = nullptr;  // [tile rows][4]: first packed row, keys, first position, sequence
     int *dms_meta = nullptr;                            // [max(maxB, maxS)][2] scored row, wild type
     float *dms_out = nullptr;                           // [max(maxB, maxS)][21] deltas, entropy
     // device staging of outputs for host-pointer calls (padded layouts)

@@ -10,9 +10,10 @@ independent of the batch it runs in: large batches take the image path, small
 ones the staged one); against the oracle, the tolerances of test_gpu_forward.
 Batches cover each head size with a ragged batch large enough for the LDS
 GEMM (the epilogue writes the images: sequences start inside 32-row GEMM
-tiles, so both the whole-line and the element-wise V stores run), a small
-batch, the prep kernel (CIH_ATT_IMG=prep: images from FP32 rows at any size)
-and every layer's maps (the two-pass export kernel).
+tiles, so both the whole-line and the element-wise V stores run; head size
+24, which has no epilogue form, takes the prep kernel there), a small batch,
+the prep kernel (CIH_ATT_IMG=prep: images from FP32 rows at any size) and
+every layer's maps (the two-pass export kernel).
 """
 import numpy as np
 import pytest
@@ -41,8 +42,9 @@ def run_paths(monkeypatch, cfg, w, seqs, flags):
     return out
 
 
-@pytest.mark.parametrize("hd,n_seq,lo,hi", [(64, 6, 190, 420), (32, 9, 250, 420), (16, 13, 300, 420),
-                                             (64, 2, 20, 90), (32, 3, 5, 40), (16, 2, 1, 33)])
+@pytest.mark.parametrize("hd,n_seq,lo,hi", [(64, 6, 190, 420), (32, 9, 250, 420), (24, 9, 250, 420),
+                                             (16, 13, 300, 420), (64, 2, 20, 90), (32, 3, 5, 40), (24, 2, 10, 60),
+                                             (16, 2, 1, 33)])
 def test_image_vs_staged(monkeypatch, hd, n_seq, lo, hi):
     d = 20 * hd
     cfg = ch.EsmConfig(d, 4 * d, 2, 20)
@@ -65,7 +67,7 @@ def test_image_vs_staged(monkeypatch, hd, n_seq, lo, hi):
     assert e <= 1e-3
 
 
-@pytest.mark.parametrize("hd", [64, 32, 16])
+@pytest.mark.parametrize("hd", [64, 32, 24, 16])
 def test_image_maps_vs_staged(monkeypatch, hd):
     """Every layer's attention maps and the final-layer mean: the two-pass
     export kernel on images (prep kernel) bit-identical to its staged twin,
