@@ -355,10 +355,23 @@ hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, c
     // Quantized weights go to the 16-bit-limb MFMA kernel (FP32 or pre-split
     // activations) unless CIH_QGEMM=fp32 selects the FP32-MFMA kernel, which
     // gives the same results to FP32 rounding and is kept for A/B runs.
+    const char *path = getenv("CIH_QGEMM");
+    const bool fp32_path = path && !strcmp(path, "fp32");
     if (W.fmt != WF_F32) {
-        const char *path = getenv("CIH_QGEMM");
-        if (a_fmt != AF_F32 || !(path && !strcmp(path, "fp32")))
-            return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st);
+        if (a_fmt != AF_F32 || !fp32_path) return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st);
+    }
+    // FP32 weights with a pair copy: the same f16-limb GEMM on [hi | lo]
+    // (CIH_QGEMM=fp32, CIH_LIMBS=bf16x3 and full range keep FP32 MFMA)
+    const char *lv = getenv("CIH_LIMBS");
+    if (W.fmt == WF_F32 && W.p16 && W.psc && !fp32_path && !(lv && !strcmp(lv, "bf16x3")) && !full_range_mode() &&
+        (a_fmt == AF_F32 || a_fmt == AF_H2)) {
+        DevMatrix P;
+        P.fmt = WF_F16P;
+        P.N = W.N;
+        P.K = W.K;
+        P.q = W.p16;
+        P.sc = W.psc;
+        return launch_gemm_x3(P, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st);
     }
     if (a_fmt != AF_F32 || epi == EPI_GELU_X3 || epi == EPI_GELU_H2 || ldx % 4 != 0) return hipErrorInvalidValue;
     const float *X = reinterpret_cast<const float *>(Xv);

@@ -119,9 +119,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     constexpr int MT = BM / 64, NT = BN / 64;
     // A tile per k-block: FP32 -> BM*8 float4 (split here); X3 -> BM*12, H2 -> BM*8 16-byte chunks (copied)
     constexpr int A_LOADS = AF == AF_X3 ? BM * 12 / 256 : BM / 32;
-    constexpr int B_ITEMS = BN * 2;                  // (column, half of the block's bytes)
+    constexpr bool PAIR = WF == WF_F16P;             // f16 quants, K doubled: weight block kb meets A block kb mod KB
+    static_assert(!PAIR || LIMB == LIMB_F16X2, "pair weights with f16 limbs only");
+    constexpr int B_ITEMS = BN * (PAIR ? 4 : 2);     // (column, quarter or half of the block's bytes)
     constexpr int B_LOADS = (B_ITEMS + 255) / 256;
-    constexpr int QB = WF == WF_Q8 ? 32 : 16;        // quant bytes per block
+    constexpr int QB = WF == WF_Q8 ? 32 : (PAIR ? 64 : 16);  // quant bytes per block
     constexpr int NL = LimbT<LIMB>::NL, AROW = LimbT<LIMB>::AROW;
     using V8 = typename LimbT<LIMB>::V;
     static_assert(AF == AF_F32 || (AF == AF_X3) == (LIMB == LIMB_BF16X3), "activation format / limb type mismatch");
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     int mt, nt;
     tile_xcd(blockIdx.x, nM * nN, nM, nN, mt, nt);
     const int m0 = mt * BM, n0 = nt * BN;
-    const int KB = K / 32;
+    const int KB = K / 32, KBW = PAIR ? 2 * KB : KB;  // activation / weight k-blocks
 
     // two register stages: block kb+2 is in flight while block kb is multiplied
     u32x4 ra[2][A_LOADS];
@@ -149,7 +151,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     // last row / column instead (their outputs are never stored), so the
     // compiler can count outstanding loads and keep the newer stage in
     // flight while the older one is waited for.
-    auto gload = [&](int kb, u32x4 (&a)[A_LOADS], u32x4 (&b)[B_LOADS], float &sc) __attribute__((always_inline)) {
+    auto gload = [&](int kbw, u32x4 (&a)[A_LOADS], u32x4 (&b)[B_LOADS], float &sc) __attribute__((always_inline)) {
+        const int kb = PAIR && kbw >= KB ? kbw - KB : kbw;  // the activation block
 #pragma unroll
         for (int i = 0; i < A_LOADS; i++) {
             if constexpr (AF == AF_X3) {
@@ -171,17 +174,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; i++) {
-            const int idx = tid + 256 * i, col = idx >> 1, part = idx & 1;
-            const int gc = min(n0 + col, N - 1);
-            const unsigned char *src = reinterpret_cast<const unsigned char *>(Wq) + ((size_t)kb * N + gc) * QB;
-            if constexpr (WF == WF_Q8) {
+            const int idx = tid + 256 * i, col = PAIR ? idx >> 2 : idx >> 1, part = PAIR ? idx & 3 : idx & 1;
+            const int gc = min(n0 + min(col, BN - 1), N - 1);
+            const unsigned char *src = reinterpret_cast<const unsigned char *>(Wq) + ((size_t)kbw * N + gc) * QB;
+            if constexpr (WF == WF_Q8 || PAIR) {
                 b[i] = *reinterpret_cast<const u32x4 *>(src + part * 16);
             } else {
                 const uint2 h = *reinterpret_cast<const uint2 *>(src + part * 8);
                 b[i] = u32x4{h.x, h.y, 0u, 0u};
             }
         }
-        sc = Wsc[(size_t)kb * N + min(n0 + min(tid, BN - 1), N - 1)];
+        sc = Wsc[(size_t)kbw * N + min(n0 + min(tid, BN - 1), N - 1)];
     };
 
     auto sstore = [&](int stg, const u32x4 (&a)[A_LOADS], const u32x4 (&b)[B_LOADS], float sc) __attribute__((always_inline)) {
@@ -217,10 +220,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; i++) {
-            const int idx = tid + 256 * i, col = idx >> 1, part = idx & 1;
+            const int idx = tid + 256 * i, col = PAIR ? idx >> 2 : idx >> 1, part = PAIR ? idx & 3 : idx & 1;
             if (idx >= B_ITEMS) continue;
             const unsigned w[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
-            if constexpr (WF == WF_Q8 && LIMB == LIMB_F16X2) {
+            if constexpr (PAIR) {
+                // 8 f16 quants = elements 8*part .. 8*part+7
+                *reinterpret_cast<u32x4 *>(&Bl[col * XL + part * 8]) = b[i];
+            } else if constexpr (WF == WF_Q8 && LIMB == LIMB_F16X2) {
                 // 16 int8 = elements 16*part .. 16*part+15.  Biased byte u = q + 128 placed
                 // under the f16 exponent of 1024 reads as 1024 + u; subtracting 1152 leaves q.
                 unsigned o[8];
@@ -330,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     };
 
     // k-blocks [kb0, kend) of this split (all of K without split-K)
-    const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kend = SPLIT ? min(KB, kb0 + kps) : KB;
+    const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kend = SPLIT ? min(KBW, kb0 + kps) : KBW;
     // Prefetches past the last block re-read the last block (unused), so every
     // path issues the same loads and the waits count only the older stage.
     gload(kb0, ra[0], rb[0], rs[0]);
@@ -455,7 +461,7 @@ hipError_t launch_splitk_reduce(const float *part, int S, int M, int N, const fl
 template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
 static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy, int M,
                               const PartialBuf *pb, hipStream_t st) {
-    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN, KB = W.K / 32;
+    const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN, KB = W.K / 32 * (WF == WF_F16P ? 2 : 1);
     // Split K when the tiles alone leave the GPU mostly idle: up to ~1024
     // workgroups, at least 4 k-blocks per split, partials within pb.  Only
     // the 64x64 tile (the one chosen for small problems) is built with it.
@@ -519,6 +525,51 @@ static hipError_t launch_x3_epi(const DevMatrix &W, const void *X, int ldx, cons
     }
 }
 
+// Pair copy of an FP32 k-block-major matrix, one thread per (k-block, column):
+// d = 2^(e - 14) for the block's largest magnitude m in [2^e, 2^(e+1)), so
+// w / d (exact) is below 2^15; hi = f16(w / d), lo = f16(w / d - hi).
+__global__ __launch_bounds__(256) void k_pair_f16(const float *__restrict__ w, int N, int KB,
+                                                  unsigned short *__restrict__ p16, float *__restrict__ psc) {
+    const size_t blk = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= (size_t)KB * N) return;
+    const float4 *src = reinterpret_cast<const float4 *>(w + blk * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) *reinterpret_cast<float4 *>(&v[4 * i]) = src[i];
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(v[i]));
+    const int e = mx > 0.0f && __builtin_isfinite(mx) ? max(ilogbf(mx) - 14, -126) : 0;
+    unsigned hi[16], lo[16];
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+        const float x0 = ldexpf(v[i], -e), x1 = ldexpf(v[i + 1], -e);
+        const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+        const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+        hi[i / 2] = __builtin_bit_cast(unsigned short, h0) | (unsigned)__builtin_bit_cast(unsigned short, h1) << 16;
+        lo[i / 2] = __builtin_bit_cast(unsigned short, l0) | (unsigned)__builtin_bit_cast(unsigned short, l1) << 16;
+    }
+    u32x4 *dh = reinterpret_cast<u32x4 *>(p16 + blk * 32);
+    u32x4 *dl = reinterpret_cast<u32x4 *>(p16 + ((size_t)KB * N + blk) * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        dh[i] = u32x4{hi[4 * i], hi[4 * i + 1], hi[4 * i + 2], hi[4 * i + 3]};
+        dl[i] = u32x4{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]};
+    }
+    const float d = ldexpf(1.0f, e);
+    psc[blk] = d;
+    psc[(size_t)KB * N + blk] = d;
+}
+
+hipError_t launch_pair_f16(const DevMatrix &W, unsigned short *p16, float *psc, hipStream_t st) {
+    if (W.fmt != WF_F32 || W.K % 32 || !W.q || !p16 || !psc) return hipErrorInvalidValue;
+    const size_t blocks = (size_t)(W.K / 32) * W.N;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pair_f16, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const float *>(W.q), W.N, W.K / 32, p16, psc);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
                           int M, int epi, const PartialBuf *pb, hipStream_t st) {
     if (M <= 0) return hipSuccess;
@@ -528,6 +579,12 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     // FP32 activations: f16 two-limb split unless CIH_LIMBS=bf16x3
     const char *lv = getenv("CIH_LIMBS");
     const bool bf16 = (lv && !strcmp(lv, "bf16x3")) || full_range_mode();
+    if (W.fmt == WF_F16P) {
+        if (a_fmt == AF_H2) return launch_x3_epi<WF_F16P, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (a_fmt == AF_F32 && !bf16)
+            return launch_x3_epi<WF_F16P, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        return hipErrorInvalidValue;
+    }
     if (a_fmt == AF_H2) {
         if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
         if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);

@@ -13,7 +13,10 @@ namespace cih {
 //   F32: w  [K/32][N][32] float
 //   Q8 : qs [K/32][N][32] int8,   sc [K/32][N] float
 //   Q4 : qs [K/32][N][16] uint8,  sc [K/32][N] float   (reference nibble order)
-enum WFmt { WF_F32 = 0, WF_Q8 = 1, WF_Q4 = 2 };
+// WF_F16P: FP32 weights as two f16 limbs per 32-wide block scale (the pair
+// copy of an FP32 matrix, p16/psc below): block kb of K holds hi(w / d), block
+// KB + kb lo(w / d), so the quantized GEMM multiplies [X | X] by [Whi | Wlo].
+enum WFmt { WF_F32 = 0, WF_Q8 = 1, WF_Q4 = 2, WF_F16P = 3 };
 
 // GEMM epilogue applied to v = acc + bias[n]; EPI_GELU_X3 / EPI_GELU_H2 write
 // gelu(v) in the limb formats of x3.h (for the next quantized GEMM).
@@ -98,6 +101,13 @@ struct DevMatrix {
     // order of the block, Q4_0 nibbles already minus 8): the operand of the
     // LDS-staged GEMM.  Same values as q, so the same products.
     const unsigned short *q16 = nullptr;
+    // Optional pair copy of an FP32 matrix: p16 [2K/32][N][32] f16 (blocks
+    // 0..K/32-1: hi = f16(w / d), blocks K/32..: lo = f16(w / d - hi)), psc
+    // [2K/32][N] the power-of-two block scales d (stored for both halves).
+    // hi + lo keeps 22 significant bits of w; the f16-MFMA GEMM takes it
+    // instead of FP32 MFMA (CIH_QGEMM=fp32 or full range: the FP32 kernel).
+    const unsigned short *p16 = nullptr;
+    const float *psc = nullptr;
 };
 
 // Workgroup -> output tile: consecutive workgroup ids go to the 8 XCDs in
@@ -199,6 +209,8 @@ hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias,
                            hipStream_t st, const QkvOut *qo = nullptr);
 // W.q16 from W.q (quantized W, k-block-major), on stream st.
 hipError_t launch_expand_f16(const DevMatrix &W, unsigned short *q16, hipStream_t st);
+// The pair copy (p16, psc) of an FP32 matrix W, on stream st.
+hipError_t launch_pair_f16(const DevMatrix &W, unsigned short *p16, float *psc, hipStream_t st);
 
 // Dequantizes nblocks of a device matrix in k-block-major layout back to the
 // reference's row-major [N][K] FP32 (test path).

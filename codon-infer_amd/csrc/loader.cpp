@@ -325,6 +325,13 @@ int stage(int device, int fd, const std::vector<Region> &regs, uint8_t *img) {
 
 int wfmt(int dtype) { return dtype == DT_Q8 ? WF_Q8 : (dtype == DT_Q4 ? WF_Q4 : WF_F32); }
 
+// FP32 matrices also keep the f16 pair copy (4.25 bytes per weight) for the
+// f16-limb GEMM; CIH_F32_PAIR=0 leaves it out (FP32 MFMA only).
+bool pair_copies() {
+    const char *e = getenv("CIH_F32_PAIR");
+    return !(e && !strcmp(e, "0"));
+}
+
 // Device buffers are carved from one allocation: plan (sizes, jobs), then
 // allocate, then point and launch.
 struct Plan {
@@ -339,6 +346,7 @@ struct Plan {
     std::vector<Job> jobs;
     std::vector<CopySeg> copies;
     std::vector<DevMatrix *> expand;  // matrices that also get the f16 copy of their quants
+    std::vector<DevMatrix *> pairs;   // FP32 matrices that also get the f16 pair copy
 
     size_t take(size_t b) {
         const size_t off = (bytes + 255) & ~(size_t)255;
@@ -356,6 +364,11 @@ struct Plan {
         const size_t blocks = (size_t)(K / 32) * Ntot;
         if (dst_dt == DT_FP32) {
             fix.push_back({&M.q, take(blocks * 128)});
+            if (pair_copies()) {
+                fix.push_back({(const void **)&M.p16, take(blocks * 128)});
+                fix.push_back({(const void **)&M.psc, take(blocks * 8)});
+                pairs.push_back(&M);
+            }
         } else {
             fix.push_back({&M.q, take(blocks * (block_bytes(dst_dt) - 4))});
             fix.push_back({(const void **)&M.sc, take(blocks * 4)});
@@ -438,6 +451,9 @@ int build_from_image(cih_model *m, const Layout &y, int dst_dt, const uint8_t *i
     }
     for (size_t i = 0; e == hipSuccess && i < p.expand.size(); i++)
         e = launch_expand_f16(*p.expand[i], const_cast<unsigned short *>(p.expand[i]->q16), m->stream);
+    for (size_t i = 0; e == hipSuccess && i < p.pairs.size(); i++)
+        e = launch_pair_f16(*p.pairs[i], const_cast<unsigned short *>(p.pairs[i]->p16),
+                            const_cast<float *>(p.pairs[i]->psc), m->stream);
     if (e == hipSuccess) e = launch_copy_segments(img, arena, segs, (int)p.copies.size(), m->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
     if (segs) hipFree(segs);
@@ -492,7 +508,7 @@ int create(const cih_config &cfg, const Layout &y, int dst_dt, int fd, const std
 
 }  // namespace
 
-int upload_matrix(cih_model *m, int src_dt, int dst_dt, int K, const std::vector<Part> &parts, DevMatrix &out) {
+int upload_matrix(cih_model *m, int src_dt, int dst_dt, int K, const std::vector<Part> &parts, DevMatrix &out, bool pair) {
     if (src_dt != dst_dt && src_dt != DT_FP32) return set_error(CIH_ERR_ARG, "cannot convert dtype %d to %d", src_dt, dst_dt);
     int Ntot = 0;
     int64_t raw = 0;
@@ -528,6 +544,17 @@ int upload_matrix(cih_model *m, int src_dt, int dst_dt, int K, const std::vector
         if (e == hipSuccess) e = launch_load_matrix(img + at, wfmt(src_dt), parts[i].N, out, n_off, nullptr);
         at += b;
         n_off += parts[i].N;
+    }
+    if (e == hipSuccess && dst_dt == DT_FP32 && pair && pair_copies()) {
+        unsigned short *p16 = nullptr;
+        float *psc = nullptr;
+        e = dalloc(p16, blocks * 64, m->allocs);
+        if (e == hipSuccess) e = dalloc(psc, blocks * 2, m->allocs);
+        if (e == hipSuccess) {
+            out.p16 = p16;
+            out.psc = psc;
+            e = launch_pair_f16(out, p16, psc, nullptr);
+        }
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     hipFree(img);

@@ -195,6 +195,8 @@ struct Part {
 // dtype src_dt (one H2D copy, repack on the GPU), stored as dst_dt: equal to
 // src_dt, or Q8_0 / Q4_0 quantized on the GPU from FP32.  Buffers go to
 // m->allocs.
-int upload_matrix(cih_model *m, int src_dt, int dst_dt, int K, const std::vector<Part> &parts, DevMatrix &out);
+// pair: FP32 destinations also get the f16 pair copy (CIH_F32_PAIR=0: never)
+int upload_matrix(cih_model *m, int src_dt, int dst_dt, int K, const std::vector<Part> &parts, DevMatrix &out,
+                  bool pair = false);
 
 }  // namespace cih
