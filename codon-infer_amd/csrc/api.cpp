@@ -124,7 +124,8 @@ namespace {
 namespace cih {
 
 hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, const void *X, int ldx, int a_fmt,
-                      const float *bias, void *Y, int ldy, int M, int epi) {
+                      const float *bias, void *Y, int ldy, int M, int epi, int *defer) {
+    if (defer) *defer = 0;
     const double flops = 2.0 * M * W.N * W.K;
     const double in_b = a_fmt == AF_X3 ? 6.0 : 4.0, out_b = epi == EPI_GELU_X3 ? 6.0 : 4.0;  // H2: 4 B/element
     const double bytes = wbytes(W) + in_b * M * W.K + out_b * M * W.N * (epi == EPI_RESIDUAL ? 2 : 1);
@@ -133,7 +134,7 @@ hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, co
         return launch_gemv(W, (const float *)X, ldx, M, bias, (float *)Y, ldy, epi, pb, m->stream);
     if (gemv16_applies(W, a_fmt, M, epi))
         return launch_gemv16(W, (const unsigned short *)X, M, bias, Y, ldy, epi, &pb, m->stream);
-    return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, &pb, m->stream);
+    return launch_gemm(W, X, ldx, a_fmt, bias, Y, ldy, M, epi, &pb, m->stream, defer);
 }
 
 void profile_collect(cih_model *m) {
@@ -183,8 +184,8 @@ void rope_tables_host(size_t max_len, int hd, std::vector<float> &c, std::vector
 namespace {
 
 hipError_t gemm(cih_model *m, const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
-                int M, int epi) {
-    return model_gemm(m, m->ws.part, W, X, ldx, a_fmt, bias, Y, ldy, M, epi);
+                int M, int epi, int *defer = nullptr) {
+    return model_gemm(m, m->ws.part, W, X, ldx, a_fmt, bias, Y, ldy, M, epi, defer);
 }
 
 }  // namespace
@@ -384,6 +385,9 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     float *const part_a = ws.part.part, *const part_b = ws.part.part + part_half;
     int pend_splits = 0;  // FC2 splits waiting in part_a
     const float *pend_bias = nullptr;
+    // split residual projections of the other paths defer their splits to the
+    // LayerNorm after them (which writes FP32 or f16 limbs)
+    const bool defer_ok = (af == AF_F32 || af == AF_H2) && d % 32 == 0 && d <= 8192;
     // K/V tile images: the QKV projection's epilogue rotates K, splits K and V
     // into f16 limbs and lays them out as attention's LDS tiles, once per
     // key; attention copies them (CIH_ATT_IMG=0: K/V as FP32 rows, staged by
@@ -522,7 +526,11 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         }
         {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-            HIPCHK(launch_layernorm(ws.x, ly.ln1w, ly.ln1b, ws.xb, af, T, d, st));
+            if (pend_splits)
+                HIPCHK(launch_residual_layernorm(ws.x, part_a, pend_splits, pend_bias, ly.ln1w, ly.ln1b, ws.xb, af, T,
+                                                 d, st));
+            else
+                HIPCHK(launch_layernorm(ws.x, ly.ln1w, ly.ln1b, ws.xb, af, T, d, st));
         }
         if (epi_img) {
             const double bytes = wbytes(ly.wqkv) + 4.0 * T * d + 4.0 * T * 3 * d;
@@ -556,13 +564,23 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             ProfScope ps(m, CIH_KC_OTHER, 0, 0);
             HIPCHK(launch_head_mean(P, pb, ph, H, sm, t_final, st));
         }
-        HIPCHK(gemm(m, ly.wo, ws.ao, d, af, ly.bo, ws.x, d, T, EPI_RESIDUAL));
+        // A residual projection that splits K leaves its partial sums for the
+        // LayerNorm after it (k_rln adds them, the bias and the residual):
+        // Wo's for LN2, FC2's for the next layer's LN1 or the final LN.
+        int so = 0, s2 = 0;
+        HIPCHK(gemm(m, ly.wo, ws.ao, d, af, ly.bo, ws.x, d, T, EPI_RESIDUAL, defer_ok ? &so : nullptr));
         {
-            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-            HIPCHK(launch_layernorm(ws.x, ly.ln2w, ly.ln2b, ws.xb, af, T, d, st));
+            ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d + 4.0 * so * T * d);
+            if (so)
+                HIPCHK(launch_residual_layernorm(ws.x, part_a, so, ly.bo, ly.ln2w, ly.ln2b, ws.xb, af, T, d, st));
+            else
+                HIPCHK(launch_layernorm(ws.x, ly.ln2w, ly.ln2b, ws.xb, af, T, d, st));
         }
         HIPCHK(gemm(m, ly.w1, ws.xb, d, af, ly.b1, ws.hbuf, F, T, epi_fc1));
-        HIPCHK(gemm(m, ly.w2, ws.hbuf, F, af, ly.b2, ws.x, d, T, EPI_RESIDUAL));
+        HIPCHK(gemm(m, ly.w2, ws.hbuf, F, af, ly.b2, ws.x, d, T, EPI_RESIDUAL,
+                    defer_ok && !want_layer ? &s2 : nullptr));
+        pend_splits = s2;
+        pend_bias = ly.b2;
         if (want_layer) HIPCHK(launch_scatter_rows(ws.x, d, sm, t_layer + (size_t)l * S_max * d, (int64_t)L * S_max * d, st));
     }
     if (want_contacts) {

@@ -25,31 +25,22 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int FEW_THREADS = 256;
 constexpr int RLN_MAX_THREADS = 1024;
 
-// sum over the workgroup's waves (added in order); red: one float per wave
-__device__ __forceinline__ float wg_sum(float v, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    __syncthreads();  // red free from a previous use
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const int nw = blockDim.x >> 6;
-    float r = red[0];
-    for (int i = 1; i < nw; i++) r += red[i];
-    return r;
-}
-
 }  // namespace
 
 // One workgroup per row; thread t owns column quads t, t + blockDim, ... (Q of
 // them), so that every partial sum of a row is requested at once.  part (may
 // be null): [S][rows][d] partial sums of the projection whose residual is
-// added, with bias pb.
+// added, with bias pb (x + (sum + bias), the split GEMM's reduction order).
+// The row's mean and variance are then formed by wave 0 exactly as
+// k_layernorm4 forms them (lane l sums quads l, l + 64, ... in order, then a
+// butterfly), so the output does not depend on which kernel normalised it.
 template <int Q, int OF>
 __global__ __launch_bounds__(RLN_MAX_THREADS) void k_rln(float *__restrict__ x, const float *__restrict__ part, int S,
                                                          const float *__restrict__ pb, const float *__restrict__ w,
                                                          const float *__restrict__ b, void *__restrict__ out,
                                                          int rows, int d, int *__restrict__ flag) {
-    __shared__ float red[RLN_MAX_THREADS / 64];
+    __shared__ f32x4 xs[Q * RLN_MAX_THREADS];
+    __shared__ float stat[2];
     const int row = blockIdx.x, n4 = d >> 2, nt = blockDim.x;
     f32x4 *xr = reinterpret_cast<f32x4 *>(x + (size_t)row * d);
     f32x4 v[Q], g[Q], be[Q];
@@ -71,21 +62,33 @@ __global__ __launch_bounds__(RLN_MAX_THREADS) void k_rln(float *__restrict__ x, 
             if ((int)threadIdx.x + nt * i < n4) xr[c] = v[i];
         }
     }
-    float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < Q; i++)
-        if ((int)threadIdx.x + nt * i < n4) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    const float mean = wg_sum(s, red) / (float)d;
-    float q = 0.0f;
+        if ((int)threadIdx.x + nt * i < n4) xs[threadIdx.x + nt * i] = v[i];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float s = 0.0f;
+        for (int c = lane; c < n4; c += 64) s += (xs[c].x + xs[c].y) + (xs[c].z + xs[c].w);
 #pragma unroll
-    for (int i = 0; i < Q; i++) {
-        const f32x4 t = v[i] - mean;
-        if ((int)threadIdx.x + nt * i < n4) q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+        const float mean = s / (float)d;
+        float q = 0.0f;
+        for (int c = lane; c < n4; c += 64) {
+            const f32x4 t = xs[c] - mean;
+            q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+        const float var = q / (float)d;
+        if (lane == 0) {
+            stat[0] = mean;
+            stat[1] = 1.0f / sqrtf(var + 1e-5f);
+            if (flag && !(__builtin_isfinite(mean) && __builtin_isfinite(var))) atomicOr(flag, FLAG_NONFINITE);
+        }
     }
-    const float var = wg_sum(q, red) / (float)d;
-    const float inv = 1.0f / sqrtf(var + 1e-5f);
-    if (flag && threadIdx.x == 0 && !(__builtin_isfinite(mean) && __builtin_isfinite(var)))
-        atomicOr(flag, FLAG_NONFINITE);
+    __syncthreads();
+    const float mean = stat[0], inv = stat[1];
 #pragma unroll
     for (int i = 0; i < Q; i++) {
         const int c = threadIdx.x + nt * i;

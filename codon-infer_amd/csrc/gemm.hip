@@ -349,7 +349,8 @@ static hipError_t launch_epi(const DevMatrix &W, const float *X, int ldx, const 
 }
 
 hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, const float *bias, void *Yv, int ldy,
-                       int M, int epi, const PartialBuf *pb, hipStream_t st) {
+                       int M, int epi, const PartialBuf *pb, hipStream_t st, int *defer) {
+    if (defer) *defer = 0;
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0) return hipErrorInvalidValue;
     // Quantized weights go to the 16-bit-limb MFMA kernel (FP32 or pre-split
@@ -358,7 +359,7 @@ hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, c
     const char *path = getenv("CIH_QGEMM");
     const bool fp32_path = path && !strcmp(path, "fp32");
     if (W.fmt != WF_F32) {
-        if (a_fmt != AF_F32 || !fp32_path) return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st);
+        if (a_fmt != AF_F32 || !fp32_path) return launch_gemm_x3(W, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st, defer);
     }
     // FP32 weights with a pair copy: the same f16-limb GEMM on [hi | lo]
     // (CIH_QGEMM=fp32, CIH_LIMBS=bf16x3 and full range keep FP32 MFMA)
@@ -371,7 +372,7 @@ hipError_t launch_gemm(const DevMatrix &W, const void *Xv, int ldx, int a_fmt, c
         P.K = W.K;
         P.q = W.p16;
         P.sc = W.psc;
-        return launch_gemm_x3(P, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st);
+        return launch_gemm_x3(P, Xv, ldx, a_fmt, bias, Yv, ldy, M, epi, pb, st, defer);
     }
     if (a_fmt != AF_F32 || epi == EPI_GELU_X3 || epi == EPI_GELU_H2 || ldx % 4 != 0) return hipErrorInvalidValue;
     const float *X = reinterpret_cast<const float *>(Xv);

@@ -460,7 +460,7 @@ hipError_t launch_splitk_reduce(const float *part, int S, int M, int N, const fl
 
 template <int WF, int EPI, int BM, int BN, int AF, int LIMB>
 static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy, int M,
-                              const PartialBuf *pb, hipStream_t st) {
+                              const PartialBuf *pb, hipStream_t st, int *defer) {
     const int nM = (M + BM - 1) / BM, nN = (W.N + BN - 1) / BN, KB = W.K / 32 * (WF == WF_F16P ? 2 : 1);
     // Split K when the tiles alone leave the GPU mostly idle: up to ~1024
     // workgroups, at least 4 k-blocks per split, partials within pb.  Only
@@ -480,7 +480,8 @@ static hipError_t launch_x3_t(const DevMatrix &W, const void *X, int ldx, const 
     float *part = S > 1 ? pb->part : nullptr;
     hipLaunchKernelGGL((k_gemm_x3<WF, EPI, BM, BN, AF, LIMB, SPLIT>), dim3(nM * nN, S), dim3(256), 0, st, X, ldx, W.q, W.sc,
                        bias, Y, ldy, M, W.N, W.K, kps, part);
-    if (S > 1)
+    if (defer) *defer = S > 1 ? S : 0;  // the caller adds the splits (and bias, epilogue) itself
+    else if (S > 1)
         hipLaunchKernelGGL(k_splitk_reduce, dim3((M * W.N + 255) / 256), dim3(256), 0, st, part, S, M, W.N, bias, Y,
                            ldy, EPI);
     return hipGetLastError();
@@ -502,26 +503,27 @@ static void pick_tile(int M, int N, int &bm, int &bn) {
 
 template <int WF, int EPI, int AF, int LIMB>
 static hipError_t launch_x3_shape(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
-                                  int M, const PartialBuf *pb, hipStream_t st) {
+                                  int M, const PartialBuf *pb, hipStream_t st, int *defer) {
     int bm, bn;
     pick_tile(M, W.N, bm, bn);
-    if (bm == 128 && bn == 128) return launch_x3_t<WF, EPI, 128, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
-    if (bm == 128) return launch_x3_t<WF, EPI, 128, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
-    if (bn == 128) return launch_x3_t<WF, EPI, 64, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
-    return launch_x3_t<WF, EPI, 64, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    if (defer) *defer = 0;
+    if (bm == 128 && bn == 128) return launch_x3_t<WF, EPI, 128, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
+    if (bm == 128) return launch_x3_t<WF, EPI, 128, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
+    if (bn == 128) return launch_x3_t<WF, EPI, 64, 128, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
+    return launch_x3_t<WF, EPI, 64, 64, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
 }
 
 template <int WF, int AF, int LIMB>
 static hipError_t launch_x3_epi(const DevMatrix &W, const void *X, int ldx, const float *bias, void *Y, int ldy,
-                                int M, int epi, const PartialBuf *pb, hipStream_t st) {
+                                int M, int epi, const PartialBuf *pb, hipStream_t st, int *defer) {
     switch (epi) {
-    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
-    case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    case EPI_GELU: return launch_x3_shape<WF, EPI_GELU, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
+    case EPI_GELU_X3: return launch_x3_shape<WF, EPI_GELU_X3, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
     case EPI_GELU_H2:
-        if constexpr (LIMB == LIMB_F16X2) return launch_x3_shape<WF, EPI_GELU_H2, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+        if constexpr (LIMB == LIMB_F16X2) return launch_x3_shape<WF, EPI_GELU_H2, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
         return hipErrorInvalidValue;
-    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
-    default: return launch_x3_shape<WF, EPI_NONE, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st);
+    case EPI_RESIDUAL: return launch_x3_shape<WF, EPI_RESIDUAL, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
+    default: return launch_x3_shape<WF, EPI_NONE, AF, LIMB>(W, X, ldx, bias, Y, ldy, M, pb, st, defer);
     }
 }
 
@@ -571,7 +573,8 @@ hipError_t launch_pair_f16(const DevMatrix &W, unsigned short *p16, float *psc, 
 }
 
 hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y, int ldy,
-                          int M, int epi, const PartialBuf *pb, hipStream_t st) {
+                          int M, int epi, const PartialBuf *pb, hipStream_t st, int *defer) {
+    if (defer) *defer = 0;
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
     if ((epi == EPI_GELU_X3 || epi == EPI_GELU_H2) && W.N % 32 != 0) return hipErrorInvalidValue;
@@ -580,23 +583,23 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     const char *lv = getenv("CIH_LIMBS");
     const bool bf16 = (lv && !strcmp(lv, "bf16x3")) || full_range_mode();
     if (W.fmt == WF_F16P) {
-        if (a_fmt == AF_H2) return launch_x3_epi<WF_F16P, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (a_fmt == AF_H2) return launch_x3_epi<WF_F16P, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
         if (a_fmt == AF_F32 && !bf16)
-            return launch_x3_epi<WF_F16P, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+            return launch_x3_epi<WF_F16P, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
         return hipErrorInvalidValue;
     }
     if (a_fmt == AF_H2) {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_H2, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
     } else if (a_fmt == AF_X3) {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_X3, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
     } else if (bf16) {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_BF16X3>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
     } else {
-        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
-        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st);
+        if (W.fmt == WF_Q8) return launch_x3_epi<WF_Q8, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
+        if (W.fmt == WF_Q4) return launch_x3_epi<WF_Q4, AF_F32, LIMB_F16X2>(W, X, ldx, bias, Y, ldy, M, epi, pb, st, defer);
     }
     return hipErrorInvalidValue;
 }

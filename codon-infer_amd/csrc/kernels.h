@@ -147,14 +147,17 @@ constexpr size_t SPLITK_PART_FLOATS = (size_t)1024 * 64 * 64;
 // Y[M][N] (row stride ldy) = epi(X[M][K] * W^T + bias).  X is FP32 with row
 // stride ldx (a_fmt AF_F32) or in a limb format of x3.h (AF_X3 / AF_H2,
 // quantized W only).  With pb, a GEMM too small to fill the GPU splits K
-// (CIH_SPLITK=0 disables).
+// (CIH_SPLITK=0 disables).  defer (may be null): a split GEMM of the f16-limb
+// kernel leaves its [*defer][M][N] partial sums in pb for the caller to add
+// (with bias and epilogue: the residual LayerNorm); *defer = 0 when the
+// output was written.
 hipError_t launch_gemm(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
-                       int ldy, int M, int epi, const PartialBuf *pb, hipStream_t st);
+                       int ldy, int M, int epi, const PartialBuf *pb, hipStream_t st, int *defer = nullptr);
 
 // Q8_0/Q4_0 GEMM on bf16 MFMA: exact integer weights, activations split
 // into three bf16 limbs (FP32-equivalent products), block scale in FP32.
 hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt, const float *bias, void *Y,
-                          int ldy, int M, int epi, const PartialBuf *pb, hipStream_t st);
+                          int ldy, int M, int epi, const PartialBuf *pb, hipStream_t st, int *defer = nullptr);
 
 // Weight-streaming GEMV for M <= GEMV_MAX_M tokens (FP32 activations, epilogue
 // EPI_NONE / EPI_GELU / EPI_RESIDUAL).  With several k-splits the partial sums

@@ -175,7 +175,7 @@ bool use_gemv(int M, int a_fmt, int epi);
 // Y = epi(X W^T + bias) on the model's stream: the weight-streaming GEMV for
 // a few FP32 rows, the MFMA GEMM otherwise; partial sums through pb.
 hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, const void *X, int ldx, int a_fmt,
-                      const float *bias, void *Y, int ldy, int M, int epi);
+                      const float *bias, void *Y, int ldy, int M, int epi, int *defer = nullptr);
 // After the stream has drained: adds the launches recorded since the last
 // call (event pairs of model_gemm and friends) to the per-class totals.
 void profile_collect(cih_model *m);
