@@ -1189,7 +1189,15 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     bool wide = (long)((sm.S_max + 255) / 256) * H * sm.B >= 512;
     if (qe && !strcmp(qe, "128")) wide = false;
     if (qe && !strcmp(qe, "256")) wide = true;
-    const int QB = wide ? 256 : 128, nq = (sm.S_max + QB - 1) / QB;
+    int QB = wide ? 256 : 128;
+    // With a probability export there is no key split: batches whose 128-query
+    // tasks do not cover the compute units take 64- or 32-query workgroups
+    // (the per-query arithmetic does not depend on the block: same bits).
+    if (P && !fp32 && !wide && !qe) {
+        const long t128 = (long)((sm.S_max + 127) / 128) * H * sm.B;
+        if (t128 < device_cus()) QB = t128 * 2 < device_cus() ? 32 : 64;
+    }
+    const int nq = (sm.S_max + QB - 1) / QB;
     const int tasks = sm.B * H * nq;
     // Key split (no probability export): when the tasks do not fill one round
     // of the 'slots' workgroups resident at once (two of 256 or four of 128
@@ -1226,6 +1234,8 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                          \
     else if (fp32) CIH_ATT_K(k_attention, HDV, true);                                                           \
     else if (P && wide) CIH_ATT_H(HDV, false, 512);                                                             \
+    else if (P && QB == 32) CIH_ATT_H(HDV, false, 64);                                                          \
+    else if (P && QB == 64) CIH_ATT_H(HDV, false, 128);                                                         \
     else if (P) CIH_ATT_H(HDV, false, 256);                                                                     \
     else if (wide) CIH_ATT_H(HDV, true, 512);                                                                   \
     else CIH_ATT_H(HDV, true, 256);                                                                             \
