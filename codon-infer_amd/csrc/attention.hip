@@ -71,6 +71,60 @@ __device__ __forceinline__ void store_p(float *Prow, const float (&p)[16], int k
     }
 }
 
+// One 32-key tile of the one-pass f16-limb kernels (staged and image), the
+// same arithmetic in both.  Per lane (query column, in both lane halves): m
+// the base-2 exponent offset, l the running sum, oacc the P V accumulators.
+// scores(acc, c0) leaves c0 + the tile's base-2 scores (the query is
+// pre-scaled) in acc; it is called with c0 = -m, so acc holds the exponents
+// themselves.  m moves, lazily, only when a score exceeds it by more than 8
+// (and at the first tile): then the accumulators are rescaled and the tile's
+// exponents shifted.  Register 8c + e of lane half hh holds key
+// kt0 + 16c + 8(e/4) + 4hh + e%4; keys from kend on are masked (MASKED).
+template <int DT, bool MASKED, class Scores, class PV>
+__device__ __forceinline__ void online_tile(float &m, float &l, f32x16 (&oacc)[DT], int kt0, int kend, int hh,
+                                            Scores &&scores, PV &&pv) {
+    const bool first = m == -INFINITY;
+    const float mc = first ? 0.0f : m;
+    f32x16 acc;
+    scores(acc, -mc);
+    float sv[16];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        float v = acc[q];
+        if constexpr (MASKED) {
+            const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+            v = key < kend ? v : -INFINITY;
+        }
+        sv[q] = v;
+        tmax = fmaxf(tmax, v);
+    }
+    // key kt0 (< kend) sits in half 0, so the combined tile max is finite
+    const float tm = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const bool need = first || tm > 8.0f;
+    if (__ballot(need)) {
+        const float mn = need ? tm + mc : m;
+        const float corr = __builtin_amdgcn_exp2f(m - mn);
+        l *= corr;
+        m = mn;
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
+        const float sh = need ? mn - mc : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) sv[q] -= sh;
+    }
+    float p[16], sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        p[q] = __builtin_amdgcn_exp2f(sv[q]);
+        sum += p[q];
+    }
+    l += sum;
+    pv(p);
+}
+
 // Sum of the lane's probabilities whose keys are residues (1 <= key <= len - 2).
 __device__ __forceinline__ float residue_sum(const float (&p)[16], int k0, int len) {
     float s = 0.0f;
@@ -396,7 +450,10 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
             Vl[bf * VBUF + c * V_LD + key] = (_Float16)0.0f;
         }
 
-    // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs
+    // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs; the
+    // one-pass kernel takes them pre-scaled by log2(e) / sqrt(hd), so its
+    // scores come out of the MFMAs in base-2 units
+    const float sl2 = inv_scale * 1.44269504088896340736f;
     const int qi = qblk + wave * 32 + li;
     const int qc = min(qi, len - 1);
     f16x8 qh[NC], ql[NC];
@@ -412,7 +469,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 float r = 0.0f;
                 if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
                 else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
-                v[e] = r;
+                v[e] = ONEPASS ? opaque(r * sl2) : r;
             }
             split8(v, qh[c], ql[c]);
         }
@@ -466,10 +523,10 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
             *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + pos]) = lv;
         }
     };
-    // S^T tile (32 keys x 32 queries): A = K rows (keys), B = Q columns (queries)
-    auto scores = [&](f32x16 &acc) {
+    // S^T tile (32 keys x 32 queries) + c0: A = K rows (keys), B = Q columns (queries)
+    auto scores = [&](f32x16 &acc, float c0) {
 #pragma unroll
-        for (int q = 0; q < 16; q++) acc[q] = 0.0f;
+        for (int q = 0; q < 16; q++) acc[q] = c0;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const f16x8 kh = *reinterpret_cast<const f16x8 *>(&Kh[cur * KBUF + li * K_LD + 16 * c + 8 * hh]);
@@ -506,54 +563,22 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
     float out_scale;
     if constexpr (ONEPASS) {
-        // One pass, online softmax (see k_attention) in base 2: scores are
+        // One pass, online softmax (see k_attention) in base 2: the query is
         // pre-scaled by log2(e) / sqrt(hd) so every exponential is one
-        // v_exp_f32.  Whole tiles skip the key mask.  The exponent offset m
-        // follows the running max lazily (it moves only when a score exceeds
-        // it by more than 8, so p <= 256), which leaves the accumulators
-        // unscaled on most tiles; o / l is unchanged.
-        const float sl2 = inv_scale * 1.44269504088896340736f;
+        // v_exp_f32, and the MFMAs start from -m, so their results are the
+        // exponents themselves.  Whole tiles skip the key mask.  The exponent
+        // offset m follows the running max lazily (it moves only when a score
+        // exceeds it by more than 8, so p <= 256), which leaves the
+        // accumulators unscaled on most tiles; o / l is unchanged.
         float m = -INFINITY, l = 0.0f;
         auto tile = [&](int kt0, auto masked) {
             __syncthreads();
             load_k(kt0);
             load_v(kt0);
             __syncthreads();
-            f32x16 acc;
-            scores(acc);
-            float sv[16];
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                float v = acc[q] * sl2;
-                if constexpr (decltype(masked)::value) {
-                    const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                    v = key < kend ? v : -INFINITY;
-                }
-                sv[q] = v;
-                tmax = fmaxf(tmax, v);
-            }
-            // key kt0 (< kend) sits in half 0, so the combined tile max is finite;
-            // the offset m moves only when a score exceeds it by more than 8
-            const float tm = fmaxf(tmax, __shfl_xor(tmax, 32));
-            if (__ballot(tm > m + 8.0f)) {
-                const float mn = tm > m + 8.0f ? tm : m;
-                const float corr = __builtin_amdgcn_exp2f(m - mn);
-                l *= corr;
-                m = mn;
-#pragma unroll
-                for (int t = 0; t < DT; t++)
-#pragma unroll
-                    for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
-            }
-            float p[16], sum = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                p[q] = __builtin_amdgcn_exp2f(sv[q] - m);
-                sum += p[q];
-            }
-            l += sum;
-            pv(oacc, p);
+            online_tile<DT, decltype(masked)::value>(m, l, oacc, kt0, kend, hh,
+                                                     [&](f32x16 &acc, float c0) { scores(acc, c0); },
+                                                     [&](const float (&p)[16]) { pv(oacc, p); });
         };
         int kt0 = kbeg;
         for (; kt0 + 32 <= kend; kt0 += 32) tile(kt0, std::false_type{});
@@ -676,7 +701,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         float m = -INFINITY, l = 0.0f;
         sweep(false, [&](int kt0) __attribute__((always_inline)) {
             f32x16 acc;
-            scores(acc);
+            scores(acc, 0.0f);
             float sv[16];
             float tmax = -INFINITY;
 #pragma unroll
@@ -702,7 +727,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         float rs = 0.0f;  // sum of this query's probabilities over residue keys (contacts)
         sweep(true, [&](int kt0) __attribute__((always_inline)) {
             f32x16 acc;
-            scores(acc);
+            scores(acc, 0.0f);
             float p[16];
 #pragma unroll
             for (int q = 0; q < 16; q++) {
@@ -830,6 +855,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     const float sl2 = inv_scale * 1.44269504088896340736f;
 
     // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs
+    // (pre-scaled by log2(e) / sqrt(hd) in the one-pass kernel, as in k_attention_h)
     const int qi = qblk + wave * 32 + li;
     const int qc = min(qi, len - 1);
     f16x8 qh[NC], ql[NC];
@@ -845,7 +871,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 float r = 0.0f;
                 if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
                 else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
-                v[e] = r;
+                v[e] = ONEPASS ? opaque(r * sl2) : r;
             }
             split8_mix(v, qh[c], ql[c]);
         }
@@ -864,10 +890,10 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
             if (j < nj) dma16(src + j * 1024, __builtin_amdgcn_readfirstlane(lds0 + stg * TB + j * 1024));
         }
     };
-    // S^T tile (32 keys x 32 queries) from stage st
-    auto scores = [&](const unsigned char *st, f32x16 &acc) __attribute__((always_inline)) {
+    // S^T tile (32 keys x 32 queries) + c0 from stage st
+    auto scores = [&](const unsigned char *st, f32x16 &acc, float c0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < 16; q++) acc[q] = 0.0f;
+        for (int q = 0; q < 16; q++) acc[q] = c0;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int dim = 16 * c + 8 * hh;
@@ -926,40 +952,9 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     if constexpr (ONEPASS) {
         float m = -INFINITY, l = 0.0f;
         sweep(std::true_type{}, [&](const unsigned char *st, int kt0, auto masked) __attribute__((always_inline)) {
-            f32x16 acc;
-            scores(st, acc);
-            float sv[16];
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                float v = acc[q] * sl2;
-                if constexpr (decltype(masked)::value) {
-                    const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                    v = key < kend ? v : -INFINITY;
-                }
-                sv[q] = v;
-                tmax = fmaxf(tmax, v);
-            }
-            // key kt0 (< kend) sits in half 0, so the combined tile max is finite
-            const float tm = fmaxf(tmax, __shfl_xor(tmax, 32));
-            if (__ballot(tm > m + 8.0f)) {
-                const float mn = tm > m + 8.0f ? tm : m;
-                const float corr = __builtin_amdgcn_exp2f(m - mn);
-                l *= corr;
-                m = mn;
-#pragma unroll
-                for (int t = 0; t < DT; t++)
-#pragma unroll
-                    for (int q = 0; q < 16; q++) oacc[t][q] *= corr;
-            }
-            float p[16], sum = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                p[q] = __builtin_amdgcn_exp2f(sv[q] - m);
-                sum += p[q];
-            }
-            l += sum;
-            pv(st, oacc, p);
+            online_tile<DT, decltype(masked)::value>(
+                m, l, oacc, kt0, kend, hh, [&](f32x16 &acc, float c0) { scores(st, acc, c0); },
+                [&](const float (&p)[16]) { pv(st, oacc, p); });
         });
         const float lt = l + __shfl_xor(l, 32);
         if (ns > 1) {
@@ -985,7 +980,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         float m = -INFINITY, l = 0.0f;
         sweep(std::false_type{}, [&](const unsigned char *st, int kt0, auto) __attribute__((always_inline)) {
             f32x16 acc;
-            scores(st, acc);
+            scores(st, acc, 0.0f);
             float sv[16];
             float tmax = -INFINITY;
 #pragma unroll
@@ -1011,7 +1006,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         float rs = 0.0f;
         sweep(std::true_type{}, [&](const unsigned char *st, int kt0, auto) __attribute__((always_inline)) {
             f32x16 acc;
-            scores(st, acc);
+            scores(st, acc, 0.0f);
             float p[16];
 #pragma unroll
             for (int q = 0; q < 16; q++) {
