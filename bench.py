@@ -42,12 +42,14 @@ PEAK_F16_MFMA_TFLOPS = 2500.0   # MI355X dense f16 matrix peak
 def qgemm_name(wname, T, d):
     """Which quantized GEMM the forward's projections take at T tokens: the
     LDS-staged kernel when even the narrowest projection (N = d) gives a full
-    round of 128 x 128 tiles and the f16 copy of the quants exists, else the
-    register-staged one (split-K for small T)."""
-    lds = (os.environ.get("CIH_GEMM_LDS") != "0" and os.environ.get("CIH_GEMM_F16") != "0"
+    round of 128 x 128 tiles (reading the f16 copy of the quants, or the quants
+    of a model loaded with CIH_GEMM_F16=0), else the register-staged one
+    (split-K for small T)."""
+    lds = (os.environ.get("CIH_GEMM_LDS") != "0"
            and (os.environ.get("CIH_GEMM_LDS") == "force" or -(-T // 128) * -(-d // 128) >= 256))
     if lds:
-        return f"k_gemm_lds<{wname}> f16 MFMA, 2 limbs, operands global->LDS (QKV, Wo, FC1, FC2)"
+        src = "quants" if os.environ.get("CIH_GEMM_F16") == "0" else "f16 copy of the quants"
+        return f"k_gemm_lds<{wname}> f16 MFMA, 2 limbs, operands global->LDS, W from the {src} (QKV, Wo, FC1, FC2)"
     return f"k_gemm_x3<{wname}> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)"
 
 

@@ -10,7 +10,9 @@
 //
 // What differs is the data movement:
 //   * the quants come from W.q16, an f16 copy made when the model is loaded,
-//     so no conversion runs in the loop and both operands are plain copies;
+//     so no conversion runs in the loop and both operands are plain copies
+//     (a model loaded without the copy: the quants themselves, 1 or 0.5 bytes
+//     per weight, converted on the LDS -> register path);
 //   * every k-block of A (BM rows x 128 B: 32 hi + 32 lo f16) and of W.q16
 //     (BN columns x 64 B) plus its BN scales is fetched with
 //     global_load_lds_dword{,x4}: the load unit writes LDS directly, nothing
@@ -50,16 +52,17 @@ typedef __attribute__((address_space(1))) void glb_ptr_t;
 // does not divide them, the waves with fewer real loads repeat their first
 // one (same source, same LDS bytes), so every wave issues NI loads per block
 // and the wait counts are the same in all waves.
-template <int RT, int CT, int WM, int WN> struct LdsTile {
+template <int RT, int CT, int WM, int WN, int BPC = 64> struct LdsTile {
     static constexpr int BM = WM * RT * 32, BN = WN * CT * 32, NW = WM * WN, THREADS = 64 * NW;
-    static constexpr int SA = BM * 128, SB = BN * 64, SS = BN * 4, STAGE = SA + SB + SS;
+    // BPC: bytes of W per column and block (64: the f16 copy; 32: Q8_0 quants; 16: Q4_0)
+    static constexpr int SA = BM * 128, SB = (BN * BPC + 1023) / 1024 * 1024, SS = BN * 4, STAGE = SA + SB + SS;
     static constexpr int LA = SA / 1024, LB = SB / 1024;
     static constexpr int NA = (LA + NW - 1) / NW, NB = (LB + NW - 1) / NW;
     static constexpr int SL = BN / NW;      // scales per wave and block (4-byte loads)
     static constexpr int NI = NA + NB + 1;  // load instructions per wave and block
     static constexpr int OCC = THREADS >= 512 ? 1 : 512 / THREADS;  // workgroups per CU
     static constexpr int WPE = NW / 4 * OCC;  // waves per SIMD (HIP's second launch bound)
-    static_assert(SA % 1024 == 0 && SB % 1024 == 0 && LA >= NW && LB >= NW, "loads");
+    static_assert(SA % 1024 == 0 && LA >= NW, "loads");
     static_assert(BN % NW == 0 && SL <= 64 && OCC * 3 * STAGE <= 160 * 1024, "tile");
 };
 
@@ -83,6 +86,15 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, Is...>, F 
 // both limbs, or a dim's 32 keys of both limbs) and stored a whole line per 8
 // lanes.  V goes this way when the 32 rows are exactly one key tile, element
 // by element otherwise (a sequence starting inside the 32 rows).
+constexpr int QKV_PP = 144;  // bytes per patch row: 128 + 16 (spreads the rows over the banks)
+
+// LDS bytes qkv_epilogue uses from the start of the kernel's LDS: the hd-64
+// partner exchange (odd CT) and one patch of 32 rows per wave.  The rows'
+// prefetched key indices and RoPE rows lie past both this and the stages.
+template <int HD, int RT, int CT, int WM, int WN> constexpr int qkv_epilogue_lds() {
+    return (HD == 64 && CT % 2 == 1 ? 2 * WM * RT * 16 * 64 * 4 : 0) + WM * WN * 32 * QKV_PP;
+}
+
 template <int HD, int RT, int CT, int WM, int WN, bool PREF>
 __device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned char *lds, const unsigned char *pre,
                                              int m0, int n0, int wm, int wn, int lane, int M, int N,
@@ -118,7 +130,7 @@ __device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned cha
                 for (int q = 0; q < 16; q++) xpart[r][q] = xch[((((1 - wn) * WM + wm) * RT + r) * 16 + q) * 64 + lane];
     }
     const bool has_k = n0 + (wn * CT + CT) * 32 > d && n0 + wn * CT * 32 < 2 * d;  // this wave has K columns
-    constexpr int PP = 144;  // bytes per patch row: 128 + 16 (spreads the rows over the banks)
+    constexpr int PP = QKV_PP;
     if constexpr (!(HD == 64 && CT % 2 == 1)) __syncthreads();  // every wave is done with the operand stages
     unsigned char *patch = lds + (HD == 64 && CT % 2 == 1 ? 2 * WM * RT * 16 * 64 * 4 : 0) + (wm * WN + wn) * 32 * PP;
     // P = parity of wn CT: hd-64 partner tiles are compile-time indices (ct ^ 1)
@@ -283,11 +295,17 @@ __device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned cha
     }
 }
 
-template <int EPI, int RT, int CT, int WM, int WN>
+// WQ: 0 = W from the f16 copy (W.q16); WF_Q8 / WF_Q4 = W from its quants
+// (W.q, a model loaded without the f16 copy), turned into f16 on the LDS ->
+// register path: v_perm puts each byte (Q8_0: + 128; Q4_0: the lane's
+// nibble) under the f16 exponent of 1024, a packed f16 subtraction removes
+// the offset (1.25 VALU per weight).
+template <int EPI, int RT, int CT, int WM, int WN, int WQ>
 __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
-    const unsigned short *__restrict__ X, const unsigned short *__restrict__ W16, const float *__restrict__ Wsc,
+    const unsigned short *__restrict__ X, const unsigned char *__restrict__ WB, const float *__restrict__ Wsc,
     const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo) {
-    using T = LdsTile<RT, CT, WM, WN>;
+    constexpr int BPC = WQ == WF_Q8 ? 32 : (WQ == WF_Q4 ? 16 : 64);
+    using T = LdsTile<RT, CT, WM, WN, BPC>;
     constexpr int BM = T::BM, BN = T::BN, NW = T::NW, SA = T::SA, SB = T::SB, STAGE = T::STAGE, NA = T::NA,
                   NB = T::NB, SL = T::SL;
     // QKV epilogue with one workgroup per CU: the rows' padded key indices,
@@ -296,8 +314,10 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     constexpr int QHALF = EPI == EPI_QKV16 ? 8 : (EPI == EPI_QKV32 ? 16 : 32);
     constexpr bool PREF = QKV && T::OCC == 1;
     constexpr int XTRA = PREF ? BM * 8 + 2 * BM * QHALF * 4 : 0;
-    static_assert(3 * STAGE + XTRA <= 160 * 1024, "LDS");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[3 * STAGE + XTRA];
+    constexpr int EL = QKV ? qkv_epilogue_lds<2 * QHALF, RT, CT, WM, WN>() : 0;
+    constexpr int LOFF = 3 * STAGE > EL ? 3 * STAGE : EL;  // start of the prefetched rows
+    static_assert(LOFF + XTRA <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[LOFF + XTRA];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -322,14 +342,27 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         srcA[i] = X + (size_t)min(m0 + row, M - 1) * KB * 64 + chunk * 8;
         dstA[i] = j * 1024;
     }
-    const unsigned short *srcB[NB];
+    // W: chunk c of column n at c ^ ((n >> 2) & 3) (f16 copy, 4 chunks), at
+    // c ^ ((n >> 3) & 1) (Q8_0, 2 chunks); Q4_0: one chunk.  Chunks past the
+    // tile's columns (Q4_0 at 160 columns) fill padding nobody reads.
+    const unsigned char *srcB[NB];
     int dstB[NB];
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-        const int j = i * NW + wave < T::LB ? i * NW + wave : wave;
+        const int j = i * NW + wave < T::LB ? i * NW + wave : wave % T::LB;
         const int p = j * 64 + lane;
-        const int col = p >> 2, chunk = (p & 3) ^ ((col >> 2) & 3);
-        srcB[i] = W16 + (size_t)min(n0 + col, N - 1) * 32 + chunk * 8;
+        int col, chunk;
+        if constexpr (BPC == 64) {
+            col = p >> 2;
+            chunk = (p & 3) ^ ((col >> 2) & 3);
+        } else if constexpr (BPC == 32) {
+            col = p >> 1;
+            chunk = (p & 1) ^ ((col >> 3) & 1);
+        } else {
+            col = min(p, BN - 1);
+            chunk = 0;
+        }
+        srcB[i] = WB + (size_t)min(n0 + col, N - 1) * BPC + chunk * 16;
         dstB[i] = SA + j * 1024;
     }
     const float *srcS = Wsc + min(n0 + wave * SL + min(lane, SL - 1), N - 1);
@@ -348,8 +381,8 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                                              16, 0, 0);
 #pragma unroll
         for (int i = 0; i < NB; i++)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcB[i] + (size_t)kb * N * 32), (lds_ptr_t *)(base + dstB[i]),
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcB[i] + (size_t)kb * N * BPC),
+                                             (lds_ptr_t *)(base + dstB[i]), 16, 0, 0);
         if (lane < SL)
             __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcS + (size_t)kb * N),
                                              (lds_ptr_t *)(base + SA + SB + wave * SL * 4), 4, 0, 0);
@@ -377,9 +410,19 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
 #pragma unroll
         for (int q = 0; q < 16; q++) pend[r][q] = 0.0f;
     const int swA = (li >> 1) & 7, swB = (li >> 2) & 3;
-    auto read_b = [&](const unsigned char *base, int c, int kh) __attribute__((always_inline)) {
+    // B operands of column tile c, both k-halves
+    auto read_b2 = [&](const unsigned char *base, int c, f16x8 (&b)[2]) __attribute__((always_inline)) {
         const int col = (wn * CT + c) * 32 + li;
-        return *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((kh * 2 + hh) ^ swB) << 4));
+        if constexpr (WQ == 0) {
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++)
+                b[kh] = *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((hh * 2 + kh) ^ swB) << 4));
+        } else {
+            const qu32x4_t w = *reinterpret_cast<const qu32x4_t *>(
+                base + SA + (BPC == 32 ? col * 32 + ((hh ^ ((li >> 3) & 1)) << 4) : col * 16));
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++) b[kh] = quants_f16<WQ>(qu32x2_t{w[2 * kh], w[2 * kh + 1]}, 4 * hh);
+        }
     };
     auto scale_of = [&](const unsigned char *base, int c) __attribute__((always_inline)) {
         return *reinterpret_cast<const float *>(base + SA + SB + ((wn * CT + c) * 32 + li) * 4);
@@ -403,7 +446,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             for (int l = 0; l < 2; l++)
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
-                    const int row = (wm * RT + r) * 32 + li, chunk = l * 4 + kh * 2 + hh;
+                    const int row = (wm * RT + r) * 32 + li, chunk = l * 4 + hh * 2 + kh;
                     a[kh][l][r] = *reinterpret_cast<const f16x8 *>(base + row * 128 + ((chunk ^ swA) << 4));
                 }
         if constexpr (RT >= 2) {
@@ -417,13 +460,14 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
 #pragma unroll
                         for (int q = 0; q < 16; q++) acc[r][CT - 1][q] += dpend * pend[r][q];
                 }
+                f16x8 b[2];
+                read_b2(base, c, b);
 #pragma unroll
                 for (int kh = 0; kh < 2; kh++) {
-                    const f16x8 b = read_b(base, c, kh);
 #pragma unroll
                     for (int l = 0; l < 2; l++)
 #pragma unroll
-                        for (int r = 0; r < RT; r++) mfma(a[kh][l][r], b, tmp[r], kh == 0 && l == 0);
+                        for (int r = 0; r < RT; r++) mfma(a[kh][l][r], b[kh], tmp[r], kh == 0 && l == 0);
                 }
                 const float d = scale_of(base, c);
                 if (c == CT - 1) {
@@ -439,15 +483,15 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             }
         } else {
             f32x16 tmp[NT];
+            f16x8 b[CT][2];
+#pragma unroll
+            for (int c = 0; c < CT; c++) read_b2(base, c, b[c]);
 #pragma unroll
             for (int kh = 0; kh < 2; kh++) {
-                f16x8 b[CT];
-#pragma unroll
-                for (int c = 0; c < CT; c++) b[c] = read_b(base, c, kh);
 #pragma unroll
                 for (int l = 0; l < 2; l++)
 #pragma unroll
-                    for (int c = 0; c < CT; c++) mfma(a[kh][l][0], b[c], tmp[c], kh == 0 && l == 0);
+                    for (int c = 0; c < CT; c++) mfma(a[kh][l][0], b[c][kh], tmp[c], kh == 0 && l == 0);
             }
 #pragma unroll
             for (int c = 0; c < CT; c++) {
@@ -471,7 +515,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     request(0, 0);
     request(min(1, KB - 1), 1);
     if constexpr (PREF) {
-        int *s_pk = reinterpret_cast<int *>(lds + 3 * STAGE), *s_pos = s_pk + BM;
+        int *s_pk = reinterpret_cast<int *>(lds + LOFF), *s_pos = s_pk + BM;
         if (tid < BM) {
             const int row = m0 + tid;
             s_pk[tid] = row < M ? qo.pk[row] : -1;
@@ -484,7 +528,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                 const int c = j * 64 + lane, tbl = c / (BM * CPRR), rem = c % (BM * CPRR);
                 const int row = min(m0 + rem / CPRR, M - 1);
                 const float *src = (tbl ? qo.rs : qo.rc) + (size_t)qo.pos[row] * QHALF + (rem % CPRR) * 4;
-                __builtin_amdgcn_global_load_lds((glb_ptr_t *)src, (lds_ptr_t *)(lds + 3 * STAGE + BM * 8 + j * 1024),
+                __builtin_amdgcn_global_load_lds((glb_ptr_t *)src, (lds_ptr_t *)(lds + LOFF + BM * 8 + j * 1024),
                                                  16, 0, 0);
             }
         }
@@ -542,7 +586,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             }
     if constexpr (EPI == EPI_QKV16 || EPI == EPI_QKV32 || EPI == EPI_QKV64) {
         qkv_epilogue<EPI == EPI_QKV16 ? 16 : (EPI == EPI_QKV32 ? 32 : 64), RT, CT, WM, WN, PREF>(
-            acc, lds, lds + 3 * STAGE, m0, n0, wm, wn, lane, M, N, reinterpret_cast<float *>(Yv), ldy, qo);
+            acc, lds, lds + LOFF, m0, n0, wm, wn, lane, M, N, reinterpret_cast<float *>(Yv), ldy, qo);
         return;
     }
     auto store = [&](bool guard) __attribute__((always_inline)) {
@@ -594,8 +638,17 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
                     const QkvOut &qo) {
     using T = LdsTile<RT, CT, WM, WN>;
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
-    hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN>), dim3(tiles), dim3(T::THREADS), 0, st,
-                       reinterpret_cast<const unsigned short *>(X), W.q16, W.sc, bias, Y, ldy, M, W.N, W.K, qo);
+    const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
+    const bool quants = !W.q16;
+    if (quants && W.fmt == WF_Q8)
+        hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, WF_Q8>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
+                           static_cast<const unsigned char *>(W.q), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
+    else if (quants && W.fmt == WF_Q4)
+        hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, WF_Q4>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
+                           static_cast<const unsigned char *>(W.q), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
+    else
+        hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
+                           reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
     return hipGetLastError();
 }
 
@@ -662,7 +715,7 @@ int device_cus() {
 }
 
 bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi) {
-    if (!W.q16 || a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || W.K % 32 || M <= 0) return false;
+    if (a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || W.K % 32 || M <= 0) return false;
     if (epi != EPI_NONE && epi != EPI_RESIDUAL && epi != EPI_GELU_H2) return false;
     const char *e = getenv("CIH_GEMM_LDS");
     if (e && !strcmp(e, "0")) return false;
@@ -672,7 +725,7 @@ bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi) {
 
 hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
                            hipStream_t st, const QkvOut *qo) {
-    if (!W.q16 || W.K % 32 || W.K <= 0 || M <= 0 || W.N <= 0) return hipErrorInvalidValue;
+    if ((W.fmt != WF_Q8 && W.fmt != WF_Q4) || W.K % 32 || W.K <= 0 || M <= 0 || W.N <= 0) return hipErrorInvalidValue;
     if (epi == EPI_GELU_H2 && W.N % 32) return hipErrorInvalidValue;
     if (epi >= EPI_QKV16) {
         const int hd = epi == EPI_QKV16 ? 16 : (epi == EPI_QKV32 ? 32 : 64);

@@ -293,7 +293,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
     auto compute = [&](int stg) __attribute__((always_inline)) {
         const unsigned short *Al = Al2[stg], *Bl = Bl2[stg];
         const float *Ss = Ss2[stg];
-        // A operands of this wave's rows for both k-halves and all limbs
+        // A operands of this wave's rows for both k-halves and all limbs.  Lane
+        // (li, hh) of k-half kh holds k = 16 hh + 8 kh + e of the block (B the
+        // same k): the LDS-staged kernel then reads a column's 16 quant bytes of
+        // both halves in one access.  Every f16-limb GEMM assigns k this way, so
+        // each MFMA sums the same products and their results agree bit for bit.
         V8 a[2][NL][MT];
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
@@ -302,14 +306,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_x3(const void *__restrict__ Xv,
 #pragma unroll
                 for (int r = 0; r < MT; r++)
                     a[kh][l][r] = *reinterpret_cast<const V8 *>(
-                        &Al[(wm * (BM / 2) + r * 32 + li) * AROW + l * 32 + kh * 16 + hh * 8]);
+                        &Al[(wm * (BM / 2) + r * 32 + li) * AROW + l * 32 + hh * 16 + kh * 8]);
 #pragma unroll
         for (int c = 0; c < NT; c++) {
             const int col = wn * (BN / 2) + c * 32 + li;
             f32x16 tmp[MT];
 #pragma unroll
             for (int kh = 0; kh < 2; kh++) {
-                const V8 b = *reinterpret_cast<const V8 *>(&Bl[col * XL + kh * 16 + hh * 8]);
+                const V8 b = *reinterpret_cast<const V8 *>(&Bl[col * XL + hh * 16 + kh * 8]);
 #pragma unroll
                 for (int l = 0; l < NL; l++)
 #pragma unroll

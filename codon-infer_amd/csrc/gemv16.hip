@@ -42,35 +42,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-// packed f16 pair minus (c, c); exact for the integer-valued inputs here
-__device__ __forceinline__ unsigned sub_pair(unsigned p, _Float16 c) {
-    return __builtin_bit_cast(unsigned, __builtin_bit_cast(f16x2, p) - f16x2{c, c});
-}
-
-// 8 quants of one column (Q8_0: 8 signed bytes; Q4_0: the low or high nibbles
-// of 8 bytes) as 8 f16 integers.  A byte b under the f16 exponent of 1024
-// (bits 0x64bb) reads as 1024 + b.
-template <int WF>
-__device__ __forceinline__ f16x8 quants_f16(u32x2 w, int shift) {
-    u32x4 o;
-    if constexpr (WF == WF_Q8) {
-#pragma unroll
-        for (int p = 0; p < 2; p++) {
-            const unsigned u = w[p] ^ 0x80808080u;  // q + 128
-            o[2 * p] = sub_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), (_Float16)1152.0f);
-            o[2 * p + 1] = sub_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), (_Float16)1152.0f);
-        }
-    } else {
-#pragma unroll
-        for (int p = 0; p < 2; p++) {
-            const unsigned u = (w[p] >> shift) & 0x0F0F0F0Fu;  // nibble n, value n - 8
-            o[2 * p] = sub_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), (_Float16)1032.0f);
-            o[2 * p + 1] = sub_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), (_Float16)1032.0f);
-        }
-    }
-    return __builtin_bit_cast(f16x8, o);
-}
-
 }  // namespace
 
 // X: [M][KB][hi 32 | lo 32] f16 (H2).  Grid (ceil(N / 64), S), 256 threads;

@@ -103,4 +103,31 @@ __device__ __forceinline__ void h2_store4(unsigned short *base, size_t row, int 
             make_uint2((unsigned)l[k][0] | ((unsigned)l[k][1] << 16), (unsigned)l[k][2] | ((unsigned)l[k][3] << 16));
 }
 
+// Quants as f16 MFMA operands.  A byte b under the f16 exponent of 1024 (bits
+// 0x64bb) reads as 1024 + b; one packed f16 subtraction takes the offset off
+// two values at once (exact: every value involved is an integer below 2048).
+typedef _Float16 qh16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 qh16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned qu32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned qu32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ unsigned sub_pair(unsigned p, _Float16 c) {
+    return __builtin_bit_cast(unsigned, __builtin_bit_cast(qh16x2_t, p) - qh16x2_t{c, c});
+}
+
+// 8 quants of one column as 8 f16 integers: Q8_0 (WF 1) 8 signed bytes, Q4_0
+// (WF 2) the low (shift 0) or high (shift 4) nibbles of 8 bytes, minus 8.
+template <int WF>
+__device__ __forceinline__ qh16x8_t quants_f16(qu32x2_t w, int shift) {
+    qu32x4_t o;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const unsigned u = WF == 1 ? w[p] ^ 0x80808080u : (w[p] >> shift) & 0x0F0F0F0Fu;  // q + 128 / nibble
+        const _Float16 off = WF == 1 ? (_Float16)1152.0f : (_Float16)1032.0f;
+        o[2 * p] = sub_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), off);
+        o[2 * p + 1] = sub_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), off);
+    }
+    return __builtin_bit_cast(qh16x8_t, o);
+}
+
 }  // namespace cih

@@ -1,16 +1,17 @@
 """The LDS-staged quantized GEMM (csrc/gemm_lds.hip: operands loaded global ->
-LDS by the load unit, quants read from an f16 copy made at model load)
-against the register-staged GEMM (csrc/gemm_x3.hip) it replaces on large
-batches.  Both compute matmul_tiled_q8/q4_parallel (src/lib.rs:4870, 4937)
-with the same operations in the same order, so whole forwards must agree
-bit for bit: a wrong swizzle, load count, stage rotation or f16 expansion
-changes the result.
+LDS by the load unit, quants read from an f16 copy made at model load, or,
+in a model loaded without that copy, the quants themselves converted on the
+LDS -> register path) against the register-staged GEMM (csrc/gemm_x3.hip) it
+replaces on large batches.  All three compute matmul_tiled_q8/q4_parallel
+(src/lib.rs:4870, 4937) with the same operations in the same order, so whole
+forwards must agree bit for bit: a wrong swizzle, load count, stage
+rotation, k assignment or f16 expansion changes the result.
 
-A model built with CIH_GEMM_F16=0 has no f16 copy and always takes the
-register-staged kernel; CIH_GEMM_LDS=force sends every eligible GEMM of the
-other model (activations in f16 limbs) to the LDS-staged one.  CIH_SPLITK=0
-keeps the register-staged kernel from splitting K on small shapes (a split
-sums the blocks in another order).
+A model built with CIH_GEMM_F16=0 has no f16 copy; CIH_GEMM_LDS=0 keeps every
+GEMM on the register-staged kernel, CIH_GEMM_LDS=force sends every eligible
+GEMM (activations in f16 limbs) to the LDS-staged one.  CIH_SPLITK=0 keeps
+the register-staged kernel from splitting K on small shapes (a split sums
+the blocks in another order).
 """
 import numpy as np
 import pytest
@@ -62,30 +63,36 @@ def test_forced_lds_gemm_is_bit_identical(fmt, tile, monkeypatch):
     cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
     seqs = [rand_tokens(rng, 298), rand_tokens(rng, 255), rand_tokens(rng, 128)]
     ref, lds = two_models(monkeypatch, cfg, w, cw, 3, 300)
-    monkeypatch.setenv("CIH_GEMM_LDS", "force")
     monkeypatch.setenv("CIH_SPLITK", "0")
-    b = lds.forward(seqs, FLAGS)
+    monkeypatch.setenv("CIH_GEMM_LDS", "0")
     a = ref.forward(seqs, FLAGS)
-    print(f"{fmt} tile {tile}: forced LDS GEMM forward equals the register-staged one", flush=True)
-    assert_same(b, a, seqs, fmt)
+    monkeypatch.setenv("CIH_GEMM_LDS", "force")
+    b = lds.forward(seqs, FLAGS)
+    c = ref.forward(seqs, FLAGS)
+    print(f"{fmt} tile {tile}: forced LDS GEMM forwards (f16 copy, quants) equal the register-staged one", flush=True)
+    assert_same(b, a, seqs, fmt + " f16 copy")
+    assert_same(c, a, seqs, fmt + " quants")
     ref.close()
     lds.close()
 
 
 def test_650m_headline_batch_is_bit_identical(monkeypatch):
     """ESM-2 650M Q8_0, 16 sequences of 510 residues (8192 tokens): the
-    default tile choice (128 x 256 for QKV and FC1, 128 x 128 for Wo and FC2,
-    K = 1280 and 5120)."""
+    default tile choice (128 x 320 for every projection, K = 1280 and
+    5120)."""
     rng = np.random.default_rng(650)
     cfg = ch.EsmConfig.esm2_650m()
     w = ch.EsmWeights.random(cfg, seed=650, bias_std=0.02).quantize_q8()
     cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.05).astype(np.float32)
     seqs = [rand_tokens(rng, 510) for _ in range(16)]
     ref, lds = two_models(monkeypatch, cfg, w, cw, 16, 512)
-    monkeypatch.delenv("CIH_GEMM_LDS", raising=False)
-    b = lds.forward(seqs, FLAGS)
+    monkeypatch.setenv("CIH_GEMM_LDS", "0")
     a = ref.forward(seqs, FLAGS)
-    print("650M B=16 L=512: LDS GEMM forward equals the register-staged one", flush=True)
-    assert_same(b, a, seqs, "650M")
+    monkeypatch.delenv("CIH_GEMM_LDS")
+    b = lds.forward(seqs, FLAGS)
+    c = ref.forward(seqs, FLAGS)
+    print("650M B=16 L=512: LDS GEMM forwards (f16 copy, quants) equal the register-staged one", flush=True)
+    assert_same(b, a, seqs, "650M f16 copy")
+    assert_same(c, a, seqs, "650M quants")
     ref.close()
     lds.close()
