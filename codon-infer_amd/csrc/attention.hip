@@ -761,6 +761,284 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     }
 }
 
+// Attention with the probability export for batches whose 32-query tasks
+// do not cover the compute units (one sequence of a few hundred residues):
+// one workgroup per (sequence, head, 32 queries) task, KS waves on the same
+// 32 queries, wave w over the 32-key tiles w, w + KS, ...  Each wave stages
+// its tiles (RoPE, limbs, V transposed, as k_attention_h stages them) in
+// its own LDS, so the waves meet only twice: pass 1's running maxima and
+// sums (per wave and lane) are combined into each query's maximum M and sum
+// L = sum 2^(m_s - M) l_s in wave order, and after pass 2 (probabilities
+// exp2(s - M) / L, stored, and P.V) the waves' P.V accumulators are added in
+// wave order.  Per query the arithmetic is k_attention_h's, with the
+// softmax sum and the P.V sum regrouped by wave: agreement to rounding, not
+// bit for bit.
+template <int HD, int KS>
+__global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restrict__ qkv, int d,
+                                                          const int *__restrict__ cu, const int *__restrict__ lens,
+                                                          int S_max, const float *__restrict__ rc,
+                                                          const float *__restrict__ rsn, void *__restrict__ out,
+                                                          int out_fmt, float *__restrict__ P, long long pb,
+                                                          long long ph, float inv_scale, float *__restrict__ rowsum,
+                                                          int H, int nq) {
+#pragma clang fp contract(off)
+    constexpr int HALF = HD / 2;
+    constexpr int HDP = (HD + 15) / 16 * 16;
+    constexpr int NC = HDP / 16;
+    constexpr int VW = HD < 32 ? 32 : HD;
+    constexpr int DT = VW / 32;
+    constexpr int K_LD = HDP + 8, V_LD = 32 + 8;
+    constexpr int KBUF = 32 * K_LD, VBUF = VW * V_LD;
+    // [Kh | Kl | Vh | Vl] of every wave; after pass 2 the same bytes hold the
+    // waves' P.V accumulators
+    constexpr int STAGE_BYTES = KS * (2 * KBUF + 2 * VBUF) * 2, OX_BYTES = KS * DT * 16 * 64 * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char sm[STAGE_BYTES > OX_BYTES ? STAGE_BYTES : OX_BYTES];
+    __shared__ float red[KS][3][64];  // per wave and lane: running max, sum, residue sum
+    static_assert((STAGE_BYTES > OX_BYTES ? STAGE_BYTES : OX_BYTES) + KS * 3 * 64 * 4 <= 160 * 1024, "LDS");
+
+    const int task = blockIdx.x, qb = task % nq, h = (task / nq) % H, b = task / nq / H;
+    const int len = lens[b], base = cu[b];
+    const int qblk = qb * 32;
+    if (qblk >= len) return;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 31, hh = lane >> 5;
+    const size_t ld = (size_t)3 * d;
+    const float *Qg = qkv + h * HD;
+    const float *Kg = qkv + d + h * HD;
+    const float *Vg = qkv + 2 * d + h * HD;
+    _Float16 *const Kh = reinterpret_cast<_Float16 *>(sm) + w * KBUF;
+    _Float16 *const Kl = reinterpret_cast<_Float16 *>(sm) + KS * KBUF + w * KBUF;
+    _Float16 *const Vh = reinterpret_cast<_Float16 *>(sm) + 2 * KS * KBUF + w * VBUF;
+    _Float16 *const Vl = reinterpret_cast<_Float16 *>(sm) + 2 * KS * KBUF + KS * VBUF + w * VBUF;
+    // A wave's LDS operations complete in order; this keeps the compiler from
+    // moving this wave's LDS accesses across the point.
+    auto wave_sync = [&]() __attribute__((always_inline)) { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+
+    // padding dims (HD..HDP of K, HD..VW of V) stay zero for every tile
+    if constexpr (HDP > HD)
+        for (int idx = lane; idx < 32 * (HDP - HD); idx += 64) {
+            const int key = idx / (HDP - HD), c = HD + idx % (HDP - HD);
+            Kh[key * K_LD + c] = (_Float16)0.0f;
+            Kl[key * K_LD + c] = (_Float16)0.0f;
+        }
+    if constexpr (VW > HD)
+        for (int idx = lane; idx < (VW - HD) * 32; idx += 64) {
+            const int c = HD + idx / 32, key = idx % 32;
+            Vh[c * V_LD + key] = (_Float16)0.0f;
+            Vl[c * V_LD + key] = (_Float16)0.0f;
+        }
+
+    // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs
+    const float sl2 = inv_scale * 1.44269504088896340736f;
+    const int qi = qblk + li;
+    const int qc = min(qi, len - 1);
+    f16x8 qh[NC], ql[NC];
+    {
+        const float *qrow = Qg + (size_t)(base + qc) * ld;
+        const float *cs = rc + (size_t)qc * HALF, *sn = rsn + (size_t)qc * HALF;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int dim = 16 * c + 8 * hh + e;
+                float r = 0.0f;
+                if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
+                else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
+                v[e] = r;
+            }
+            split8(v, qh[c], ql[c]);
+        }
+    }
+
+    // K tile: a lane rotates 4 consecutive pair-dims (c..c+3 with c+HALF..) of one key
+    auto load_k = [&](int kt0) __attribute__((always_inline)) {
+        constexpr int G = HALF / 4;
+#pragma unroll 2
+        for (int idx = lane; idx < 32 * G; idx += 64) {
+            const int key = idx / G, c = 4 * (idx % G);
+            const int kk = min(kt0 + key, len - 1);
+            const float *krow = Kg + (size_t)(base + kk) * ld;
+            const float4 k0 = *reinterpret_cast<const float4 *>(krow + c);
+            const float4 k1 = *reinterpret_cast<const float4 *>(krow + c + HALF);
+            const float4 cs = *reinterpret_cast<const float4 *>(rc + (size_t)kk * HALF + c);
+            const float4 sn = *reinterpret_cast<const float4 *>(rsn + (size_t)kk * HALF + c);
+            const float r0[4] = {rot_lo(k0.x, k1.x, cs.x, sn.x), rot_lo(k0.y, k1.y, cs.y, sn.y),
+                                 rot_lo(k0.z, k1.z, cs.z, sn.z), rot_lo(k0.w, k1.w, cs.w, sn.w)};
+            const float r1[4] = {rot_hi(k1.x, k0.x, cs.x, sn.x), rot_hi(k1.y, k0.y, cs.y, sn.y),
+                                 rot_hi(k1.z, k0.z, cs.z, sn.z), rot_hi(k1.w, k0.w, cs.w, sn.w)};
+            f16x4 h0, l0, h1, l1;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                h0[e] = (_Float16)r0[e];
+                l0[e] = (_Float16)(r0[e] - (float)h0[e]);
+                h1[e] = (_Float16)r1[e];
+                l1[e] = (_Float16)(r1[e] - (float)h1[e]);
+            }
+            *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c]) = h0;
+            *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c]) = l0;
+            *reinterpret_cast<f16x4 *>(&Kh[key * K_LD + c + HALF]) = h1;
+            *reinterpret_cast<f16x4 *>(&Kl[key * K_LD + c + HALF]) = l1;
+        }
+    };
+    // V tile, transposed: a lane takes 4 consecutive keys of one dim
+    auto load_v = [&](int kt0) __attribute__((always_inline)) {
+#pragma unroll 2
+        for (int idx = lane; idx < 8 * HD; idx += 64) {
+            const int c = idx % HD, kg = 4 * (idx / HD);
+            f16x4 hv, lv;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int kk = min(kt0 + kg + e, len - 1);
+                const float v = Vg[(size_t)(base + kk) * ld + c];
+                hv[e] = (_Float16)v;
+                lv[e] = (_Float16)(v - (float)hv[e]);
+            }
+            const int pos = (kg & ~15) | ((kg & 4) << 1) | ((kg & 8) >> 1);  // as in k_attention_h
+            *reinterpret_cast<f16x4 *>(&Vh[c * V_LD + pos]) = hv;
+            *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + pos]) = lv;
+        }
+    };
+    auto scores = [&](f32x16 &acc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[q] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const f16x8 kh = *reinterpret_cast<const f16x8 *>(&Kh[li * K_LD + 16 * c + 8 * hh]);
+            const f16x8 kl = *reinterpret_cast<const f16x8 *>(&Kl[li * K_LD + 16 * c + 8 * hh]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[c], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[c], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[c], acc, 0, 0, 0);
+        }
+    };
+    auto pv = [&](f32x16 (&oacc)[DT], const float (&p)[16]) __attribute__((always_inline)) {
+        f16x8 phi[2], plo[2];
+        split8_mix(p, phi[0], plo[0]);
+        split8_mix(p + 8, phi[1], plo[1]);
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            const int row = (t * 32 + li) * V_LD;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const f16x8 vh = *reinterpret_cast<const f16x8 *>(&Vh[row + 16 * c + 8 * hh]);
+                const f16x8 vl = *reinterpret_cast<const f16x8 *>(&Vl[row + 16 * c + 8 * hh]);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, phi[c], oacc[t], 0, 0, 0);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, plo[c], oacc[t], 0, 0, 0);
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, phi[c], oacc[t], 0, 0, 0);
+            }
+        }
+    };
+
+    const int ntile = (len + 31) / 32;
+    // pass 1: running max / sum of exp per lane over this wave's tiles
+    float m = -INFINITY, l = 0.0f;
+    for (int t = w; t < ntile; t += KS) {
+        const int kt0 = t * 32;
+        wave_sync();
+        load_k(kt0);
+        wave_sync();
+        f32x16 acc;
+        scores(acc);
+        float sv[16];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+            sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
+            tmax = fmaxf(tmax, sv[q]);
+        }
+        const float mn = fmaxf(m, tmax);
+        if (mn != -INFINITY) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) sum += __builtin_amdgcn_exp2f(sv[q] - mn);
+            l = l * __builtin_amdgcn_exp2f(m - mn) + sum;
+            m = mn;
+        }
+    }
+    red[w][0][lane] = m;
+    red[w][1][lane] = l;
+    __syncthreads();
+    // this query's max and sum over all waves and both lane halves (key 0,
+    // in wave 0's half 0, makes M finite)
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < KS; s++) M = fmaxf(M, fmaxf(red[s][0][li], red[s][0][li + 32]));
+    float L = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const float ms = red[s][0][li + 32 * hf];
+            if (ms != -INFINITY) L += red[s][1][li + 32 * hf] * __builtin_amdgcn_exp2f(ms - M);
+        }
+    const float inv_sum = 1.0f / L;
+
+    // pass 2: normalized probabilities, export, P.V
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
+    float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+    float rs = 0.0f;
+    for (int t = w; t < ntile; t += KS) {
+        const int kt0 = t * 32;
+        wave_sync();
+        load_k(kt0);
+        load_v(kt0);
+        wave_sync();
+        f32x16 acc;
+        scores(acc);
+        float p[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+            p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - M) * inv_sum : 0.0f;
+        }
+        if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
+        if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
+        pv(oacc, p);
+    }
+    red[w][2][lane] = rs;
+    __syncthreads();  // every wave is done with its stages
+    float *ox = reinterpret_cast<float *>(sm);
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) ox[((w * DT + t) * 16 + q) * 64 + lane] = oacc[t][q];
+    __syncthreads();
+    if (w != 0) return;
+    float rsum = red[0][2][lane];
+#pragma unroll
+    for (int s = 1; s < KS; s++) rsum += red[s][2][lane];
+    write_rowsum(rowsum, rsum, b, h, H, S_max, qi, len, hh);
+    if (qi < len) {
+        // output dims t 32 + 8 g + 4 hh + {0..3}: registers 4 g + {0..3} of tile t, summed in wave order
+#pragma unroll 1
+        for (int tg = 0; tg < 4 * DT; tg++) {
+            const int t = tg >> 2, g = tg & 3;
+            const int dd = t * 32 + 8 * g + 4 * hh;
+            if (dd >= HD) continue;
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int q = 4 * g + e;
+                o[e] = ox[(t * 16 + q) * 64 + lane];
+#pragma unroll
+                for (int s = 1; s < KS; s++) o[e] += ox[((s * DT + t) * 16 + q) * 64 + lane];
+            }
+            const float4 v = make_float4(o[0], o[1], o[2], o[3]);
+            if (out_fmt == AF_X3)
+                x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+            else if (out_fmt == AF_H2)
+                h2_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
+            else
+                *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d + h * HD + dd) =
+                    v;
+        }
+    }
+}
+
 // Combines the nsplit partial results of each split task (k_attention_h):
 // O = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s (the
 // running maxima are in base-2 units).  One thread per (task, query, 4 dims).
@@ -1217,6 +1495,11 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
         }
     }
     const int grid = nfull + (tasks - nfull) * nsplit;
+    // With an export whose 32-query tasks do not cover the compute units, the
+    // waves of a task split its keys instead (k_attention_xs); the same
+    // switches as the key split turn it off.
+    const bool xsplit = P && !fp32 && QB == 32 && tasks < device_cus() && !(se && !strcmp(se, "0")) &&
+                        !(ke && !strcmp(ke, "0"));
 #define CIH_ATT_K(KER, HDV, ONE)                                                                                \
     hipLaunchKernelGGL((KER<HDV, ONE>), dim3((sm.S_max + 127) / 128, H, sm.B), dim3(256), 0, st, qkv, d, sm.cu, \
                        sm.lens, sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph,     \
@@ -1226,7 +1509,11 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
                        sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum, \
                        H, nq, nfull, nsplit, part)
 #define CIH_ATT(HDV)                                                                                           \
-    if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                          \
+    if (xsplit)                                                                                                 \
+        hipLaunchKernelGGL((k_attention_xs<HDV, 8>), dim3(tasks), dim3(512), 0, st, qkv, d, sm.cu, sm.lens,     \
+                           sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, \
+                           rowsum, H, nq);                                                                      \
+    else if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                     \
     else if (fp32) CIH_ATT_K(k_attention, HDV, true);                                                           \
     else if (P && wide) CIH_ATT_H(HDV, false, 512);                                                             \
     else if (P && QB == 32) CIH_ATT_H(HDV, false, 64);                                                          \

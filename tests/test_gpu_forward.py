@@ -374,6 +374,51 @@ def test_attention_key_split(case, monkeypatch):
         assert e <= TOL[k], (case, k, e)
 
 
+@pytest.mark.parametrize("hd", [16, 24, 32, 64])
+@pytest.mark.parametrize("case", ["one", "two"])
+def test_attention_export_key_split(hd, case, monkeypatch):
+    """With the probability export, batches whose 32-query tasks do not cover
+    the compute units run each task on 8 waves that split its keys
+    (k_attention_xs): one 256-token sequence (8 tiles, one per wave) or two
+    ragged ones (partial tiles, waves without a tile).  Every output agrees
+    with the one-wave kernel (CIH_ATT_SPLIT=0) to 1e-5 and the maps of the
+    last sequence with the oracle to 1e-5."""
+    rng = np.random.default_rng(hd + (0 if case == "one" else 500))
+    d = 20 * hd
+    cfg = ch.EsmConfig(d, 4 * d, 2, 20)
+    lens = [254] if case == "one" else [61, 140]
+    seqs = [rand_tokens(rng, n) for n in lens]
+    w = ch.EsmWeights.random(cfg, seed=hd, bias_std=0.02).quantize_q8()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_ATTN | ch.OUT_FINAL_ATT | ch.OUT_CONTACTS
+    res = {}
+    for sp in ("0", "1"):
+        monkeypatch.setenv("CIH_ATT_SPLIT", sp)
+        m = ch.GpuModel(cfg, w, contact_head=(cw, 0.3), max_batch=len(seqs), max_len=max(len(t) for t in seqs),
+                        outputs=flags)
+        res[sp] = m.forward(seqs, flags)
+        m.close()
+    for i, t in enumerate(seqs):
+        n = len(t)
+        for k in ("logits", "hidden", "attn", "final_att", "contacts"):
+            a, b = res["1"][k][i], res["0"][k][i]
+            if k == "attn":
+                a, b = a[:, :, :n, :n], b[:, :, :n, :n]
+            elif k == "final_att":
+                a, b = a[:n, :n], b[:n, :n]
+            elif k == "contacts":
+                a, b = a[:n - 2, :n - 2], b[:n - 2, :n - 2]
+            else:
+                a, b = a[:n], b[:n]
+            e = float(np.abs(a - b).max())
+            assert e <= 1e-5, (hd, case, i, k, e)
+    n = len(seqs[-1])
+    ref = cr.forward(cfg, w, seqs[-1], 16, attn=True)
+    e = float(np.abs(res["1"]["attn"][-1, :, :, :n, :n] - ref["attn"]).max())
+    print(f"hd {hd} {case}: maps vs oracle {e:.2e}", flush=True)
+    assert e <= 1e-5
+
+
 def test_device_io_token_validation():
     """With CIH_IO_DEVICE the token ids are checked on the device: an id
     outside [0, vocab) returns CIH_ERR_TOKEN (as the host path does) instead
