@@ -412,6 +412,9 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         // from 2048 tokens on, except at head size 24 (35M B=8 ragged: prep
         // 8.5 us, attention 41.2 -> 33.5 us per layer; net loss)
         if (!epi_img && !prep_only && (T < 2048 || m->hd == 24)) use_img = false;
+        // batches small enough for attention's split over waves stage K/V
+        // there (from FP32 rows; images would take the kernel without it)
+        if (!epi_img && attention_wave_split(B, S_max, H)) use_img = false;
         for (int b = 0; b < B; b++) tile_rows += (lens[b] + 31) / 32;
     }
     const int epi_qkv = m->hd == 16 ? EPI_QKV16 : (m->hd == 32 ? EPI_QKV32 : EPI_QKV64);

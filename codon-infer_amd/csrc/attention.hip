@@ -761,19 +761,23 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     }
 }
 
-// Attention with the probability export for batches whose 32-query tasks
-// do not cover the compute units (one sequence of a few hundred residues):
-// one workgroup per (sequence, head, 32 queries) task, KS waves on the same
-// 32 queries, wave w over the 32-key tiles w, w + KS, ...  Each wave stages
-// its tiles (RoPE, limbs, V transposed, as k_attention_h stages them) in
-// its own LDS, so the waves meet only twice: pass 1's running maxima and
-// sums (per wave and lane) are combined into each query's maximum M and sum
-// L = sum 2^(m_s - M) l_s in wave order, and after pass 2 (probabilities
-// exp2(s - M) / L, stored, and P.V) the waves' P.V accumulators are added in
-// wave order.  Per query the arithmetic is k_attention_h's, with the
-// softmax sum and the P.V sum regrouped by wave: agreement to rounding, not
-// bit for bit.
-template <int HD, int KS>
+// Attention for batches whose 32-query tasks do not cover the compute units
+// (one sequence of a few hundred residues): one workgroup per (sequence,
+// head, 32 queries) task, KS waves on the same 32 queries, wave w over the
+// 32-key tiles w, w + KS, ...  Each wave stages its tiles (RoPE, limbs, V
+// transposed, as k_attention_h stages them) in its own LDS, so the waves
+// meet only to combine:
+//  * with the export (ONEPASS false): pass 1's running maxima and sums (per
+//    wave and lane) give each query's maximum M and sum L = sum 2^(m_s - M)
+//    l_s in wave order; pass 2 stores the probabilities exp2(s - M) / L and
+//    the waves' P.V accumulators are added in wave order;
+//  * without (ONEPASS): each wave runs the one-pass online softmax over its
+//    tiles (online_tile, as k_attention_h), and the waves' results combine
+//    as key ranges do in k_attention_merge: O = sum 2^(m_s - M) o_s /
+//    sum 2^(m_s - M) l_s, in wave order.
+// Per query the arithmetic is k_attention_h's, with the softmax and P.V sums
+// regrouped by wave: agreement to rounding, not bit for bit.
+template <int HD, int KS, bool ONEPASS>
 __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restrict__ qkv, int d,
                                                           const int *__restrict__ cu, const int *__restrict__ lens,
                                                           int S_max, const float *__restrict__ rc,
@@ -844,7 +848,7 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
                 float r = 0.0f;
                 if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
                 else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
-                v[e] = r;
+                v[e] = ONEPASS ? opaque(r * sl2) : r;  // one pass: pre-scaled, as in k_attention_h
             }
             split8(v, qh[c], ql[c]);
         }
@@ -853,8 +857,10 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
     // K tile: a lane rotates 4 consecutive pair-dims (c..c+3 with c+HALF..) of one key
     auto load_k = [&](int kt0) __attribute__((always_inline)) {
         constexpr int G = HALF / 4;
-#pragma unroll 2
-        for (int idx = lane; idx < 32 * G; idx += 64) {
+#pragma unroll
+        for (int i = 0; i < (32 * G + 63) / 64; i++) {
+            const int idx = lane + 64 * i;
+            if (32 * G % 64 != 0 && idx >= 32 * G) break;
             const int key = idx / G, c = 4 * (idx % G);
             const int kk = min(kt0 + key, len - 1);
             const float *krow = Kg + (size_t)(base + kk) * ld;
@@ -882,8 +888,10 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
     };
     // V tile, transposed: a lane takes 4 consecutive keys of one dim
     auto load_v = [&](int kt0) __attribute__((always_inline)) {
-#pragma unroll 2
-        for (int idx = lane; idx < 8 * HD; idx += 64) {
+#pragma unroll
+        for (int i = 0; i < (8 * HD + 63) / 64; i++) {
+            const int idx = lane + 64 * i;
+            if (8 * HD % 64 != 0 && idx >= 8 * HD) break;
             const int c = idx % HD, kg = 4 * (idx / HD);
             f16x4 hv, lv;
 #pragma unroll
@@ -898,9 +906,9 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
             *reinterpret_cast<f16x4 *>(&Vl[c * V_LD + pos]) = lv;
         }
     };
-    auto scores = [&](f32x16 &acc) __attribute__((always_inline)) {
+    auto scores = [&](f32x16 &acc, float c0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < 16; q++) acc[q] = 0.0f;
+        for (int q = 0; q < 16; q++) acc[q] = c0;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const f16x8 kh = *reinterpret_cast<const f16x8 *>(&Kh[li * K_LD + 16 * c + 8 * hh]);
@@ -929,91 +937,12 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
     };
 
     const int ntile = (len + 31) / 32;
-    // pass 1: running max / sum of exp per lane over this wave's tiles
-    float m = -INFINITY, l = 0.0f;
-    for (int t = w; t < ntile; t += KS) {
-        const int kt0 = t * 32;
-        wave_sync();
-        load_k(kt0);
-        wave_sync();
-        f32x16 acc;
-        scores(acc);
-        float sv[16];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-            sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
-            tmax = fmaxf(tmax, sv[q]);
-        }
-        const float mn = fmaxf(m, tmax);
-        if (mn != -INFINITY) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; q++) sum += __builtin_amdgcn_exp2f(sv[q] - mn);
-            l = l * __builtin_amdgcn_exp2f(m - mn) + sum;
-            m = mn;
-        }
-    }
-    red[w][0][lane] = m;
-    red[w][1][lane] = l;
-    __syncthreads();
-    // this query's max and sum over all waves and both lane halves (key 0,
-    // in wave 0's half 0, makes M finite)
-    float M = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < KS; s++) M = fmaxf(M, fmaxf(red[s][0][li], red[s][0][li + 32]));
-    float L = 0.0f;
-#pragma unroll
-    for (int s = 0; s < KS; s++)
-#pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            const float ms = red[s][0][li + 32 * hf];
-            if (ms != -INFINITY) L += red[s][1][li + 32 * hf] * __builtin_amdgcn_exp2f(ms - M);
-        }
-    const float inv_sum = 1.0f / L;
-
-    // pass 2: normalized probabilities, export, P.V
-    f32x16 oacc[DT];
-#pragma unroll
-    for (int t = 0; t < DT; t++)
-#pragma unroll
-        for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
-    float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
-    float rs = 0.0f;
-    for (int t = w; t < ntile; t += KS) {
-        const int kt0 = t * 32;
-        wave_sync();
-        load_k(kt0);
-        load_v(kt0);
-        wave_sync();
-        f32x16 acc;
-        scores(acc);
-        float p[16];
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-            p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - M) * inv_sum : 0.0f;
-        }
-        if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
-        if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
-        pv(oacc, p);
-    }
-    red[w][2][lane] = rs;
-    __syncthreads();  // every wave is done with its stages
     float *ox = reinterpret_cast<float *>(sm);
-#pragma unroll
-    for (int t = 0; t < DT; t++)
-#pragma unroll
-        for (int q = 0; q < 16; q++) ox[((w * DT + t) * 16 + q) * 64 + lane] = oacc[t][q];
-    __syncthreads();
-    if (w != 0) return;
-    float rsum = red[0][2][lane];
-#pragma unroll
-    for (int s = 1; s < KS; s++) rsum += red[s][2][lane];
-    write_rowsum(rowsum, rsum, b, h, H, S_max, qi, len, hh);
-    if (qi < len) {
-        // output dims t 32 + 8 g + 4 hh + {0..3}: registers 4 g + {0..3} of tile t, summed in wave order
+    // The waves' P.V accumulators (scaled by f) added in wave order and stored
+    // for this lane's query, times out_scale; every wave must have written ox.
+    auto finish = [&](float out_scale) __attribute__((always_inline)) {
+        if (qi >= len) return;
+        // output dims t 32 + 8 g + 4 hh + {0..3}: registers 4 g + {0..3} of tile t
 #pragma unroll 1
         for (int tg = 0; tg < 4 * DT; tg++) {
             const int t = tg >> 2, g = tg & 3;
@@ -1027,7 +956,7 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
 #pragma unroll
                 for (int s = 1; s < KS; s++) o[e] += ox[((s * DT + t) * 16 + q) * 64 + lane];
             }
-            const float4 v = make_float4(o[0], o[1], o[2], o[3]);
+            const float4 v = make_float4(o[0] * out_scale, o[1] * out_scale, o[2] * out_scale, o[3] * out_scale);
             if (out_fmt == AF_X3)
                 x3_store4(reinterpret_cast<unsigned short *>(out), base + qi, h * HD + dd, d, v);
             else if (out_fmt == AF_H2)
@@ -1036,6 +965,133 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
                 *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (size_t)(base + qi) * d + h * HD + dd) =
                     v;
         }
+    };
+    if constexpr (ONEPASS) {
+        f32x16 oacc[DT];
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
+        float m = -INFINITY, l = 0.0f;
+        auto tile = [&](int kt0, auto masked) __attribute__((always_inline)) {
+            online_tile<DT, decltype(masked)::value>(m, l, oacc, kt0, len, hh,
+                                                     [&](f32x16 &acc, float c0) { scores(acc, c0); },
+                                                     [&](const float (&p)[16]) { pv(oacc, p); });
+        };
+        for (int t = w; t < ntile; t += KS) {
+            const int kt0 = t * 32;
+            wave_sync();
+            load_k(kt0);
+            load_v(kt0);
+            wave_sync();
+            if (kt0 + 32 <= len) tile(kt0, std::false_type{});
+            else tile(kt0, std::true_type{});
+        }
+        const float lt = l + __shfl_xor(l, 32);  // both lane halves share m
+        red[w][0][lane] = m;
+        red[w][1][lane] = lt;
+        __syncthreads();  // every wave is done with its stages
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < KS; s++) M = fmaxf(M, red[s][0][lane]);
+        float L = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const float ms = red[s][0][lane];
+            if (ms != -INFINITY) L += __builtin_amdgcn_exp2f(ms - M) * red[s][1][lane];
+        }
+        const float f = m != -INFINITY ? __builtin_amdgcn_exp2f(m - M) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) ox[((w * DT + t) * 16 + q) * 64 + lane] = f * oacc[t][q];
+        __syncthreads();
+        if (w == 0) finish(1.0f / L);
+        return;
+    } else {
+        // pass 1: running max / sum of exp per lane over this wave's tiles
+        float m = -INFINITY, l = 0.0f;
+        for (int t = w; t < ntile; t += KS) {
+            const int kt0 = t * 32;
+            wave_sync();
+            load_k(kt0);
+            wave_sync();
+            f32x16 acc;
+            scores(acc, 0.0f);
+            float sv[16];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
+                tmax = fmaxf(tmax, sv[q]);
+            }
+            const float mn = fmaxf(m, tmax);
+            if (mn != -INFINITY) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) sum += __builtin_amdgcn_exp2f(sv[q] - mn);
+                l = l * __builtin_amdgcn_exp2f(m - mn) + sum;
+                m = mn;
+            }
+        }
+        red[w][0][lane] = m;
+        red[w][1][lane] = l;
+        __syncthreads();
+        // this query's max and sum over all waves and both lane halves (key 0,
+        // in wave 0's half 0, makes M finite)
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < KS; s++) M = fmaxf(M, fmaxf(red[s][0][li], red[s][0][li + 32]));
+        float L = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const float ms = red[s][0][li + 32 * hf];
+                if (ms != -INFINITY) L += red[s][1][li + 32 * hf] * __builtin_amdgcn_exp2f(ms - M);
+            }
+        const float inv_sum = 1.0f / L;
+
+        // pass 2: normalized probabilities, export, P.V
+        f32x16 oacc[DT];
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) oacc[t][q] = 0.0f;
+        float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+        float rs = 0.0f;
+        for (int t = w; t < ntile; t += KS) {
+            const int kt0 = t * 32;
+            wave_sync();
+            load_k(kt0);
+            load_v(kt0);
+            wave_sync();
+            f32x16 acc;
+            scores(acc, 0.0f);
+            float p[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - M) * inv_sum : 0.0f;
+            }
+            if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
+            if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
+            pv(oacc, p);
+        }
+        red[w][2][lane] = rs;
+        __syncthreads();  // every wave is done with its stages
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) ox[((w * DT + t) * 16 + q) * 64 + lane] = oacc[t][q];
+        __syncthreads();
+        if (w != 0) return;
+        float rsum = red[0][2][lane];
+#pragma unroll
+        for (int s = 1; s < KS; s++) rsum += red[s][2][lane];
+        write_rowsum(rowsum, rsum, b, h, H, S_max, qi, len, hh);
+        finish(1.0f);
     }
 }
 
@@ -1495,11 +1551,11 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
         }
     }
     const int grid = nfull + (tasks - nfull) * nsplit;
-    // With an export whose 32-query tasks do not cover the compute units, the
-    // waves of a task split its keys instead (k_attention_xs); the same
-    // switches as the key split turn it off.
-    const bool xsplit = P && !fp32 && QB == 32 && tasks < device_cus() && !(se && !strcmp(se, "0")) &&
-                        !(ke && !strcmp(ke, "0"));
+    // When even 32-query tasks fit one round of one workgroup per CU, the 8
+    // waves of each 32-query task split its keys instead (k_attention_xs);
+    // the switches of the key split turn it off.
+    const int nq32 = (sm.S_max + 31) / 32, t32 = sm.B * H * nq32;
+    const bool xsplit = !fp32 && attention_wave_split(sm.B, sm.S_max, H);
 #define CIH_ATT_K(KER, HDV, ONE)                                                                                \
     hipLaunchKernelGGL((KER<HDV, ONE>), dim3((sm.S_max + 127) / 128, H, sm.B), dim3(256), 0, st, qkv, d, sm.cu, \
                        sm.lens, sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph,     \
@@ -1509,10 +1565,14 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
                        sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, rowsum, \
                        H, nq, nfull, nsplit, part)
 #define CIH_ATT(HDV)                                                                                           \
-    if (xsplit)                                                                                                 \
-        hipLaunchKernelGGL((k_attention_xs<HDV, 8>), dim3(tasks), dim3(512), 0, st, qkv, d, sm.cu, sm.lens,     \
+    if (xsplit && P)                                                                                            \
+        hipLaunchKernelGGL((k_attention_xs<HDV, 8, false>), dim3(t32), dim3(512), 0, st, qkv, d, sm.cu, sm.lens, \
                            sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, \
-                           rowsum, H, nq);                                                                      \
+                           rowsum, H, nq32);                                                                    \
+    else if (xsplit)                                                                                            \
+        hipLaunchKernelGGL((k_attention_xs<HDV, 8, true>), dim3(t32), dim3(512), 0, st, qkv, d, sm.cu, sm.lens,  \
+                           sm.S_max, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph, inv_scale, \
+                           rowsum, H, nq32);                                                                    \
     else if (fp32 && P) CIH_ATT_K(k_attention, HDV, false);                                                     \
     else if (fp32) CIH_ATT_K(k_attention, HDV, true);                                                           \
     else if (P && wide) CIH_ATT_H(HDV, false, 512);                                                             \
@@ -1521,7 +1581,7 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     else if (P) CIH_ATT_H(HDV, false, 256);                                                                     \
     else if (wide) CIH_ATT_H(HDV, true, 512);                                                                   \
     else CIH_ATT_H(HDV, true, 256);                                                                             \
-    if (nsplit > 1) {                                                                                           \
+    if (nsplit > 1 && !xsplit) {                                                                                \
         const long n = (long)(tasks - nfull) * QB * (HDV / 4);                                                  \
         hipLaunchKernelGGL((k_attention_merge<HDV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, \
                            tasks - nfull, nsplit, nfull, H, nq, QB, sm.cu, sm.lens, d, out, out_fmt);           \
@@ -1540,6 +1600,12 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
 }
 
 bool attention_img_supported(int hd) { return hd == 16 || hd == 24 || hd == 32 || hd == 64; }
+
+bool attention_wave_split(int B, int S_max, int H) {
+    const char *se = getenv("CIH_ATT_SPLIT"), *ke = getenv("CIH_SPLITK");
+    const long t32 = (long)B * H * ((S_max + 31) / 32);
+    return t32 <= device_cus() && !(se && !strcmp(se, "0")) && !(ke && !strcmp(ke, "0"));
+}
 
 size_t kv_image_bytes(int hd) {
     switch (hd) {

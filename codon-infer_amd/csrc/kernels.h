@@ -308,6 +308,11 @@ hipError_t launch_kv_setup(SeqMeta sm, int hd, int H, int *tb, int *pk, int *pos
 hipError_t launch_kv_prep(const float *qkv, int d, int H, const int *ti, int tile_rows, const float *rope_cos,
                           const float *rope_sin, unsigned char *img, hipStream_t st);
 bool attention_img_supported(int hd);
+// Whether attention of B sequences (at most S_max tokens, H heads) runs each
+// 32-query task on 8 waves that split its keys (k_attention_xs, staging K/V
+// from FP32 rows): when those tasks fit one round of one workgroup per CU,
+// unless CIH_ATT_SPLIT=0 or CIH_SPLITK=0.
+bool attention_wave_split(int B, int S_max, int H);
 size_t kv_image_bytes(int hd);  // bytes of one (tile row, head) image
 
 // final_att[b][p][t] = sum_h P_h[p][t] * (1/H), h ascending

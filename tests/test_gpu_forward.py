@@ -341,17 +341,19 @@ def test_attention_query_block_size_is_invisible(with_maps, monkeypatch):
             assert np.array_equal(a, b), (with_maps, k, i)
 
 
-@pytest.mark.parametrize("case", ["one", "three"])
+@pytest.mark.parametrize("case", ["one", "three", "short"])
 def test_attention_key_split(case, monkeypatch):
     """Attention tasks (sequence, head, query block) that do not fill one round
     of workgroup slots run as key ranges whose partial softmax results a merge
     kernel combines: one 402-token sequence (80 tasks of 128 queries, six
-    ranges), or three ragged sequences.  The forward agrees with the unsplit
-    one (CIH_ATT_SPLIT=0) to 1e-5 and with the oracle to the stated
-    tolerances."""
+    ranges), or three ragged sequences; a 252-token sequence (160 tasks of 32
+    queries, at most one workgroup per CU) runs each 32-query task on 8
+    waves that split its keys (k_attention_xs, one pass).  The forward agrees
+    with the unsplit one (CIH_ATT_SPLIT=0) to 1e-5 and with the oracle to the
+    stated tolerances."""
     rng = np.random.default_rng(77)
     cfg = ch.EsmConfig(320, 1280, 2, 20)
-    lens = [400] if case == "one" else [300, 61, 190]
+    lens = {"one": [400], "three": [300, 61, 190], "short": [250]}[case]
     seqs = [rand_tokens(rng, n) for n in lens]
     w = ch.EsmWeights.random(cfg, seed=77, bias_std=0.02).quantize_q8()
     flags = ch.OUT_LOGITS | ch.OUT_HIDDEN
@@ -374,15 +376,17 @@ def test_attention_key_split(case, monkeypatch):
         assert e <= TOL[k], (case, k, e)
 
 
+@pytest.mark.parametrize("maps", [True, False])
 @pytest.mark.parametrize("hd", [16, 24, 32, 64])
 @pytest.mark.parametrize("case", ["one", "two"])
-def test_attention_export_key_split(hd, case, monkeypatch):
-    """With the probability export, batches whose 32-query tasks do not cover
-    the compute units run each task on 8 waves that split its keys
-    (k_attention_xs): one 256-token sequence (8 tiles, one per wave) or two
-    ragged ones (partial tiles, waves without a tile).  Every output agrees
-    with the one-wave kernel (CIH_ATT_SPLIT=0) to 1e-5 and the maps of the
-    last sequence with the oracle to 1e-5."""
+def test_attention_wave_key_split(hd, case, maps, monkeypatch):
+    """Batches whose 32-query tasks fit one round of one workgroup per CU run
+    each task on 8 waves that split its keys (k_attention_xs; with the
+    probability export, or the one-pass kernel): one 256-token sequence (8
+    tiles, one per wave) or two ragged ones (partial tiles, waves without a
+    tile).  Every output agrees with the unsplit kernels (CIH_ATT_SPLIT=0) to
+    1e-5; the maps of the last sequence agree with the oracle to 1e-5, or
+    its logits to the stated tolerance."""
     rng = np.random.default_rng(hd + (0 if case == "one" else 500))
     d = 20 * hd
     cfg = ch.EsmConfig(d, 4 * d, 2, 20)
@@ -390,7 +394,8 @@ def test_attention_export_key_split(hd, case, monkeypatch):
     seqs = [rand_tokens(rng, n) for n in lens]
     w = ch.EsmWeights.random(cfg, seed=hd, bias_std=0.02).quantize_q8()
     cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
-    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_ATTN | ch.OUT_FINAL_ATT | ch.OUT_CONTACTS
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | ((ch.OUT_ATTN | ch.OUT_FINAL_ATT | ch.OUT_CONTACTS) if maps else 0)
+    keys = ("logits", "hidden") + (("attn", "final_att", "contacts") if maps else ())
     res = {}
     for sp in ("0", "1"):
         monkeypatch.setenv("CIH_ATT_SPLIT", sp)
@@ -400,7 +405,7 @@ def test_attention_export_key_split(hd, case, monkeypatch):
         m.close()
     for i, t in enumerate(seqs):
         n = len(t)
-        for k in ("logits", "hidden", "attn", "final_att", "contacts"):
+        for k in keys:
             a, b = res["1"][k][i], res["0"][k][i]
             if k == "attn":
                 a, b = a[:, :, :n, :n], b[:, :, :n, :n]
@@ -413,10 +418,16 @@ def test_attention_export_key_split(hd, case, monkeypatch):
             e = float(np.abs(a - b).max())
             assert e <= 1e-5, (hd, case, i, k, e)
     n = len(seqs[-1])
-    ref = cr.forward(cfg, w, seqs[-1], 16, attn=True)
-    e = float(np.abs(res["1"]["attn"][-1, :, :, :n, :n] - ref["attn"]).max())
-    print(f"hd {hd} {case}: maps vs oracle {e:.2e}", flush=True)
-    assert e <= 1e-5
+    if maps:
+        ref = cr.forward(cfg, w, seqs[-1], 16, attn=True)
+        e = float(np.abs(res["1"]["attn"][-1, :, :, :n, :n] - ref["attn"]).max())
+        print(f"hd {hd} {case}: maps vs oracle {e:.2e}", flush=True)
+        assert e <= 1e-5
+    else:
+        ref = cr.forward(cfg, w, seqs[-1], 16, final_att=False)
+        e = float(np.abs(res["1"]["logits"][-1, :n].astype(np.float64) - ref["logits"]).max())
+        print(f"hd {hd} {case}: logits vs oracle {e:.2e}", flush=True)
+        assert e <= TOL["logits"]
 
 
 def test_device_io_token_validation():

@@ -13,7 +13,10 @@ GEMM (the epilogue writes the images: sequences start inside 32-row GEMM
 tiles, so both the whole-line and the element-wise V stores run; head size
 24, which has no epilogue form, takes the prep kernel there), a small batch,
 the prep kernel (CIH_ATT_IMG=prep: images from FP32 rows at any size) and
-every layer's maps (the two-pass export kernel).
+every layer's maps (the two-pass export kernel).  The key splits are off
+(CIH_ATT_SPLIT=0): batches small enough for attention's split over waves
+stage K/V themselves under every setting, and the split regroups sums
+(test_gpu_forward covers it).
 """
 import numpy as np
 import pytest
@@ -31,6 +34,7 @@ def run_paths(monkeypatch, cfg, w, seqs, flags):
     """Outputs of the default path, the staged path (CIH_ATT_IMG=0), the prep
     kernel's images (CIH_ATT_IMG=prep) and the default path again."""
     monkeypatch.setenv("CIH_FORWARD_GRAPH", "0")
+    monkeypatch.setenv("CIH_ATT_SPLIT", "0")
     m = ch.GpuModel(cfg, w, max_batch=len(seqs), max_len=max(len(s) for s in seqs), outputs=flags)
     out = {"default": m.forward(seqs, flags)}
     for tag, v in (("staged", "0"), ("prep", "prep")):
