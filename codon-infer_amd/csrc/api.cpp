@@ -409,9 +409,9 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         epi_img = use_img && !prep_only && af == AF_H2 && (m->hd == 16 || m->hd == 32 || m->hd == 64) &&
                   gemm_lds_applies(m->layers[0].wqkv, af, T, EPI_NONE);
         // without the epilogue, images cost a prep kernel per layer: it pays
-        // from 2048 tokens on, except at head size 24 (35M B=8 ragged: prep
-        // 8.5 us, attention 41.2 -> 33.5 us per layer; net loss)
-        if (!epi_img && !prep_only && (T < 2048 || m->hd == 24)) use_img = false;
+        // from 2048 tokens on (35M B=8 ragged, head size 24: prep 8.3 us,
+        // attention 38.6 -> 28.8 us per layer)
+        if (!epi_img && !prep_only && T < 2048) use_img = false;
         // batches small enough for attention's split over waves stage K/V
         // there (from FP32 rows; images would take the kernel without it)
         if (!epi_img && attention_wave_split(B, S_max, H)) use_img = false;
