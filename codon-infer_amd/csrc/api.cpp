@@ -152,7 +152,7 @@ void profile_collect(cih_model *m) {
     m->prof.used = 0;
 }
 
-size_t model_part_floats(const cih_model *m) {
+size_t model_part_floats(const cih_model *m, size_t tokens) {
     size_t pf = 0;
     std::vector<const DevMatrix *> mats = {&m->emb};
     if (m->has_head) mats.insert(mats.end(), {&m->dense, &m->dec});
@@ -161,7 +161,10 @@ size_t model_part_floats(const cih_model *m) {
         mats.insert(mats.end(), {&ly.wqkv, &ly.wo, &ly.w1, &ly.w2});
     }
     for (const DevMatrix *w : mats) pf = std::max(pf, gemv_part_floats(w->N, w->K));
-    return std::max(pf, SPLITK_PART_FLOATS);
+    // the LDS GEMM's split-K form (residual projections, N = dim): up to 4
+    // splits of tokens x dim while that is below 256 tiles of 128 x 128
+    const size_t split = std::min(tokens * m->cfg.dim, (size_t)256 * 128 * 128) * 4;
+    return std::max({pf, SPLITK_PART_FLOATS, split});
 }
 
 // RoPE tables (BidirectionalRunState::new / RunState::new, lib.rs:2513-2522,
@@ -243,7 +246,7 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
                 ok(dalloc(ws.logits, T * V, dl)) && ok(dalloc(ws.rope_c, S * half, dl)) &&
                 ok(dalloc(ws.rope_s, S * half, dl));
     if (good) {
-        ws.part.floats = model_part_floats(m);
+        ws.part.floats = model_part_floats(m, T);
         const size_t nd = std::max(B, S);
         ws.attp_floats = attention_part_floats((int)m->hd);
         good = ok(dalloc(ws.part.part, ws.part.floats, dl)) && ok(dalloc(ws.dms_meta, nd * 2, dl)) &&

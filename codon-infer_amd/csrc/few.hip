@@ -103,10 +103,88 @@ __global__ __launch_bounds__(RLN_MAX_THREADS) void k_rln(float *__restrict__ x, 
     }
 }
 
+// The same for many rows: one wave per row, four rows per workgroup, lane l
+// owning column quads l, l + 64, ... (PER of them) as k_layernorm4 does; the
+// fold, the mean and variance sums and their order are k_rln's, so both give
+// the same bits.
+template <int PER, int OF>
+__global__ __launch_bounds__(256) void k_rln4(float *__restrict__ x, const float *__restrict__ part, int S,
+                                              const float *__restrict__ pb, const float *__restrict__ w,
+                                              const float *__restrict__ b, void *__restrict__ out, int rows, int d,
+                                              int *__restrict__ flag) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int n4 = d >> 2;
+    f32x4 *xr = reinterpret_cast<f32x4 *>(x + (size_t)row * d);
+    f32x4 v[PER], g[PER], be[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = min(lane + 64 * i, n4 - 1);  // past the row: re-read, masked below
+        v[i] = xr[c];
+        g[i] = reinterpret_cast<const f32x4 *>(w)[c];
+        be[i] = reinterpret_cast<const f32x4 *>(b)[c];
+    }
+    if (part) {
+        const size_t stride = (size_t)rows * d;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int c = min(lane + 64 * i, n4 - 1);
+            const f32x4 acc = fold_splits4(part + (size_t)row * d + 4 * c, S, stride);
+            const f32x4 bb = reinterpret_cast<const f32x4 *>(pb)[c];
+            v[i] = v[i] + (acc + bb);
+            if (lane + 64 * i < n4) xr[c] = v[i];
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++)
+        if (lane + 64 * i < n4) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    const float mean = s / (float)d;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const f32x4 t = v[i] - mean;
+        if (lane + 64 * i < n4) q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+    const float var = q / (float)d;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+    if (flag && lane == 0 && !(__builtin_isfinite(mean) && __builtin_isfinite(var))) atomicOr(flag, FLAG_NONFINITE);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = lane + 64 * i;
+        if (c >= n4) break;
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+        if constexpr (OF == AF_H2)
+            h2_store4(reinterpret_cast<unsigned short *>(out), row, 4 * c, d, make_float4(y.x, y.y, y.z, y.w));
+        else
+            reinterpret_cast<f32x4 *>(out)[(size_t)row * n4 + c] = y;
+    }
+}
+
 template <int OF>
 static hipError_t launch_rln_t(float *x, const float *part, int S, const float *pbias, const float *w, const float *b,
                                void *out, int rows, int d, int *flag, hipStream_t st) {
     const int n4 = d / 4;
+    // many rows: one wave each, four rows per workgroup (the few-row form
+    // spreads a row over up to 1024 threads: faster below ~1024 rows)
+    if (rows >= 1024 && n4 <= 640) {
+        const int per = (n4 + 63) / 64;
+        const dim3 grid4((rows + 3) / 4), blk4(256);
+#define CIH_RLN4(P) hipLaunchKernelGGL((k_rln4<P, OF>), grid4, blk4, 0, st, x, part, S, pbias, w, b, out, rows, d, flag)
+        if (per <= 2) CIH_RLN4(2);
+        else if (per == 3) CIH_RLN4(3);
+        else if (per == 4) CIH_RLN4(4);
+        else if (per == 5) CIH_RLN4(5);
+        else CIH_RLN4(10);
+#undef CIH_RLN4
+        return hipGetLastError();
+    }
     const int q = (n4 + RLN_MAX_THREADS - 1) / RLN_MAX_THREADS;
     const int nt = (n4 + q - 1) / q;
     const dim3 grid(rows), blk((nt + 63) / 64 * 64);

@@ -30,6 +30,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -300,10 +301,15 @@ __device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned cha
 // register path: v_perm puts each byte (Q8_0: + 128; Q4_0: the lane's
 // nibble) under the f16 exponent of 1024, a packed f16 subtraction removes
 // the offset (1.25 VALU per weight).
-template <int EPI, int RT, int CT, int WM, int WN, int WQ>
+//
+// SPLIT: workgroup (tile, y) takes k-blocks [y kps, (y + 1) kps) and stores
+// its raw sums (no bias, no epilogue) into part + y M N, row-major [M][N];
+// the caller adds the splits in order (EPI_NONE only).
+template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false>
 __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned char *__restrict__ WB, const float *__restrict__ Wsc,
-    const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo) {
+    const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo, int kps = 0) {
+    static_assert(!SPLIT || EPI == EPI_NONE, "split partial sums carry no epilogue");
     constexpr int BPC = WQ == WF_Q8 ? 32 : (WQ == WF_Q4 ? 16 : 64);
     using T = LdsTile<RT, CT, WM, WN, BPC>;
     constexpr int BM = T::BM, BN = T::BN, NW = T::NW, SA = T::SA, SB = T::SB, STAGE = T::STAGE, NA = T::NA,
@@ -327,6 +333,12 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     tile_xcd(blockIdx.x, nM * nN, nM, nN, mt, nt);
     const int m0 = mt * BM, n0 = nt * BN;
     const int KB = K / 32;
+    // k-blocks [kb0, kb1) of this workgroup
+    const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kb1 = SPLIT ? min(KB, kb0 + kps) : KB;
+    if constexpr (SPLIT) {
+        Yv = reinterpret_cast<float *>(Yv) + (size_t)blockIdx.y * M * N;
+        ldy = N;
+    }
 
     // Per-lane sources at k-block 0.  Load instruction j fills LDS bytes
     // [j * 1024, +1024) of its region, lane l the 16 bytes at l * 16: LDS
@@ -512,8 +524,8 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     };
     // Requests past the last block re-read it into a stage nobody reads again,
     // so every wave issues the same instructions and the counts hold.
-    request(0, 0);
-    request(min(1, KB - 1), 1);
+    request(kb0, 0);
+    request(min(kb0 + 1, kb1 - 1), 1);
     if constexpr (PREF) {
         int *s_pk = reinterpret_cast<int *>(lds + LOFF), *s_pos = s_pk + BM;
         if (tid < BM) {
@@ -533,19 +545,19 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             }
         }
     }
-    for (int kb = 0;;) {
+    for (int kb = kb0;;) {
         sync();
-        request(min(kb + 2, KB - 1), 2);
+        request(min(kb + 2, kb1 - 1), 2);
         compute(0);
-        if (++kb == KB) break;
+        if (++kb == kb1) break;
         sync();
-        request(min(kb + 2, KB - 1), 0);
+        request(min(kb + 2, kb1 - 1), 0);
         compute(1);
-        if (++kb == KB) break;
+        if (++kb == kb1) break;
         sync();
-        request(min(kb + 2, KB - 1), 1);
+        request(min(kb + 2, kb1 - 1), 1);
         compute(2);
-        if (++kb == KB) break;
+        if (++kb == kb1) break;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if constexpr (RT >= 2) {
@@ -652,6 +664,27 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     return hipGetLastError();
 }
 
+// Split-K form on 128 x 128 tiles: grid (tiles, S), raw partial sums into part.
+hipError_t launch_split(const DevMatrix &W, const void *X, int M, float *part, int S, int kps, hipStream_t st) {
+    using T = LdsTile<2, 2, 2, 2>;
+    const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
+    const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
+    const dim3 grid(tiles, S), block(T::THREADS);
+    if (!W.q16 && W.fmt == WF_Q8)
+        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, 2, 2, 2, 2, WF_Q8, true>), grid, block, 0, st, Xh,
+                           static_cast<const unsigned char *>(W.q), W.sc, nullptr, part, W.N, M, W.N, W.K, QkvOut(),
+                           kps);
+    else if (!W.q16)
+        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, 2, 2, 2, 2, WF_Q4, true>), grid, block, 0, st, Xh,
+                           static_cast<const unsigned char *>(W.q), W.sc, nullptr, part, W.N, M, W.N, W.K, QkvOut(),
+                           kps);
+    else
+        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, 2, 2, 2, 2, 0, true>), grid, block, 0, st, Xh,
+                           reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
+                           QkvOut(), kps);
+    return hipGetLastError();
+}
+
 // Tile choice by a model of the time the rounds of workgroups take on the
 // device's CUs.  Candidates, in order of preference (fewest operand bytes per
 // output first): 128 x 320 and 128 x 256 (8 waves, one workgroup per CU),
@@ -721,6 +754,38 @@ bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi) {
     if (e && !strcmp(e, "0")) return false;
     if (e && !strcmp(e, "force")) return true;
     return (long)((M + 127) / 128) * ((W.N + 127) / 128) >= 256;
+}
+
+bool gemm_lds_split_applies(const DevMatrix &W, int a_fmt, int M, int epi) {
+    if (a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || W.K % 32 || M <= 0 || W.N <= 0) return false;
+    if (epi != EPI_NONE && epi != EPI_RESIDUAL) return false;
+    const char *e = getenv("CIH_GEMM_LDS"), *ke = getenv("CIH_SPLITK");
+    if ((e && !strcmp(e, "0")) || (ke && !strcmp(ke, "0"))) return false;
+    // the splits cost their partial sums' traffic (S M N floats written here
+    // and read by the caller's fold, 11-13 us per split projection on top of
+    // the LayerNorm at 4096 x 640 and 2550 x 1280): only deep products over
+    // many rows gain more than that (650M FC2, K = 5120, 2550 rows: 82 -> 56
+    // us; K = 640 to 2560: no net gain; 402 rows: the register-staged split
+    // is faster)
+    const long tiles = (long)((M + 127) / 128) * ((W.N + 127) / 128);
+    return tiles >= 32 && tiles < 256 && W.K >= 4096 && M >= 1024;
+}
+
+hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const PartialBuf &pb, int *splits,
+                                 hipStream_t st) {
+    *splits = 0;
+    if ((W.fmt != WF_Q8 && W.fmt != WF_Q4) || W.K % 32 || M <= 0 || W.N <= 0 || !pb.part) return hipErrorInvalidValue;
+    // two 4-wave workgroups per CU: splits up to one round of them, at least
+    // 4 k-blocks each, partial sums within pb
+    const int KB = W.K / 32;
+    const long tiles = (long)((M + 127) / 128) * ((W.N + 127) / 128);
+    int S = (int)std::min<long>(2L * device_cus() / tiles, KB / 4);
+    while (S > 1 && (size_t)S * M * W.N > pb.floats) S--;
+    if (S < 2) return hipSuccess;
+    const int kps = (KB + S - 1) / S;
+    S = (KB + kps - 1) / kps;
+    *splits = S;
+    return launch_split(W, X, M, pb.part, S, kps, st);
 }
 
 hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,

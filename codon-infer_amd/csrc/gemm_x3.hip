@@ -583,6 +583,15 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
     if ((epi == EPI_GELU_X3 || epi == EPI_GELU_H2) && W.N % 32 != 0) return hipErrorInvalidValue;
     if (gemm_lds_applies(W, a_fmt, M, epi)) return launch_gemm_lds(W, X, bias, Y, ldy, M, epi, st);
+    // a caller that adds the splits itself: the LDS kernel split over K
+    if (defer && pb && gemm_lds_split_applies(W, a_fmt, M, epi)) {
+        int S = 0;
+        const hipError_t e = launch_gemm_lds_split(W, X, M, *pb, &S, st);
+        if (e != hipSuccess || S > 1) {
+            *defer = S;
+            return e;
+        }
+    }
     // FP32 activations: f16 two-limb split unless CIH_LIMBS=bf16x3
     const char *lv = getenv("CIH_LIMBS");
     const bool bf16 = (lv && !strcmp(lv, "bf16x3")) || full_range_mode();

@@ -210,6 +210,13 @@ hipError_t launch_to_h2(const float *x, int M, int K, unsigned short *out, hipSt
 bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi);
 hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
                            hipStream_t st, const QkvOut *qo = nullptr);
+// Split-K form for shapes whose 128 x 128 tiles do not fill one round (32 to
+// 255 tiles; EPI_NONE / EPI_RESIDUAL, whose caller adds the splits): raw
+// partial sums X * W^T over k-ranges into pb.part as [S][M][N], *splits = S
+// (0: no split fits, nothing launched).
+bool gemm_lds_split_applies(const DevMatrix &W, int a_fmt, int M, int epi);
+hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const PartialBuf &pb, int *splits,
+                                 hipStream_t st);
 // W.q16 from W.q (quantized W, k-block-major), on stream st.
 hipError_t launch_expand_f16(const DevMatrix &W, unsigned short *q16, hipStream_t st);
 // The pair copy (p16, psc) of an FP32 matrix W, on stream st.

@@ -180,7 +180,8 @@ hipError_t model_gemm(cih_model *m, const PartialBuf &pb, const DevMatrix &W, co
 // call (event pairs of model_gemm and friends) to the per-class totals.
 void profile_collect(cih_model *m);
 // partial-sum floats any GEMM / GEMV of the model needs
-size_t model_part_floats(const cih_model *m);
+// partial-sum floats a workspace for `tokens` tokens needs (split GEMMs and GEMVs)
+size_t model_part_floats(const cih_model *m, size_t tokens = 0);
 // RoPE cos / sin tables [max_len][hd/2] as the reference computes them
 void rope_tables_host(size_t max_len, int hd, std::vector<float> &c, std::vector<float> &s);
 
