@@ -136,6 +136,27 @@ __device__ __forceinline__ float residue_sum(const float (&p)[16], int k0, int l
     return s;
 }
 
+// residue_sum over the 32-key tile from kt0: when every key of the tile is a
+// residue (1 <= kt0, kt0 + 31 <= len - 2) the masks are all true and the
+// plain sum in the same order gives the same value.
+__device__ __forceinline__ float tile_residue_sum(const float (&p)[16], int kt0, int hh, int len) {
+    if (kt0 >= 1 && kt0 + 33 <= len) {
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) s += p[q];
+        return s;
+    }
+    return residue_sum(p, kt0 + 4 * hh, len);
+}
+
+// store_p for a whole tile (kt0 + 32 <= len) of a 16-byte aligned row: four
+// unconditional 16-byte stores
+__device__ __forceinline__ void store_p_whole(float *Prow, const float (&p)[16], int k0) {
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+        *reinterpret_cast<float4 *>(Prow + k0 + 8 * g) = make_float4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
+}
+
 // rowsum[b][h][qi] for residue queries: the two lane halves hold disjoint keys.
 __device__ __forceinline__ void write_rowsum(float *rowsum, float rs, int b, int h, int H, int S_max, int qi, int len,
                                              int hh) {
@@ -735,7 +756,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - mx) * inv_sum : 0.0f;
             }
             if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
-            if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
+            if (rowsum) rs += tile_residue_sum(p, kt0, hh, len);
             pv(oacc, p);
         });
         write_rowsum(rowsum, rs, b, h, H, S_max, qi, len, hh);
@@ -1076,7 +1097,7 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
                 p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - M) * inv_sum : 0.0f;
             }
             if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
-            if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
+            if (rowsum) rs += tile_residue_sum(p, kt0, hh, len);
             pv(oacc, p);
         }
         red[w][2][lane] = rs;
@@ -1312,7 +1333,8 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     } else {
         // pass 1 (K limbs only): running max / sum of exp per lane
         float m = -INFINITY, l = 0.0f;
-        sweep(std::false_type{}, [&](const unsigned char *st, int kt0, auto) __attribute__((always_inline)) {
+        sweep(std::false_type{}, [&](const unsigned char *st, int kt0, auto masked) __attribute__((always_inline)) {
+            constexpr bool MASKED = decltype(masked)::value;  // whole tiles: every key is < len
             f32x16 acc;
             scores(st, acc, 0.0f);
             float sv[16];
@@ -1320,7 +1342,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
+                sv[q] = !MASKED || key < len ? acc[q] * sl2 : -INFINITY;
                 tmax = fmaxf(tmax, sv[q]);
             }
             const float mn = fmaxf(m, tmax);
@@ -1337,18 +1359,23 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         const float inv_sum = 1.0f / (l * __builtin_amdgcn_exp2f(m - mx) + lo * __builtin_amdgcn_exp2f(mo - mx));
         // pass 2: normalized probabilities, optional export, P.V
         float *Prow = (P && qi < len) ? P + b * pb + h * ph + (size_t)qi * S_max : nullptr;
+        const bool p_al = P && ((uintptr_t)P & 15) == 0 && ((pb | ph | (long long)S_max) & 3) == 0;
         float rs = 0.0f;
-        sweep(std::true_type{}, [&](const unsigned char *st, int kt0, auto) __attribute__((always_inline)) {
+        sweep(std::true_type{}, [&](const unsigned char *st, int kt0, auto masked) __attribute__((always_inline)) {
+            constexpr bool MASKED = decltype(masked)::value;  // whole tiles: every key is < len
             f32x16 acc;
             scores(st, acc, 0.0f);
             float p[16];
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - mx) * inv_sum : 0.0f;
+                p[q] = !MASKED || key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - mx) * inv_sum : 0.0f;
             }
-            if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
-            if (rowsum) rs += residue_sum(p, kt0 + 4 * hh, len);
+            if (Prow) {
+                if (!MASKED && p_al) store_p_whole(Prow, p, kt0 + 4 * hh);
+                else store_p(Prow, p, kt0 + 4 * hh, len);
+            }
+            if (rowsum) rs += tile_residue_sum(p, kt0, hh, len);
             pv(st, oacc, p);
         });
         write_rowsum(rowsum, rs, b, h, H, S_max, qi, len, hh);
