@@ -471,9 +471,9 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
             Vl[bf * VBUF + c * V_LD + key] = (_Float16)0.0f;
         }
 
-    // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs; the
-    // one-pass kernel takes them pre-scaled by log2(e) / sqrt(hd), so its
-    // scores come out of the MFMAs in base-2 units
+    // rotated query dims 16c + 8hh + e of this lane's query, as f16 limbs,
+    // pre-scaled by log2(e) / sqrt(hd): the scores come out of the MFMAs in
+    // base-2 units
     const float sl2 = inv_scale * 1.44269504088896340736f;
     const int qi = qblk + wave * 32 + li;
     const int qc = min(qi, len - 1);
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 float r = 0.0f;
                 if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
                 else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
-                v[e] = ONEPASS ? opaque(r * sl2) : r;
+                v[e] = opaque(r * sl2);
             }
             split8(v, qh[c], ql[c]);
         }
@@ -625,13 +625,11 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         out_scale = 1.0f / lt;
     } else {
         // Two passes over the keys (the exported probabilities are final, so
-        // the row max and sum come first), base-2 exponentials of scores
-        // pre-scaled by log2(e) / sqrt(hd).  With one 32-query wave per SIMD
-        // slot and few waves, a tile's global loads are the critical path:
-        // they go to registers one tile ahead (fetch) and into LDS as f16
-        // limbs after the barrier (stage), so tile t+1 is in flight while
-        // tile t is computed.
-        const float sl2 = inv_scale * 1.44269504088896340736f;
+        // the row max and sum come first), base-2 exponentials of the
+        // pre-scaled scores.  With one 32-query wave per SIMD slot and few
+        // waves, a tile's global loads are the critical path: they go to
+        // registers one tile ahead (fetch) and into LDS as f16 limbs after the
+        // barrier (stage), so tile t+1 is in flight while tile t is computed.
         constexpr int KG = HALF / 4, KI = (32 * KG + NTH - 1) / NTH, VI = (8 * HD + NTH - 1) / NTH;
         f32x4 kr[KI][4], vr[VI];
         auto fetch = [&](int kt0, bool with_v) __attribute__((always_inline)) {
@@ -728,7 +726,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
+                sv[q] = key < len ? acc[q] : -INFINITY;
                 tmax = fmaxf(tmax, sv[q]);
             }
             const float mn = fmaxf(m, tmax);
@@ -753,7 +751,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - mx) * inv_sum : 0.0f;
+                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] - mx) * inv_sum : 0.0f;
             }
             if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
             if (rowsum) rs += tile_residue_sum(p, kt0, hh, len);
@@ -869,7 +867,7 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
                 float r = 0.0f;
                 if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
                 else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
-                v[e] = ONEPASS ? opaque(r * sl2) : r;  // one pass: pre-scaled, as in k_attention_h
+                v[e] = opaque(r * sl2);  // pre-scaled, as in k_attention_h
             }
             split8(v, qh[c], ql[c]);
         }
@@ -1044,7 +1042,7 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                sv[q] = key < len ? acc[q] * sl2 : -INFINITY;
+                sv[q] = key < len ? acc[q] : -INFINITY;
                 tmax = fmaxf(tmax, sv[q]);
             }
             const float mn = fmaxf(m, tmax);
@@ -1094,7 +1092,7 @@ __global__ __launch_bounds__(64 * KS) void k_attention_xs(const float *__restric
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - M) * inv_sum : 0.0f;
+                p[q] = key < len ? __builtin_amdgcn_exp2f(acc[q] - M) * inv_sum : 0.0f;
             }
             if (Prow) store_p(Prow, p, kt0 + 4 * hh, len);
             if (rowsum) rs += tile_residue_sum(p, kt0, hh, len);
@@ -1226,7 +1224,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
                 float r = 0.0f;
                 if (dim < HALF) r = rot_lo(qrow[dim], qrow[dim + HALF], cs[dim], sn[dim]);
                 else if (dim < HD) r = rot_hi(qrow[dim], qrow[dim - HALF], cs[dim - HALF], sn[dim - HALF]);
-                v[e] = ONEPASS ? opaque(r * sl2) : r;
+                v[e] = opaque(r * sl2);
             }
             split8_mix(v, qh[c], ql[c]);
         }
@@ -1342,7 +1340,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                sv[q] = !MASKED || key < len ? acc[q] * sl2 : -INFINITY;
+                sv[q] = !MASKED || key < len ? acc[q] : -INFINITY;
                 tmax = fmaxf(tmax, sv[q]);
             }
             const float mn = fmaxf(m, tmax);
@@ -1369,7 +1367,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int key = kt0 + 8 * (q >> 2) + 4 * hh + (q & 3);
-                p[q] = !MASKED || key < len ? __builtin_amdgcn_exp2f(acc[q] * sl2 - mx) * inv_sum : 0.0f;
+                p[q] = !MASKED || key < len ? __builtin_amdgcn_exp2f(acc[q] - mx) * inv_sum : 0.0f;
             }
             if (Prow) {
                 if (!MASKED && p_al) store_p_whole(Prow, p, kt0 + 4 * hh);
