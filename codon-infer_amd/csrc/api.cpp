@@ -40,7 +40,8 @@ std::string kernel_switches() {
     static const char *const names[] = {"CIH_ATT",     "CIH_ATT_QB", "CIH_ATT_SPLIT", "CIH_SPLITK",
                                         "CIH_QGEMM",   "CIH_ACT",    "CIH_LIMBS",     "CIH_GEMV",
                                         "CIH_GEMV_NB", "CIH_GEMM_LDS", "CIH_GEMM_TILE", "CIH_GEMM_TILE_N",
-                                        "CIH_GEMM_TILE_N_GELU", "CIH_ATT_IMG", "CIH_GEMV16", "CIH_GEMV16_KW"};
+                                        "CIH_GEMM_TILE_N_GELU", "CIH_ATT_IMG", "CIH_GEMV16", "CIH_GEMV16_KW",
+                                        "CIH_FEW_WO"};
     std::string s = g_full_range ? "R|" : "|";
     for (const char *n : names) {
         const char *v = getenv(n);
@@ -385,6 +386,7 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     // LayerNorm (or a per-layer hidden-state export).
     const bool few = af == AF_H2 && T <= GEMV_MAX_M;
     const size_t part_half = ws.part.floats / 2 / 64 * 64;
+    const char *few_wo_env = getenv("CIH_FEW_WO");
     float *const part_a = ws.part.part, *const part_b = ws.part.part + part_half;
     int pend_splits = 0;  // FC2 splits waiting in part_a
     const float *pend_bias = nullptr;
@@ -473,7 +475,18 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
                              wbytes(ly.wqkv) + 4.0 * T * d + 4.0 * T * 3 * d);
                 HIPCHK(launch_gemv16_partials(ly.wqkv, (const unsigned short *)ws.xb, T, part_b, part_half, &sq, st));
             }
-            if (!need_P && m->hd % 8 == 0 && m->hd <= FEW_MAX_HD) {
+            // head sizes of whole 32-wide blocks: attention and Wo in one kernel
+            // (each head's share of Wo, the heads as splits); CIH_FEW_WO=0: apart
+            const bool fuse_wo = !need_P && m->hd % 32 == 0 && m->hd <= FEW_MAX_HD &&
+                                 (ly.wo.fmt == WF_Q8 || ly.wo.fmt == WF_Q4) && (size_t)H * T * d <= part_half &&
+                                 !(few_wo_env && !std::strcmp(few_wo_env, "0"));
+            if (fuse_wo) {
+                double fl = 0;
+                for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
+                ProfScope ps(m, CIH_KC_ATTENTION, fl + 2.0 * T * ly.wo.N * ly.wo.K, 16.0 * T * d + wbytes(ly.wo));
+                HIPCHK(launch_attention_few_wo(part_b, sq, T, ly.bqkv, ly.wo, d, H, sm, ws.rope_c, ws.rope_s, part_a,
+                                               part_half, st));
+            } else if (!need_P && m->hd % 8 == 0 && m->hd <= FEW_MAX_HD) {
                 double fl = 0;
                 for (int b = 0; b < B; b++) fl += 4.0 * (double)lens[b] * lens[b] * d;
                 ProfScope ps(m, CIH_KC_ATTENTION, fl, 16.0 * T * d);
@@ -499,8 +512,8 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
                 ProfScope ps(m, CIH_KC_OTHER, 0, 0);
                 HIPCHK(launch_head_mean(P, pb, ph, H, sm, t_final, st));
             }
-            int so = 0, s1 = 0, s2 = 0;
-            {
+            int so = fuse_wo ? H : 0, s1 = 0, s2 = 0;
+            if (!fuse_wo) {
                 ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * T * ly.wo.N * ly.wo.K, wbytes(ly.wo) + 8.0 * T * d);
                 HIPCHK(launch_gemv16_partials(ly.wo, (const unsigned short *)ws.ao, T, part_a, part_half, &so, st));
             }

@@ -11,6 +11,7 @@
 //
 // Partial sums are added in split order (fold_splits), so results do not
 // depend on scheduling.
+#include <algorithm>
 #include <cmath>
 
 #include "kernels.h"
@@ -323,6 +324,220 @@ __global__ __launch_bounds__(ATTF_THREADS) void k_attn_few(const float *__restri
         if constexpr (OF == AF_H2) h2_store(static_cast<unsigned short *>(out), r0 + i, h * hd + j, d, a);
         else static_cast<float *>(out)[(size_t)(r0 + i) * d + h * hd + j] = a;
     }
+}
+
+// k_attn_few followed by this head's share of the output projection Wo
+// (Q8_0 / Q4_0, k-block-major), for head sizes that are whole 32-wide
+// blocks: workgroup (sequence b, head h, column chunk z) forms the head's
+// output o (n tokens x hd, FP32, in LDS) as k_attn_few does, splits it into
+// f16 limbs as the GEMV's operand (A row = token + 8 limb, lane l holds
+// A[l % 16][8 (l / 16) ..]) and multiplies it by Wo's k-blocks of the head
+// for columns [z ncols, (z + 1) ncols) on v_mfma_f32_16x16x32_f16, each
+// block's sum times its scale, as k_gemv16 does.  opart [H][T][N]: the head
+// is the split, which the residual LayerNorm after it adds (with bo).
+template <int WF>
+__global__ __launch_bounds__(ATTF_THREADS) void k_attn_few_wo(const float *__restrict__ part, int S, int T,
+                                                              const float *__restrict__ bias, int d, int hd,
+                                                              const int *__restrict__ cu, const int *__restrict__ lens,
+                                                              const float *__restrict__ rc,
+                                                              const float *__restrict__ rs, float inv_scale,
+                                                              const unsigned char *__restrict__ Wq,
+                                                              const float *__restrict__ Wsc, int N, int ncols,
+                                                              float *__restrict__ opart) {
+    typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+    typedef unsigned u2_t __attribute__((ext_vector_type(2)));
+    typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+    constexpr int RW = FEW_MAX_HD + 4;
+    constexpr int KBH = FEW_MAX_HD / 32;  // k-blocks of a head, at most
+    __shared__ float qkv[3][GEMV_MAX_M][RW];
+    __shared__ float p[GEMV_MAX_M][GEMV_MAX_M];
+    const int b = blockIdx.x, h = blockIdx.y;
+    const int half = hd / 2, hq = hd / 4, pq = hd / 8;
+    const size_t stride = (size_t)T * 3 * d;
+    const int len = lens[b], r0 = cu[b];
+    // q, k, v of the head, folded, with RoPE (as k_attn_few)
+    const int nqk = 2 * T * pq, nitem = nqk + T * hq;
+    const int it = min((int)threadIdx.x, nitem - 1);
+    const bool pair = it < nqk;
+    int which, r, j;
+    if (pair) {
+        which = it / (T * pq);
+        const int rem = it - which * T * pq;
+        r = rem / pq;
+        j = 4 * (rem - r * pq);
+    } else {
+        which = 2;
+        const int rem = it - nqk;
+        r = rem / hq;
+        j = 4 * (rem - r * hq);
+    }
+    const float *src = part + (size_t)r * 3 * d + which * d + h * hd + j;
+    const int up = pair ? half : 0;
+    fold4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < S; s0 += FOLD_CHUNK) {
+        fold4_t v0[FOLD_CHUNK], v1[FOLD_CHUNK];
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++) {
+            const bool in = s0 + u < S;
+            v0[u] = in ? *reinterpret_cast<const fold4_t *>(src + (size_t)(s0 + u) * stride) : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            v1[u] = in && pair ? *reinterpret_cast<const fold4_t *>(src + up + (size_t)(s0 + u) * stride)
+                               : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < FOLD_CHUNK; u++) {
+            a0 += v0[u];
+            a1 += v1[u];
+        }
+    }
+    const float *bp = bias + which * d + h * hd + j;
+    a0 += *reinterpret_cast<const fold4_t *>(bp);
+    if (pair) a1 += *reinterpret_cast<const fold4_t *>(bp + up);
+    const int n = min(len, GEMV_MAX_M), pos = r - r0;
+    if (pair && pos >= 0 && pos < n) {
+        const fold4_t c = *reinterpret_cast<const fold4_t *>(rc + (size_t)pos * half + j);
+        const fold4_t sn = *reinterpret_cast<const fold4_t *>(rs + (size_t)pos * half + j);
+        fold4_t lo, hi;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            lo[t] = __fsub_rn(__fmul_rn(a0[t], c[t]), __fmul_rn(a1[t], sn[t]));
+            hi[t] = __fadd_rn(__fmul_rn(a1[t], c[t]), __fmul_rn(a0[t], sn[t]));
+        }
+        a0 = lo;
+        a1 = hi;
+    }
+    if ((int)threadIdx.x < nitem) {
+        *reinterpret_cast<fold4_t *>(&qkv[which][r][j]) = a0;
+        if (pair) *reinterpret_cast<fold4_t *>(&qkv[which][r][j + half]) = a1;
+    }
+    if (n <= 0) return;  // uniform: no barrier follows for this workgroup
+    // this workgroup's Wo columns and the head's k-blocks: weights and scales
+    // requested now, used after the attention
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+    const int nkb = hd / 32, kb0 = h * nkb;
+    const int npass = (ncols + 127) / 128;
+    constexpr int MAXP = 4;  // column passes of 8 waves x 16 columns (ncols <= 512)
+    u2_t wq[MAXP][KBH];
+    float dsc[MAXP][KBH];
+#pragma unroll
+    for (int ps = 0; ps < MAXP; ps++) {
+        const int col = min((int)blockIdx.z * ncols + 128 * ps + 16 * w + c16, N - 1);
+#pragma unroll
+        for (int k = 0; k < KBH; k++) {
+            if (ps >= npass || k >= nkb) continue;
+            const size_t blk = (size_t)(kb0 + k) * N + col;
+            if constexpr (WF == WF_Q8) wq[ps][k] = *reinterpret_cast<const u2_t *>(Wq + blk * 32 + 8 * g);
+            else wq[ps][k] = *reinterpret_cast<const u2_t *>(Wq + blk * 16 + 8 * (g & 1));
+            dsc[ps][k] = Wsc[blk];
+        }
+    }
+    __syncthreads();
+    // scores and softmax (as k_attn_few)
+    if (threadIdx.x < 64) {
+        const int i = threadIdx.x >> 3, jj = threadIdx.x & 7;
+        const bool live = i < n && jj < n;
+        const f32x4 *qr = reinterpret_cast<const f32x4 *>(qkv[0][r0 + min(i, n - 1)]);
+        const f32x4 *kr = reinterpret_cast<const f32x4 *>(qkv[1][r0 + min(jj, n - 1)]);
+        float a = 0.0f;
+#pragma unroll 8
+        for (int k = 0; k < hq; k++) {
+            const f32x4 x = qr[k], y = kr[k];
+            a = fmaf(x.x, y.x, a);
+            a = fmaf(x.y, y.y, a);
+            a = fmaf(x.z, y.z, a);
+            a = fmaf(x.w, y.w, a);
+        }
+        const float sc = live ? a * inv_scale : -INFINITY;
+        float mx = sc;
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float e = live ? expf(sc - mx) : 0.0f;
+        float sum = e;
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o);
+        p[i][jj] = e * (1.0f / sum);
+    }
+    __syncthreads();
+    // o = P v into the q rows of this sequence (q is no longer read)
+    for (int e = threadIdx.x; e < n * hd; e += ATTF_THREADS) {
+        const int i = e / hd, jj = e - i * hd;
+        float a = 0.0f;
+#pragma unroll
+        for (int t = 0; t < GEMV_MAX_M; t++)
+            if (t < n) a = fmaf(p[i][t], qkv[2][r0 + t][jj], a);
+        qkv[0][r0 + i][jj] = a;
+    }
+    __syncthreads();
+    // the GEMV operand: row c16 = token (c16 & 7) limb (c16 >> 3), dims 32 k + 8 g ..
+    h8_t xa[KBH];
+    {
+        const int tok = min(c16 & 7, n - 1), limb = c16 >> 3;
+        const float *orow = qkv[0][r0 + tok];
+#pragma unroll
+        for (int k = 0; k < KBH; k++) {
+            if (k >= nkb) continue;
+            unsigned pk[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float v0 = orow[32 * k + 8 * g + 2 * e], v1 = orow[32 * k + 8 * g + 2 * e + 1];
+                limb_source(v0);
+                limb_source(v1);
+                const unsigned short h0 = f16_bits(v0), h1 = f16_bits(v1);
+                const unsigned short b0 = limb ? f16_bits(v0 - f16_val(h0)) : h0;
+                const unsigned short b1 = limb ? f16_bits(v1 - f16_val(h1)) : h1;
+                pk[e] = (unsigned)b0 | ((unsigned)b1 << 16);
+            }
+            xa[k] = __builtin_bit_cast(h8_t, u4_t{pk[0], pk[1], pk[2], pk[3]});
+        }
+    }
+    const int shift = (g >> 1) * 4;
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ps = 0; ps < MAXP; ps++) {
+        if (ps >= npass) break;
+        const int col = (int)blockIdx.z * ncols + 128 * ps + 16 * w + c16;
+        f32x4 acc = zero;
+#pragma unroll
+        for (int k = 0; k < KBH; k++) {
+            if (k >= nkb) continue;
+            const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[k], quants_f16<WF>(wq[ps][k], shift), zero, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(dsc[ps][k], t[i], acc[i]);
+        }
+        // lanes g < 2 hold the hi rows of tokens 4 g + i; lane + 32 the lo rows
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] += __shfl_down(acc[i], 32);
+        if (g >= 2 || col >= N || col >= (int)(blockIdx.z + 1) * ncols) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * g + i;
+            if (t < n) opart[((size_t)h * T + r0 + t) * N + col] = acc[i];
+        }
+    }
+}
+
+hipError_t launch_attention_few_wo(const float *part, int S, int T, const float *bias, const DevMatrix &Wo, int d,
+                                   int H, const SeqMeta &sm, const float *rope_c, const float *rope_s, float *opart,
+                                   size_t opart_floats, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    const int hd = H > 0 ? d / H : 0;
+    if (T > GEMV_MAX_M || !part || S < 1 || !bias || hd <= 0 || hd * H != d || hd % 32 || hd > FEW_MAX_HD ||
+        (Wo.fmt != WF_Q8 && Wo.fmt != WF_Q4) || Wo.K != d || Wo.N % 16 || !opart ||
+        (size_t)H * T * Wo.N > opart_floats)
+        return hipErrorInvalidValue;
+    const float inv_scale = 1.0f / sqrtf((float)hd);
+    // 128 columns per workgroup (8 waves x 16 columns; measured at 650M, B=1,
+    // L=8: 1.207 ms per forward, 1.221 with 256, 1.252 with 512, 1.248 with
+    // attention and Wo apart)
+    const int ncols = 128, nz = (Wo.N + ncols - 1) / ncols;
+    const dim3 grid(sm.B, H, nz), blk(ATTF_THREADS);
+    const unsigned char *wq = static_cast<const unsigned char *>(Wo.q);
+    if (Wo.fmt == WF_Q8)
+        hipLaunchKernelGGL(k_attn_few_wo<WF_Q8>, grid, blk, 0, st, part, S, T, bias, d, hd, sm.cu, sm.lens, rope_c,
+                           rope_s, inv_scale, wq, Wo.sc, Wo.N, ncols, opart);
+    else
+        hipLaunchKernelGGL(k_attn_few_wo<WF_Q4>, grid, blk, 0, st, part, S, T, bias, d, hd, sm.cu, sm.lens, rope_c,
+                           rope_s, inv_scale, wq, Wo.sc, Wo.N, ncols, opart);
+    return hipGetLastError();
 }
 
 hipError_t launch_attention_few(const float *part, int S, int T, const float *bias, int d, int H, const SeqMeta &sm,

@@ -264,6 +264,12 @@ hipError_t launch_residual_layernorm(float *x, const float *part, int S, const f
 constexpr int FEW_MAX_HD = 128;
 hipError_t launch_attention_few(const float *part, int S, int T, const float *bias, int d, int H, const SeqMeta &sm,
                                 const float *rope_c, const float *rope_s, void *out, int out_fmt, hipStream_t st);
+// The same attention followed by each head's share of the output projection
+// Wo (Q8_0 / Q4_0, K = d, hd a multiple of 32): partial sums per head into
+// opart [H][T][Wo.N] (the caller adds the H splits and Wo's bias).
+hipError_t launch_attention_few_wo(const float *part, int S, int T, const float *bias, const DevMatrix &Wo, int d,
+                                   int H, const SeqMeta &sm, const float *rope_c, const float *rope_s, float *opart,
+                                   size_t opart_floats, hipStream_t st);
 
 // Full-range mode: quantized GEMMs take three bf16 limbs and attention the
 // FP32-MFMA kernel, which cover the whole FP32 exponent range (the f16 limbs

@@ -254,6 +254,31 @@ def test_forward_few_tokens(dtype, gemv, monkeypatch):
         check_batch(cfg, w, seqs, ALL, contact=(cw, np.float32(0.25)))
 
 
+@pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("hd", [32, 64])
+def test_few_tokens_attention_with_wo(dtype, hd, monkeypatch):
+    """Few tokens without maps and head sizes of whole 32-wide blocks: the
+    8-token attention also applies each head's share of Wo (k_attn_few_wo,
+    the heads as the projection's splits).  Logits and hidden state against
+    the oracle, and against attention and Wo run apart (CIH_FEW_WO=0) to
+    1e-5."""
+    rng = np.random.default_rng(hd + dtype)
+    cfg = ch.EsmConfig(4 * hd, 16 * hd, 2, 4)
+    w = quantized(ch.EsmWeights.random(cfg, seed=hd + 10 * dtype, bias_std=0.02), dtype)
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN
+    for lens in ([2], [1, 2], [0, 1, 1], [6]):  # at most 8 tokens per batch
+        seqs = [rand_tokens(rng, n) for n in lens]
+        print(f"attention + Wo hd={hd} dtype={dtype} residues={lens}", flush=True)
+        monkeypatch.delenv("CIH_FEW_WO", raising=False)
+        fused = check_batch(cfg, w, seqs, flags)
+        monkeypatch.setenv("CIH_FEW_WO", "0")
+        apart = check_batch(cfg, w, seqs, flags)
+        for k in ("logits", "hidden"):
+            for b, t in enumerate(seqs):
+                e = float(np.abs(fused[k][b, :len(t)] - apart[k][b, :len(t)]).max())
+                assert e <= 1e-5, (k, b, e)
+
+
 @pytest.mark.parametrize("T", [8, 40])
 def test_forward_graph_replays_match_eager(T, monkeypatch):
     """Forwards of a shape seen before replay a captured graph (keyed by
