@@ -87,6 +87,14 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
     float *const part_a = dc->part.part, *const part_b = dc->part.part + part_half;
     int pend_splits = 0;  // FC2 splits waiting in part_a
     const float *pend_bias = nullptr;
+    // attention and Wo in one kernel (head sizes 32 / 64, quantized Wo) for
+    // one or two rows: each (row, head, 256 columns) workgroup reads its Wo
+    // columns itself, which the GEMV reads once for all rows (650M Q4_0:
+    // one stream 854 -> 888 tokens/s, 8 streams 6012 -> 4557); CIH_FEW_WO=0: apart
+    const char *few_wo_env = getenv("CIH_FEW_WO");
+    const bool fuse_wo = n <= 2 && (m->hd == 32 || m->hd == 64) && L > 0 &&
+                         (m->layers[0].wo.fmt == WF_Q8 || m->layers[0].wo.fmt == WF_Q4) &&
+                         (size_t)H * n * d <= part_half && !(few_wo_env && !strcmp(few_wo_env, "0"));
     for (int l = 0; l < L && g16; l++) {
         const Layer &ly = m->layers[l];
         const unsigned short *xbh = reinterpret_cast<const unsigned short *>(dc->xb);
@@ -103,7 +111,13 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
         float *kc = dc->kc + l * layer, *vc = dc->vc + l * layer;
         {
             ProfScope ps(m, CIH_KC_ATTENTION, 4.0 * keys * d, 8.0 * keys * d + 24.0 * n * d);
-            if (fused) {
+            if (fused && fuse_wo) {
+                // attention and each head's share of Wo in one kernel: the heads are Wo's splits
+                HIPCHK(launch_decode_attention_fused_wo(dc->qkv, part_b, sq, ly.bqkv, d, H, dc->d_rows, n,
+                                                        dc->max_len, dc->rope_c, dc->rope_s, kc, vc, dc->slot_stride,
+                                                        ly.wo, part_a, part_half, st));
+                so = H;
+            } else if (fused) {
                 HIPCHK(launch_decode_attention_fused(dc->qkv, part_b, sq, ly.bqkv, d, H, dc->d_rows, n, dc->max_len,
                                                      dc->rope_c, dc->rope_s, kc, vc, dc->slot_stride, dc->ao, st,
                                                      AF_H2));
@@ -115,7 +129,7 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
                                                dc->ao, st, AF_H2));
             }
         }
-        {
+        if (!(fused && fuse_wo)) {
             ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * n * d * d, wbytes(ly.wo) + 8.0 * n * d);
             HIPCHK(launch_gemv16_partials(ly.wo, reinterpret_cast<const unsigned short *>(dc->ao), n, part_a,
                                           part_half, &so, st));

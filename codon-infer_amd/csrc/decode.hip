@@ -5,6 +5,7 @@
 // (codon-infer src/lib.rs:3616-3663, 3438-3483).
 #include <math.h>
 
+#include "head_wo.h"
 #include "kernels.h"
 #include "x3.h"
 
@@ -70,7 +71,15 @@ __device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_m
 // RoPE to its head's Q and K, writes K and V at pos into the cache for later
 // steps, and takes key pos from LDS rather than from the cache, so no
 // workgroup reads what another one writes.  Otherwise k_rope_kv has run.
-template <int HD, bool FUSED, int OF>
+//
+// WOF (WF_Q8 / WF_Q4; 0: none): instead of storing the head's output, the
+// workgroup multiplies it by the head's k-blocks of Wo (HeadWo) for columns
+// [z 128 WO_P, (z + 1) 128 WO_P), z = blockIdx.z, into wo_part + (h n + r) N:
+// the heads are the projection's splits.  Its weights are requested before
+// the attention, which each column chunk repeats (only chunk 0 writes the
+// cache).
+constexpr int WO_P = 2;
+template <int HD, bool FUSED, int OF, int WOF = 0>
 __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *__restrict__ qkv,
                                                                   const float *__restrict__ part, int splits,
                                                                   const float *__restrict__ bias, int d,
@@ -78,7 +87,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
                                                                   const float *__restrict__ rc,
                                                                   const float *__restrict__ rs, float *__restrict__ kc,
                                                                   float *__restrict__ vc, int64_t slot_stride,
-                                                                  float inv_scale, float *__restrict__ out) {
+                                                                  float inv_scale, float *__restrict__ out,
+                                                                  const unsigned char *__restrict__ wo_q = nullptr,
+                                                                  const float *__restrict__ wo_sc = nullptr,
+                                                                  int wo_n = 0) {
     constexpr int G = ATT_THREADS / HD;
     constexpr int HALF = HD / 2;
     extern __shared__ float sm[];
@@ -93,6 +105,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
     float *V = vc + slot * slot_stride + h * HD;
     const int t = threadIdx.x;
     const int n_cached = FUSED ? pos : pos + 1;  // keys read from the cache
+    constexpr int NKB = HD / 32;
+    HeadWo<WOF ? WOF : WF_Q8, WO_P> wo;
+    const int wc0 = (int)blockIdx.z * 128 * WO_P, wc1 = min(wc0 + 128 * WO_P, wo_n);
+    if constexpr (WOF != 0) wo.load(wo_q, wo_sc, wo_n, h * NKB, NKB, wc0, wc1);
+    const bool cache_writer = WOF == 0 || blockIdx.z == 0;
     // This thread's first key row is requested before anything waits, so its
     // latency overlaps the gather, the rotation and the barriers.
     float4 kfirst[HD / 4];
@@ -146,9 +163,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
             const float r1 = __fadd_rn(__fmul_rn(k1, c), __fmul_rn(k0, s));
             kcur[t] = r0;
             kcur[t + HALF] = r1;
-            K[(size_t)pos * d + t] = r0;
-            K[(size_t)pos * d + t + HALF] = r1;
-        } else if (t >= 64 && t < 64 + HD) {
+            if (cache_writer) {
+                K[(size_t)pos * d + t] = r0;
+                K[(size_t)pos * d + t + HALF] = r1;
+            }
+        } else if (t >= 64 && t < 64 + HD && cache_writer) {
             V[(size_t)pos * d + t - 64] = vcur[t - 64];
         }
     } else {
@@ -220,8 +239,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_decode_attention(const float *_
         float o = gsum[t];
 #pragma unroll
         for (int k = 1; k < G; k++) o += gsum[k * HD + t];
-        if constexpr (OF == AF_H2) h2_store(reinterpret_cast<unsigned short *>(out), r, h * HD + t, d, o);
+        if constexpr (WOF != 0) qs[t] = o;  // the query is no longer read
+        else if constexpr (OF == AF_H2) h2_store(reinterpret_cast<unsigned short *>(out), r, h * HD + t, d, o);
         else out[(size_t)r * d + h * HD + t] = o;
+    }
+    if constexpr (WOF != 0) {
+        static_assert(HD % 32 == 0, "heads of whole 32-wide blocks");
+        __syncthreads();
+        wo.run(qs, HD, 1, NKB, wo_n, wc0, wc1, out + ((size_t)h * gridDim.x + r) * wo_n);
     }
 }
 
@@ -274,6 +299,32 @@ hipError_t launch_decode_attention(const float *qkv, int d, int H, const int *ro
     if (n <= 0) return hipSuccess;
     return launch_att<false>(qkv, nullptr, 0, nullptr, d, H, rows, n, max_len, nullptr, nullptr,
                              const_cast<float *>(kc), const_cast<float *>(vc), slot_stride, out, out_fmt, st);
+}
+
+hipError_t launch_decode_attention_fused_wo(float *qkv, const float *part, int splits, const float *bias, int d, int H,
+                                            const int *rows, int n, int max_len, const float *rope_c,
+                                            const float *rope_s, float *kc, float *vc, int64_t slot_stride,
+                                            const DevMatrix &Wo, float *wo_part, size_t wo_part_floats,
+                                            hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int hd = H > 0 ? d / H : 0;
+    if ((part && (!bias || splits < 1)) || hd * H != d || (hd != 32 && hd != 64) ||
+        (Wo.fmt != WF_Q8 && Wo.fmt != WF_Q4) || Wo.K != d || Wo.N % 16 || !wo_part ||
+        (size_t)H * n * Wo.N > wo_part_floats)
+        return hipErrorInvalidValue;
+    const float inv_scale = 1.0f / sqrtf((float)hd);
+    const size_t lds = decode_attention_lds(hd, max_len);
+    const dim3 grid(n, H, (Wo.N + 128 * WO_P - 1) / (128 * WO_P)), block(ATT_THREADS);
+    const unsigned char *wq = static_cast<const unsigned char *>(Wo.q);
+#define CIH_ATT_WO(HDV, WFV)                                                                                       \
+    hipLaunchKernelGGL((k_decode_attention<HDV, true, AF_F32, WFV>), grid, block, lds, st, qkv, part, splits, bias, \
+                       d, rows, rope_c, rope_s, kc, vc, slot_stride, inv_scale, wo_part, wq, Wo.sc, Wo.N)
+    if (hd == 64 && Wo.fmt == WF_Q8) CIH_ATT_WO(64, WF_Q8);
+    else if (hd == 64) CIH_ATT_WO(64, WF_Q4);
+    else if (Wo.fmt == WF_Q8) CIH_ATT_WO(32, WF_Q8);
+    else CIH_ATT_WO(32, WF_Q4);
+#undef CIH_ATT_WO
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_attention_fused(float *qkv, const float *part, int splits, const float *bias, int d, int H,

@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "head_wo.h"
 #include "kernels.h"
 #include "x3.h"
 
@@ -344,11 +345,7 @@ __global__ __launch_bounds__(ATTF_THREADS) void k_attn_few_wo(const float *__res
                                                               const unsigned char *__restrict__ Wq,
                                                               const float *__restrict__ Wsc, int N, int ncols,
                                                               float *__restrict__ opart) {
-    typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-    typedef unsigned u2_t __attribute__((ext_vector_type(2)));
-    typedef unsigned u4_t __attribute__((ext_vector_type(4)));
     constexpr int RW = FEW_MAX_HD + 4;
-    constexpr int KBH = FEW_MAX_HD / 32;  // k-blocks of a head, at most
     __shared__ float qkv[3][GEMV_MAX_M][RW];
     __shared__ float p[GEMV_MAX_M][GEMV_MAX_M];
     const int b = blockIdx.x, h = blockIdx.y;
@@ -412,24 +409,9 @@ __global__ __launch_bounds__(ATTF_THREADS) void k_attn_few_wo(const float *__res
     if (n <= 0) return;  // uniform: no barrier follows for this workgroup
     // this workgroup's Wo columns and the head's k-blocks: weights and scales
     // requested now, used after the attention
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
-    const int nkb = hd / 32, kb0 = h * nkb;
-    const int npass = (ncols + 127) / 128;
-    constexpr int MAXP = 4;  // column passes of 8 waves x 16 columns (ncols <= 512)
-    u2_t wq[MAXP][KBH];
-    float dsc[MAXP][KBH];
-#pragma unroll
-    for (int ps = 0; ps < MAXP; ps++) {
-        const int col = min((int)blockIdx.z * ncols + 128 * ps + 16 * w + c16, N - 1);
-#pragma unroll
-        for (int k = 0; k < KBH; k++) {
-            if (ps >= npass || k >= nkb) continue;
-            const size_t blk = (size_t)(kb0 + k) * N + col;
-            if constexpr (WF == WF_Q8) wq[ps][k] = *reinterpret_cast<const u2_t *>(Wq + blk * 32 + 8 * g);
-            else wq[ps][k] = *reinterpret_cast<const u2_t *>(Wq + blk * 16 + 8 * (g & 1));
-            dsc[ps][k] = Wsc[blk];
-        }
-    }
+    const int nkb = hd / 32, c0 = (int)blockIdx.z * ncols, c1 = min(c0 + ncols, N);
+    HeadWo<WF, 1> wo;
+    wo.load(Wq, Wsc, N, h * nkb, nkb, c0, c1);
     __syncthreads();
     // scores and softmax (as k_attn_few)
     if (threadIdx.x < 64) {
@@ -467,52 +449,7 @@ __global__ __launch_bounds__(ATTF_THREADS) void k_attn_few_wo(const float *__res
         qkv[0][r0 + i][jj] = a;
     }
     __syncthreads();
-    // the GEMV operand: row c16 = token (c16 & 7) limb (c16 >> 3), dims 32 k + 8 g ..
-    h8_t xa[KBH];
-    {
-        const int tok = min(c16 & 7, n - 1), limb = c16 >> 3;
-        const float *orow = qkv[0][r0 + tok];
-#pragma unroll
-        for (int k = 0; k < KBH; k++) {
-            if (k >= nkb) continue;
-            unsigned pk[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float v0 = orow[32 * k + 8 * g + 2 * e], v1 = orow[32 * k + 8 * g + 2 * e + 1];
-                limb_source(v0);
-                limb_source(v1);
-                const unsigned short h0 = f16_bits(v0), h1 = f16_bits(v1);
-                const unsigned short b0 = limb ? f16_bits(v0 - f16_val(h0)) : h0;
-                const unsigned short b1 = limb ? f16_bits(v1 - f16_val(h1)) : h1;
-                pk[e] = (unsigned)b0 | ((unsigned)b1 << 16);
-            }
-            xa[k] = __builtin_bit_cast(h8_t, u4_t{pk[0], pk[1], pk[2], pk[3]});
-        }
-    }
-    const int shift = (g >> 1) * 4;
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int ps = 0; ps < MAXP; ps++) {
-        if (ps >= npass) break;
-        const int col = (int)blockIdx.z * ncols + 128 * ps + 16 * w + c16;
-        f32x4 acc = zero;
-#pragma unroll
-        for (int k = 0; k < KBH; k++) {
-            if (k >= nkb) continue;
-            const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[k], quants_f16<WF>(wq[ps][k], shift), zero, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(dsc[ps][k], t[i], acc[i]);
-        }
-        // lanes g < 2 hold the hi rows of tokens 4 g + i; lane + 32 the lo rows
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] += __shfl_down(acc[i], 32);
-        if (g >= 2 || col >= N || col >= (int)(blockIdx.z + 1) * ncols) continue;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 4 * g + i;
-            if (t < n) opart[((size_t)h * T + r0 + t) * N + col] = acc[i];
-        }
-    }
+    wo.run(qkv[0][r0], RW, n, nkb, N, c0, c1, opart + ((size_t)h * T + r0) * N);
 }
 
 hipError_t launch_attention_few_wo(const float *part, int S, int T, const float *bias, const DevMatrix &Wo, int d,
@@ -525,9 +462,9 @@ hipError_t launch_attention_few_wo(const float *part, int S, int T, const float 
         (size_t)H * T * Wo.N > opart_floats)
         return hipErrorInvalidValue;
     const float inv_scale = 1.0f / sqrtf((float)hd);
-    // 128 columns per workgroup (8 waves x 16 columns; measured at 650M, B=1,
-    // L=8: 1.207 ms per forward, 1.221 with 256, 1.252 with 512, 1.248 with
-    // attention and Wo apart)
+    // 128 columns per workgroup (8 waves x 16 columns, one pass; measured at
+    // 650M, B=1, L=8: 1.207 ms per forward, 1.221 with 256, 1.252 with 512,
+    // 1.248 with attention and Wo apart)
     const int ncols = 128, nz = (Wo.N + ncols - 1) / ncols;
     const dim3 grid(sm.B, H, nz), blk(ATTF_THREADS);
     const unsigned char *wq = static_cast<const unsigned char *>(Wo.q);

@@ -371,6 +371,14 @@ hipError_t launch_decode_attention_fused(float *qkv, const float *part, int spli
                                          const int *rows, int n, int max_len, const float *rope_c,
                                          const float *rope_s, float *kc, float *vc, int64_t slot_stride, float *out,
                                          hipStream_t st, int out_fmt = AF_F32);
+// The same, each head's output multiplied by its k-blocks of Wo (Q8_0 /
+// Q4_0, K = d, hd 32 or 64) instead of stored: partial sums per head into
+// wo_part [H][n][Wo.N] (the caller adds the H splits and Wo's bias).
+hipError_t launch_decode_attention_fused_wo(float *qkv, const float *part, int splits, const float *bias, int d, int H,
+                                            const int *rows, int n, int max_len, const float *rope_c,
+                                            const float *rope_s, float *kc, float *vc, int64_t slot_stride,
+                                            const DevMatrix &Wo, float *wo_part, size_t wo_part_floats,
+                                            hipStream_t st);
 size_t decode_attention_lds(int hd, int max_len);  // dynamic LDS bytes per workgroup
 
 // Copies packed rows [T][width] into padded [B][S_max][width] (valid rows only).
