@@ -465,7 +465,7 @@ def main():
         # weight streaming: algorithmic bytes = quantized weights + activations in/out
         achieved = q["bytes"] / (q["total_ms"] * 1e-3) / 1e9 if q["total_ms"] > 0 else 0.0
         if not fp32_model and os.environ.get("CIH_GEMV16") != "0" and not fp32_path:
-            wo_in_att = cfg.dim // cfg.n_heads % 32 == 0 and os.environ.get("CIH_FEW_WO") != "0" and not args.outputs.startswith("maps")
+            wo_in_att = cfg.dim // cfg.n_heads % 32 == 0 and os.environ.get("CIH_FEW_WO") != "0" and args.outputs == "logits"
             kname = f"k_gemv16<{wname}> split-K GEMV on f16 MFMA " + (
                 "(QKV, FC1, FC2; Wo inside the attention kernel)" if wo_in_att else "(QKV, Wo, FC1, FC2)")
         else:
