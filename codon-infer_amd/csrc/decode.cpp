@@ -95,16 +95,26 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
     const bool fuse_wo = n <= 2 && (m->hd == 32 || m->hd == 64) && L > 0 &&
                          (m->layers[0].wo.fmt == WF_Q8 || m->layers[0].wo.fmt == WF_Q4) &&
                          (size_t)H * n * d <= part_half && !(few_wo_env && !strcmp(few_wo_env, "0"));
+    // one row: the residual LayerNorms are formed inside the QKV and FC1
+    // GEMVs (every workgroup normalises the row itself; the new residual goes
+    // to xb, then back to x), two launches fewer per layer; CIH_DECODE_LN=0: apart
+    const char *ln_env = getenv("CIH_DECODE_LN");
+    const bool ln_fused = g16 && n == 1 && d <= GEMV16_LN_MAX_K && !(ln_env && !strcmp(ln_env, "0"));
     for (int l = 0; l < L && g16; l++) {
         const Layer &ly = m->layers[l];
         const unsigned short *xbh = reinterpret_cast<const unsigned short *>(dc->xb);
-        {
+        if (!ln_fused) {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
             HIPCHK(launch_residual_layernorm(dc->x, pend_splits ? part_a : nullptr, pend_splits, pend_bias, ly.ln1w,
                                              ly.ln1b, dc->xb, AF_H2, n, d, st));
         }
         int sq = 0, so = 0, s1 = 0;
-        {
+        if (ln_fused) {
+            ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * ly.wqkv.N * d,
+                         wbytes(ly.wqkv) + 4.0 * (pend_splits + 2) * d + 4.0 * ly.wqkv.N);
+            HIPCHK(launch_gemv16_ln_partials(ly.wqkv, dc->x, dc->xb, pend_splits ? part_a : nullptr, pend_splits,
+                                             pend_bias, ly.ln1w, ly.ln1b, part_b, part_half, &sq, st));
+        } else {
             ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * n * ly.wqkv.N * d, wbytes(ly.wqkv) + 4.0 * n * d + 4.0 * n * ly.wqkv.N);
             HIPCHK(launch_gemv16_partials(ly.wqkv, xbh, n, part_b, part_half, &sq, st));
         }
@@ -134,11 +144,15 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
             HIPCHK(launch_gemv16_partials(ly.wo, reinterpret_cast<const unsigned short *>(dc->ao), n, part_a,
                                           part_half, &so, st));
         }
-        {
-            ProfScope ps(m, CIH_KC_OTHER, 0, 4.0 * so * n * d + 12.0 * n * d);
-            HIPCHK(launch_residual_layernorm(dc->x, part_a, so, ly.bo, ly.ln2w, ly.ln2b, dc->xb, AF_H2, n, d, st));
-        }
-        {
+        if (ln_fused) {
+            ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * F * d, wbytes(ly.w1) + 4.0 * (so + 2) * d + 4.0 * F);
+            HIPCHK(launch_gemv16_ln_partials(ly.w1, dc->xb, dc->x, part_a, so, ly.bo, ly.ln2w, ly.ln2b, part_b,
+                                             part_half, &s1, st));
+        } else {
+            {
+                ProfScope ps(m, CIH_KC_OTHER, 0, 4.0 * so * n * d + 12.0 * n * d);
+                HIPCHK(launch_residual_layernorm(dc->x, part_a, so, ly.bo, ly.ln2w, ly.ln2b, dc->xb, AF_H2, n, d, st));
+            }
             ProfScope ps(m, CIH_KC_GEMM_QUANT, 2.0 * n * F * d, wbytes(ly.w1) + 4.0 * n * (d + F));
             HIPCHK(launch_gemv16_partials(ly.w1, xbh, n, part_b, part_half, &s1, st));
         }

@@ -70,19 +70,8 @@ __global__ __launch_bounds__(RLN_MAX_THREADS) void k_rln(float *__restrict__ x, 
     __syncthreads();
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        float s = 0.0f;
-        for (int c = lane; c < n4; c += 64) s += (xs[c].x + xs[c].y) + (xs[c].z + xs[c].w);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-        const float mean = s / (float)d;
-        float q = 0.0f;
-        for (int c = lane; c < n4; c += 64) {
-            const f32x4 t = xs[c] - mean;
-            q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
-        const float var = q / (float)d;
+        float mean, var;
+        row_stats64(xs, n4, d, lane, mean, var);
         if (lane == 0) {
             stat[0] = mean;
             stat[1] = 1.0f / sqrtf(var + 1e-5f);

@@ -51,15 +51,92 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // AG: the activations are GELU(sum of the aS splits of apart + abias) instead
 // (apart: [aS][M][K] partial sums of the projection before, FC1's), formed
 // and split into limbs while staging: that projection needs no fold kernel.
-template <int WF, int KW, int EPI, bool AG>
+//
+// LN (one row, K <= GEMV16_LN_MAX_K): the activations are LayerNorm(x + abias
+// + sum of the aS splits of apart) with weights ln.w, ln.b: every workgroup
+// forms the whole row (k_rln's sums in k_rln's order, row_stats64), so the
+// residual LayerNorm needs no launch of its own; workgroup (0, 0) stores the
+// new residual x + ... to ln.xo (a buffer other than ln.x, which the other
+// workgroups are still reading).  apart == nullptr: LayerNorm(x).
+template <int WF, int KW, int EPI, bool AG, bool LN = false>
 __global__ __launch_bounds__(256) void k_gemv16(const unsigned short *__restrict__ X, int M, int KB,
                                                 const void *__restrict__ Wq, const float *__restrict__ Wsc, int N,
                                                 const float *__restrict__ bias, void *__restrict__ Yv, int ldy,
                                                 float *__restrict__ part, int rounds, const float *__restrict__ apart,
-                                                int aS, const float *__restrict__ abias) {
+                                                int aS, const float *__restrict__ abias, const LnIn ln) {
+    static_assert(!(AG && LN), "one activation form");
     __shared__ u32x4 xs[KW][64];  // per k-block of the round: the A operand of each lane
+    __shared__ f32x4 lnv[LN ? GEMV16_LN_MAX_K / 4 : 1];  // LN: the row, then its LayerNorm
+    __shared__ float lnst[2];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if constexpr (LN) {
+        const int d = KB * 32, n4 = d >> 2;
+        constexpr int UPT = (GEMV16_LN_MAX_K / 4 + 255) / 256;  // quads per thread
+        const int nu = (n4 - tid + 255) / 256;                 // this thread's quads: tid + 256 i, i < nu
+        f32x4 v[UPT], g4[UPT], b4[UPT];
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int c = min(tid + 256 * i, n4 - 1);
+            v[i] = reinterpret_cast<const f32x4 *>(ln.x)[c];
+            g4[i] = reinterpret_cast<const f32x4 *>(ln.w)[c];
+            b4[i] = reinterpret_cast<const f32x4 *>(ln.b)[c];
+        }
+        if (apart) {
+            // fold_splits4 for all of the thread's quads at once: the same
+            // additions in the same order, every load of a chunk in flight
+            fold4_t acc[UPT];
+#pragma unroll
+            for (int i = 0; i < UPT; i++) acc[i] = fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int s0 = 0; s0 < aS; s0 += FOLD_CHUNK) {
+                fold4_t t[UPT][FOLD_CHUNK];
+#pragma unroll
+                for (int i = 0; i < UPT; i++)
+#pragma unroll
+                    for (int u = 0; u < FOLD_CHUNK; u++)
+                        t[i][u] = s0 + u < aS && i < nu
+                                      ? *reinterpret_cast<const fold4_t *>(apart + (size_t)(s0 + u) * KB * 32 +
+                                                                           4 * (tid + 256 * i))
+                                      : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int i = 0; i < UPT; i++)
+#pragma unroll
+                    for (int u = 0; u < FOLD_CHUNK; u++) acc[i] += t[i][u];
+            }
+#pragma unroll
+            for (int i = 0; i < UPT; i++) {
+                const f32x4 bb = reinterpret_cast<const f32x4 *>(abias)[min(tid + 256 * i, n4 - 1)];
+                v[i] = v[i] + (acc[i] + bb);
+            }
+        }
+        const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+        for (int i = 0; i < UPT; i++)
+            if (i < nu) {
+                lnv[tid + 256 * i] = v[i];
+                if (writer) reinterpret_cast<f32x4 *>(ln.xo)[tid + 256 * i] = v[i];
+            }
+        __syncthreads();
+        if (w == 0) {
+            float mean, var;
+            row_stats64(lnv, n4, d, lane, mean, var);
+            if (lane == 0) {
+                lnst[0] = mean;
+                lnst[1] = 1.0f / sqrtf(var + 1e-5f);
+            }
+        }
+        __syncthreads();
+        const float mean = lnst[0], inv = lnst[1];
+#pragma unroll
+        for (int i = 0; i < UPT; i++)
+            if (i < nu) {
+                f32x4 y;
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = g4[i][e] * (v[i][e] - mean) * inv + b4[i][e];
+                lnv[tid + 256 * i] = y;
+            }
+        __syncthreads();
+    }
     const int g = lane >> 4, c = lane & 15;
     const bool live = blockIdx.x * 64 + 16 * w < N;  // wave-uniform (N % 16 == 0)
     const int n = live ? blockIdx.x * 64 + 16 * w + c : N - 1;
@@ -88,6 +165,29 @@ __global__ __launch_bounds__(256) void k_gemv16(const unsigned short *__restrict
                 ga[q][1] = fold_splits4(pp + 4, aS, (size_t)M * K);
                 gb[q][0] = *reinterpret_cast<const fold4_t *>(abias + k0);
                 gb[q][1] = *reinterpret_cast<const fold4_t *>(abias + k0 + 4);
+            }
+        } else if constexpr (LN) {
+            // the row's LayerNorm as limbs (h2_store4's split): lane l of k-block
+            // j holds k = 32 kb + 8 (l >> 4) .. + 7, hi limbs for l % 16 < 8
+#pragma unroll
+            for (int q = 0; q < XE; q++) {
+                const int e = min(tid + 256 * q, KW * 64 - 1), j = e >> 6, l = e & 63;
+                const int kb = min(kb0 + j, KB - 1), c4 = kb * 8 + 2 * (l >> 4);
+                const bool lo = (l & 15) >= 8;
+                unsigned h[4];
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    float y0 = lnv[c4 + (p >> 1)][2 * (p & 1)], y1 = lnv[c4 + (p >> 1)][2 * (p & 1) + 1];
+                    limb_source(y0);
+                    limb_source(y1);
+                    unsigned short a0 = f16_bits(y0), a1 = f16_bits(y1);
+                    if (lo) {
+                        a0 = f16_bits(y0 - f16_val(a0));
+                        a1 = f16_bits(y1 - f16_val(a1));
+                    }
+                    h[p] = (unsigned)a0 | ((unsigned)a1 << 16);
+                }
+                xe[q] = u32x4{h[0], h[1], h[2], h[3]};
             }
         } else {
 #pragma unroll
@@ -240,16 +340,22 @@ struct GeluIn {
 
 template <int WF, int KW>
 static void launch_kw(const DevMatrix &W, const unsigned short *X, int M, const float *bias, void *Y, int ldy, int epi,
-                      float *part, int S, const GeluIn &gi, hipStream_t st) {
+                      float *part, int S, const GeluIn &gi, const LnIn *ln, hipStream_t st) {
     const int KB = W.K / 32;
     const int rounds = (KB + S * KW - 1) / (S * KW);
     const dim3 grid((W.N + 63) / 64, S), block(256);
+    const LnIn noln{nullptr, nullptr, nullptr, nullptr};
 #define CIH_G16(E)                                                                                                  \
     hipLaunchKernelGGL((k_gemv16<WF, KW, E, false>), grid, block, 0, st, X, M, KB, W.q, W.sc, W.N, bias, Y, ldy,  \
-                       part, rounds, nullptr, 0, nullptr)
+                       part, rounds, nullptr, 0, nullptr, noln)
+    if (ln) {  // gi: the residual's splits
+        hipLaunchKernelGGL((k_gemv16<WF, KW, EPI_NONE, false, true>), grid, block, 0, st, nullptr, 1, KB, W.q, W.sc,
+                           W.N, nullptr, nullptr, 0, part, rounds, gi.part, gi.S, gi.bias, *ln);
+        return;
+    }
     if (gi.part) {
         hipLaunchKernelGGL((k_gemv16<WF, KW, EPI_NONE, true>), grid, block, 0, st, nullptr, M, KB, W.q, W.sc, W.N,
-                           nullptr, nullptr, 0, part, rounds, gi.part, gi.S, gi.bias);
+                           nullptr, nullptr, 0, part, rounds, gi.part, gi.S, gi.bias, noln);
         return;
     }
     if (part) CIH_G16(EPI_NONE);
@@ -261,13 +367,14 @@ static void launch_kw(const DevMatrix &W, const unsigned short *X, int M, const 
 }
 
 static void launch_any(const DevMatrix &W, const unsigned short *X, int M, const float *bias, void *Y, int ldy,
-                       int epi, float *part, int S, int kw, hipStream_t st, const GeluIn &gi = GeluIn()) {
+                       int epi, float *part, int S, int kw, hipStream_t st, const GeluIn &gi = GeluIn(),
+                       const LnIn *ln = nullptr) {
 #define CIH_KW(WF)                                                                                                  \
     switch (kw) {                                                                                                  \
-    case 4: launch_kw<WF, 4>(W, X, M, bias, Y, ldy, epi, part, S, gi, st); break;                                  \
-    case 10: launch_kw<WF, 10>(W, X, M, bias, Y, ldy, epi, part, S, gi, st); break;                                \
-    case 20: launch_kw<WF, 20>(W, X, M, bias, Y, ldy, epi, part, S, gi, st); break;                                \
-    default: launch_kw<WF, 8>(W, X, M, bias, Y, ldy, epi, part, S, gi, st);                                        \
+    case 4: launch_kw<WF, 4>(W, X, M, bias, Y, ldy, epi, part, S, gi, ln, st); break;                              \
+    case 10: launch_kw<WF, 10>(W, X, M, bias, Y, ldy, epi, part, S, gi, ln, st); break;                            \
+    case 20: launch_kw<WF, 20>(W, X, M, bias, Y, ldy, epi, part, S, gi, ln, st); break;                            \
+    default: launch_kw<WF, 8>(W, X, M, bias, Y, ldy, epi, part, S, gi, ln, st);                                    \
     }
     if (W.fmt == WF_Q8) {
         CIH_KW(WF_Q8)
@@ -299,6 +406,24 @@ hipError_t launch_gemv16_gelu_partials(const DevMatrix &W, const float *apart, i
     gi.S = aS;
     gi.bias = abias;
     launch_any(W, nullptr, M, nullptr, nullptr, 0, EPI_NONE, part, g.splits, g.kw, st, gi);
+    *splits = g.splits;
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv16_ln_partials(const DevMatrix &W, const float *x, float *xo, const float *rpart, int rS,
+                                     const float *rbias, const float *lnw, const float *lnb, float *part,
+                                     size_t part_floats, int *splits, hipStream_t st) {
+    if (!gemv16_applies(W, AF_H2, 1, EPI_NONE) || W.K > GEMV16_LN_MAX_K || !x || !xo || x == xo || !lnw || !lnb ||
+        !part || (rpart && (rS < 1 || !rbias)))
+        return hipErrorInvalidValue;
+    const Gemv16Grid g = gemv16_grid(W.N, W.K);
+    if ((size_t)g.splits * W.N > part_floats) return hipErrorInvalidValue;
+    GeluIn ri;
+    ri.part = rpart;
+    ri.S = rpart ? rS : 0;
+    ri.bias = rbias;
+    const LnIn ln{x, xo, lnw, lnb};
+    launch_any(W, nullptr, 1, nullptr, nullptr, 0, EPI_NONE, part, g.splits, g.kw, st, ri, &ln);
     *splits = g.splits;
     return hipGetLastError();
 }

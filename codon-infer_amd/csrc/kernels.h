@@ -78,6 +78,25 @@ __device__ __forceinline__ float fold_splits(const float *__restrict__ p, int S,
     return acc;
 }
 typedef float fold4_t __attribute__((ext_vector_type(4)));
+// Mean and variance of one row of n4 quads held in LDS, formed by one wave:
+// lane l sums quads l, l + 64, ... in order, then a butterfly (the
+// reduction order of k_layernorm4, shared by every kernel that normalises a
+// row of the residual stream so that all of them give the same bits).
+__device__ __forceinline__ void row_stats64(const fold4_t *xs, int n4, int d, int lane, float &mean, float &var) {
+    float s = 0.0f;
+    for (int c = lane; c < n4; c += 64) s += (xs[c].x + xs[c].y) + (xs[c].z + xs[c].w);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    mean = s / (float)d;
+    float q = 0.0f;
+    for (int c = lane; c < n4; c += 64) {
+        const fold4_t t = xs[c] - mean;
+        q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+    var = q / (float)d;
+}
 __device__ __forceinline__ fold4_t fold_splits4(const float *__restrict__ p, int S, size_t stride) {
     fold4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < S; s0 += FOLD_CHUNK) {
@@ -185,6 +204,20 @@ Gemv16Grid gemv16_grid(int N, int K);
 // partial sums [*splits][M][N] (no bias) for a consumer that adds them in split order
 hipError_t launch_gemv16_partials(const DevMatrix &W, const unsigned short *X, int M, float *part, size_t part_floats,
                                   int *splits, hipStream_t st);
+// The residual LayerNorm of one row folded into the projection after it:
+// x' = x + rbias + (sum of the rS splits of rpart, [rS][K]) is stored to xo
+// (not x), and the activations are LayerNorm(x') with lnw, lnb, formed in
+// every workgroup with k_rln's arithmetic (the same bits as k_rln followed by
+// launch_gemv16_partials).  rpart == nullptr: x' = x.  K <= GEMV16_LN_MAX_K.
+constexpr int GEMV16_LN_MAX_K = 2048;
+struct LnIn {
+    const float *x;
+    float *xo;
+    const float *w, *b;
+};
+hipError_t launch_gemv16_ln_partials(const DevMatrix &W, const float *x, float *xo, const float *rpart, int rS,
+                                     const float *rbias, const float *lnw, const float *lnb, float *part,
+                                     size_t part_floats, int *splits, hipStream_t st);
 // the same with activations GELU(sum of the aS splits of apart + abias) formed
 // while staging (apart: [aS][M][W.K], the FC1 projection's partial sums)
 hipError_t launch_gemv16_gelu_partials(const DevMatrix &W, const float *apart, int aS, const float *abias, int M,

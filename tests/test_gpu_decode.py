@@ -178,6 +178,32 @@ def test_650m_q8_decode_steps():
     m.close()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("hd,fmt", [(64, "q4"), (32, "q8"), (16, "q8")])
+def test_decode_layernorm_in_gemv(hd, fmt, monkeypatch):
+    """One stream: the residual LayerNorms run inside the QKV and FC1 GEMVs
+    (every workgroup normalises the row; the residual alternates between two
+    buffers).  Same bits as the separate residual LayerNorm kernel
+    (CIH_DECODE_LN=0) at every step, and steps against the oracle."""
+    cfg = ch.EsmConfig(4 * hd, 16 * hd, 3, 4)
+    w = ch.EsmWeights.random(cfg, seed=100 + hd, bias_std=0.02)
+    w = w.quantize_q8() if fmt == "q8" else w.quantize_q4()
+    toks = [0, 20, 15, 7, 32, 9, 11]
+    got = {}
+    for env in ("1", "0"):
+        monkeypatch.setenv("CIH_DECODE_LN", env)
+        m = ch.GpuModel(cfg, w, max_batch=1, max_len=16)
+        dec = ch.GpuDecoder(m, n_slots=1, max_len=32, max_rows=8)
+        got[env] = [dec.decode([0], [t], [p])[0].copy() for p, t in enumerate(toks)]
+        dec.close()
+        m.close()
+    for p in range(len(toks)):
+        assert np.array_equal(got["1"][p], got["0"][p]), (p, float(np.abs(got["1"][p] - got["0"][p]).max()))
+    rs = cr.RunState(cfg, w, max_len=32, num_threads=8)
+    for p, t in enumerate(toks):
+        report(f"hd {hd} {fmt} step {p}", got["1"][p], rs.step(t, p))
+
+
 @pytest.mark.parametrize("hd,fmt", [(64, "q4"), (32, "q8")])
 def test_decode_attention_with_wo(hd, fmt, monkeypatch):
     """Head sizes 32 and 64 with quantized weights: each (row, head)
