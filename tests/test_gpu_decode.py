@@ -179,14 +179,17 @@ def test_650m_q8_decode_steps():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("hd,fmt", [(64, "q4"), (32, "q8"), (16, "q8")])
-def test_decode_layernorm_in_gemv(hd, fmt, monkeypatch):
+@pytest.mark.parametrize("d,heads,fmt", [(256, 4, "q4"), (128, 4, "q8"), (64, 4, "q8"), (480, 20, "q8"),
+                                          (1280, 20, "q4"), (2048, 32, "q8")])
+def test_decode_layernorm_in_gemv(d, heads, fmt, monkeypatch):
     """One stream: the residual LayerNorms run inside the QKV and FC1 GEMVs
     (every workgroup normalises the row; the residual alternates between two
-    buffers).  Same bits as the separate residual LayerNorm kernel
-    (CIH_DECODE_LN=0) at every step, and steps against the oracle."""
-    cfg = ch.EsmConfig(4 * hd, 16 * hd, 3, 4)
-    w = ch.EsmWeights.random(cfg, seed=100 + hd, bias_std=0.02)
+    buffers).  Rows of one to two quads per thread, partial waves (d = 480:
+    120 quads), the largest row taken (2048).  Same bits as the separate
+    residual LayerNorm kernel (CIH_DECODE_LN=0) at every step, and steps
+    against the oracle."""
+    cfg = ch.EsmConfig(d, 4 * d, 2 if d > 256 else 3, heads)
+    w = ch.EsmWeights.random(cfg, seed=100 + d, bias_std=0.02)
     w = w.quantize_q8() if fmt == "q8" else w.quantize_q4()
     toks = [0, 20, 15, 7, 32, 9, 11]
     got = {}
@@ -201,7 +204,7 @@ def test_decode_layernorm_in_gemv(hd, fmt, monkeypatch):
         assert np.array_equal(got["1"][p], got["0"][p]), (p, float(np.abs(got["1"][p] - got["0"][p]).max()))
     rs = cr.RunState(cfg, w, max_len=32, num_threads=8)
     for p, t in enumerate(toks):
-        report(f"hd {hd} {fmt} step {p}", got["1"][p], rs.step(t, p))
+        report(f"d {d} {fmt} step {p}", got["1"][p], rs.step(t, p))
 
 
 @pytest.mark.parametrize("hd,fmt", [(64, "q4"), (32, "q8")])
