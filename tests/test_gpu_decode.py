@@ -207,29 +207,31 @@ def test_decode_layernorm_in_gemv(d, heads, fmt, monkeypatch):
         report(f"d {d} {fmt} step {p}", got["1"][p], rs.step(t, p))
 
 
-@pytest.mark.parametrize("hd,fmt", [(64, "q4"), (32, "q8")])
-def test_decode_attention_with_wo(hd, fmt, monkeypatch):
-    """Head sizes 32 and 64 with quantized weights: each (row, head)
-    workgroup of the decode attention also applies the head's share of Wo
-    (the heads as the projection's splits).  Two streams, steps against the
-    oracle, and against attention and Wo run apart (CIH_FEW_WO=0) to 1e-5."""
+@pytest.mark.parametrize("hd,fmt,streams", [(64, "q4", 2), (32, "q8", 2), (64, "q8", 1), (32, "q4", 1)])
+def test_decode_attention_with_wo(hd, fmt, streams, monkeypatch):
+    """Head sizes 32 and 64 with quantized weights: each (row, head, column
+    chunk) workgroup of the decode attention also applies the head's share of
+    Wo (the heads as the projection's splits; 128 columns per workgroup for
+    one row, 256 for two).  Steps against the oracle, and against attention
+    and Wo run apart (CIH_FEW_WO=0) to 1e-5."""
     cfg = ch.EsmConfig(4 * hd, 16 * hd, 2, 4)
     w = ch.EsmWeights.random(cfg, seed=hd, bias_std=0.02)
     w = w.quantize_q8() if fmt == "q8" else w.quantize_q4()
-    toks = [[0, 20, 15, 7, 32, 9], [0, 5, 11, 24, 6, 13]]
+    toks = [[0, 20, 15, 7, 32, 9], [0, 5, 11, 24, 6, 13]][:streams]
+    sl = list(range(streams))
     got = {}
     for env in ("1", "0"):
         monkeypatch.setenv("CIH_FEW_WO", env)
         m = ch.GpuModel(cfg, w, max_batch=1, max_len=16)
         dec = ch.GpuDecoder(m, n_slots=2, max_len=32, max_rows=8)
-        got[env] = [dec.decode([0, 1], [a, b], [p, p]) for p, (a, b) in enumerate(zip(*toks))]
+        got[env] = [dec.decode(sl, list(col), [p] * streams) for p, col in enumerate(zip(*toks))]
         dec.close()
         m.close()
     for p in range(len(toks[0])):
-        for s in range(2):
+        for s in range(streams):
             e = float(np.abs(got["1"][p][s] - got["0"][p][s]).max())
             assert e <= 1e-5, (p, s, e)
-    for s in range(2):
+    for s in range(streams):
         rs = cr.RunState(cfg, w, max_len=32, num_threads=8)
         for p, t in enumerate(toks[s]):
             report(f"hd {hd} {fmt} stream {s} step {p}", got["1"][p][s], rs.step(t, p))
