@@ -406,7 +406,10 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     //    column tile's scaling is deferred under the next block's MFMAs (its
     //    FMAs would otherwise trail the block);
     //  * RT == 1: all CT chains interleaved (one chain per column tile would
-    //    leave each MFMA waiting for its predecessor), scaled after the block.
+    //    leave each MFMA waiting for its predecessor); a block's sums are
+    //    scaled at the start of the next block, each column tile just before
+    //    its chain restarts, so the FMAs run under the LDS reads and MFMAs
+    //    of that block instead of trailing this one (same order of additions).
     f32x16 acc[RT][CT];
 #pragma unroll
     for (int r = 0; r < RT; r++)
@@ -421,6 +424,15 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     for (int r = 0; r < (RT >= 2 ? RT : 1); r++)
 #pragma unroll
         for (int q = 0; q < 16; q++) pend[r][q] = 0.0f;
+    // RT == 1: the previous block's chains and scales (zero before the first)
+    f32x16 tcar[RT >= 2 ? 1 : CT];
+    float dcar[RT >= 2 ? 1 : CT];
+#pragma unroll
+    for (int c = 0; c < (RT >= 2 ? 1 : CT); c++) {
+        dcar[c] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) tcar[c][q] = 0.0f;
+    }
     const int swA = (li >> 1) & 7, swB = (li >> 2) & 3;
     // B operands of column tile c, both k-halves
     auto read_b2 = [&](const unsigned char *base, int c, f16x8 (&b)[2]) __attribute__((always_inline)) {
@@ -494,23 +506,24 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                 }
             }
         } else {
-            f32x16 tmp[NT];
             f16x8 b[CT][2];
 #pragma unroll
             for (int c = 0; c < CT; c++) read_b2(base, c, b[c]);
 #pragma unroll
+            for (int c = 0; c < CT; c++) {
+#pragma unroll
+                for (int q = 0; q < 16; q++) acc[0][c][q] += dcar[c] * tcar[c][q];
+                mfma(a[0][0][0], b[c][0], tcar[c], true);
+            }
+#pragma unroll
             for (int kh = 0; kh < 2; kh++) {
 #pragma unroll
-                for (int l = 0; l < 2; l++)
+                for (int l = kh == 0 ? 1 : 0; l < 2; l++)
 #pragma unroll
-                    for (int c = 0; c < CT; c++) mfma(a[kh][l][0], b[c][kh], tmp[c], kh == 0 && l == 0);
+                    for (int c = 0; c < CT; c++) mfma(a[kh][l][0], b[c][kh], tcar[c], false);
             }
 #pragma unroll
-            for (int c = 0; c < CT; c++) {
-                const float d = scale_of(base, c);
-#pragma unroll
-                for (int q = 0; q < 16; q++) acc[0][c][q] += d * tmp[c][q];
-            }
+            for (int c = 0; c < CT; c++) dcar[c] = scale_of(base, c);
         }
     };
 
@@ -565,6 +578,11 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         for (int r = 0; r < RT; r++)
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][CT - 1][q] += dpend * pend[r][q];
+    } else {
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc[0][c][q] += dcar[c] * tcar[c][q];
     }
 
     // Epilogue: every output value is formed before the first store (the
