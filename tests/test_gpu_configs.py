@@ -3,11 +3,17 @@ finishes in seconds it checks one or more sequences of the batch directly;
 everywhere, size-independent properties: exported softmax rows sum to 1,
 contact maps are symmetric probabilities, and the default kernels agree with
 independent ones (FP32-MFMA attention and FP32-MFMA dequantizing GEMM)."""
+import os
+import sys
+
 import numpy as np
 import pytest
 
 import codon_hip as ch
 import cpu_ref as cr
+from test_gpu_forward import check_argmax
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 pytestmark = pytest.mark.gpu
 
@@ -81,21 +87,31 @@ def test_config3_150m_q4_contacts_maps(monkeypatch):
 
 
 def test_config5_3b_q4_long(monkeypatch):
-    """3B Q4_0, B=1, L=2048 (attention-dominated).  The oracle needs minutes
-    at this length, so: a 62-residue sequence vs the oracle on the same
-    weights, and at L=2048 the default kernels against the independent
-    FP32-MFMA attention + FP32-MFMA GEMM (CIH_ATT=fp32, CIH_QGEMM=fp32)."""
-    rng = np.random.default_rng(5)
-    cfg = ch.EsmConfig.esm2_3b()
-    w = ch.EsmWeights.random(cfg, seed=3000, bias_std=0.02).quantize_q4()
+    """3B Q4_0, B=1, L=2048 (attention-dominated).  The full-length logits
+    against the oracle's: the oracle needs minutes at this length, so
+    tests/golden/make_config5_fixture.py ran it once on the same seeded model
+    and tokens and committed its logits.  Also a 62-residue sequence against
+    the oracle run here, and at L=2048 the default kernels against the
+    independent FP32-MFMA attention + FP32-MFMA GEMM (CIH_ATT=fp32,
+    CIH_QGEMM=fp32)."""
+    sys.path.insert(0, GOLDEN)
+    from make_config5_fixture import model_and_tokens, weights_digest
+
+    fx = np.load(os.path.join(GOLDEN, "config5_3b_q4_l2048.npz"))
+    cfg, w, toks = model_and_tokens()
+    assert np.array_equal(toks, fx["tokens"])
+    assert weights_digest(w) == str(fx["weights_sha256"]), "the seeded 3B model differs from the fixture's"
     m = ch.GpuModel(cfg, w, max_batch=1, max_len=2048, outputs=ch.OUT_LOGITS)
+    a = m.forward([toks])["logits"][0]
+    e = float(np.abs(a.astype(np.float64) - fx["logits"]).max())
+    print(f"3B Q4_0 L=2048 logits vs oracle: max abs {e:.2e}", flush=True)
+    assert e <= 1e-3
+    check_argmax(a, fx["logits"], "3B Q4_0 L=2048")
+    rng = np.random.default_rng(5)
     short = rand_tokens(rng, 62)
     got = m.forward([short])["logits"][0]
     ref = cr.forward(cfg, w, short, 16, final_att=False, hidden=False)["logits"]
     assert np.abs(got - ref).max() <= 1e-3
-    toks = rand_tokens(rng, 2046)
-    a = m.forward([toks])["logits"][0]
-    assert np.isfinite(a).all()
     # kernel by kernel, so that no graph captured under the default switches
     # can stand in for the FP32-MFMA kernels; their results must differ in
     # rounding (identical logits would mean the same kernels ran twice)
