@@ -219,7 +219,10 @@ int enqueue_rows(cih_decoder *dc, int n, bool fused) {
         HIPCHK(model_gemm(m, dc->part, m->dense, dc->ao, d, AF_F32, m->dense_b, dc->h, d, n, EPI_GELU));
         {
             ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * n * d);
-            HIPCHK(launch_layernorm(dc->h, m->lm_lnw, m->lm_lnb, dc->xb, AF_F32, n, d, st));
+            // its output feeds the decoder's GEMM, which splits it into f16
+            // limbs for more rows than the GEMV takes
+            HIPCHK(launch_layernorm(dc->h, m->lm_lnw, m->lm_lnb, dc->xb, AF_F32, n, d, st,
+                                    step_limbs(dc, n) ? dc->d_flag : nullptr));
         }
         HIPCHK(model_gemm(m, dc->part, m->dec, dc->xb, d, AF_F32, m->dec_b, dc->logits, V, n, EPI_NONE));
     } else {

@@ -86,7 +86,10 @@ __global__ __launch_bounds__(RLN_MAX_THREADS) void k_rln(float *__restrict__ x, 
         if (c >= n4) break;
         f32x4 y;
 #pragma unroll
-        for (int e = 0; e < 4; e++) y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+        for (int e = 0; e < 4; e++) {
+            y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+            flag_limb_range(flag, y[e]);
+        }
         if constexpr (OF == AF_H2)
             h2_store4(reinterpret_cast<unsigned short *>(out), row, 4 * c, d, make_float4(y.x, y.y, y.z, y.w));
         else
@@ -150,7 +153,10 @@ __global__ __launch_bounds__(256) void k_rln4(float *__restrict__ x, const float
         if (c >= n4) break;
         f32x4 y;
 #pragma unroll
-        for (int e = 0; e < 4; e++) y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+        for (int e = 0; e < 4; e++) {
+            y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+            flag_limb_range(flag, y[e]);
+        }
         if constexpr (OF == AF_H2)
             h2_store4(reinterpret_cast<unsigned short *>(out), row, 4 * c, d, make_float4(y.x, y.y, y.z, y.w));
         else

@@ -283,7 +283,16 @@ struct SeqMeta {
 // Bits of a forward's device status word (one int, cleared before the
 // forward, read after it).
 constexpr int FLAG_BAD_TOKEN = 1;  // a token id outside [0, V) (device-pointer input)
-constexpr int FLAG_NONFINITE = 2;  // a LayerNorm row with a non-finite mean or variance
+// FLAG_NONFINITE: a LayerNorm row with a non-finite mean or variance, or (in a
+// LayerNorm given the flag) an output the f16 limbs of the GEMM it feeds cannot
+// hold: |y| >= 65520 rounds to an infinite hi limb.
+constexpr int FLAG_NONFINITE = 2;
+
+// Flags a LayerNorm output that is not finite or lies beyond the f16 limbs'
+// range (no-op without a status word).
+__device__ __forceinline__ void flag_limb_range(int *flag, float y) {
+    if (flag && !(__builtin_fabsf(y) < 65520.0f)) atomicOr(flag, FLAG_NONFINITE);
+}
 
 // Few-token forward (few.hip).  x += pbias + (sum of the S splits of part,
 // [S][rows][d]; part may be null), then out = LayerNorm(x) as FP32 or H2
@@ -318,7 +327,9 @@ hipError_t launch_embed(const int *tokens, SeqMeta sm, int emb_fmt, const void *
 
 // out = LayerNorm(x) over rows of width d (eps 1e-5); out_fmt AF_F32, AF_X3
 // or AF_H2.  flag (may be null): FLAG_NONFINITE is set when a row's mean or
-// variance is not finite (the row holds an inf or NaN).
+// variance is not finite (the row holds an inf or NaN) or an output is not
+// finite or reaches 65520 in magnitude (beyond the f16 limbs of the GEMM that
+// reads it).
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, void *out, int out_fmt, int rows,
                             int d, hipStream_t st, int *flag = nullptr);
 

@@ -101,6 +101,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
         const int c = lane + 64 * i;
         if (c < d) {
             const float y = g[i] * (v[i] - mean) * inv + be[i];
+            flag_limb_range(flag, y);
             if constexpr (OF == AF_X3)
                 x3_store(reinterpret_cast<unsigned short *>(out), row, c, d, y);
             else if constexpr (OF == AF_H2)
@@ -152,7 +153,10 @@ __global__ __launch_bounds__(256) void k_layernorm4(const float *__restrict__ x,
         if (c < n4) {
             f32x4 y;
 #pragma unroll
-            for (int e = 0; e < 4; e++) y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+            for (int e = 0; e < 4; e++) {
+                y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+                flag_limb_range(flag, y[e]);
+            }
             const float4 yy = make_float4(y.x, y.y, y.z, y.w);
             if constexpr (OF == AF_X3)
                 x3_store4(reinterpret_cast<unsigned short *>(out), row, 4 * c, d, yy);

@@ -142,12 +142,14 @@ int cih_model_destroy(cih_model *m);
  * Token ids outside [0, vocab) return CIH_ERR_TOKEN: checked on the host, or
  * with CIH_IO_DEVICE on the device during the forward (the outputs are then
  * undefined).
- * Range: the default kernels hand activations to the quantized GEMMs and to
- * attention as two f16 limbs, which hold |x| < 65504 only.  A forward whose
- * residual stream turns non-finite is run once more with the full-range
- * kernels (three bf16 limbs, FP32-MFMA attention, the whole FP32 exponent
- * range), and those results are returned: outputs are finite wherever the
- * reference's are. */
+ * Range: the default kernels hand activations to the GEMMs and to attention
+ * as two f16 limbs, which hold |x| < 65520 only.  A forward whose residual
+ * stream turns non-finite, or whose final or LM-head LayerNorm writes a value
+ * of 65520 or more in magnitude (the input of the LM head's limb GEMMs), is
+ * run once more with the full-range kernels (three bf16 limbs, FP32-MFMA
+ * attention and FP32-MFMA LM head, the whole FP32 exponent range), and those
+ * results are returned.  Covered: an overflow inside a layer (it reaches the
+ * residual stream) and at the LM head's inputs. */
 int cih_forward(cih_model *m, const int32_t *tokens, const int32_t *lens, int32_t B,
                 int32_t S_max, uint32_t flags, const cih_outputs *out);
 

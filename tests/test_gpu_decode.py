@@ -235,3 +235,66 @@ def test_decode_attention_with_wo(hd, fmt, streams, monkeypatch):
         rs = cr.RunState(cfg, w, max_len=32, num_threads=8)
         for p, t in enumerate(toks[s]):
             report(f"hd {hd} {fmt} stream {s} step {p}", got["1"][p][s], rs.step(t, p))
+
+
+def overflow_model(where, seed):
+    """A model whose reference results do not depend on one activation column
+    that the f16 limbs cannot hold (~7e4, past f16's 65504): layer 0's LN1
+    column 37 (Q, K, V weights of that column zero) or the LM head's
+    LayerNorm column 37 (decoder weights of that column zero)."""
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=seed, bias_std=0.02)
+    d, V, c = cfg.dim, cfg.vocab_size, 37
+    if where == "ln1":
+        b1 = np.array(w.ln_1_bias, np.float32)
+        b1[c] = 7.0e4
+        w.ln_1_bias = b1
+        for name in ("wq", "wk", "wv"):
+            a = np.array(getattr(w, name), np.float32).reshape(cfg.n_layers, d, d)
+            a[0, :, c] = 0.0
+            setattr(w, name, a.ravel())
+    else:
+        cw = np.array(w.classifier_weights, np.float32)
+        cw[d + c] = 7.0e4
+        cw[3 * d + d * d:3 * d + d * d + V * d].reshape(V, d)[:, c] = 0.0
+        w.classifier_weights = cw
+    return cfg, w.quantize_q8()
+
+
+@pytest.mark.parametrize("rows", [1, 2])
+def test_limb_overflow_decode_steps_run_full_range(rows):
+    """Decode analogue of test_limb_overflow_runs_full_range: every step of
+    one stream (LayerNorms inside the QKV and FC1 GEMVs, attention with Wo,
+    replayed graph) or of two streams overflows the f16 limbs in layer 0; the
+    NaN reaches the final LayerNorm, the step runs again in full range,
+    rewriting the same cache positions, and every step and the steps after
+    it match the oracle."""
+    cfg, w = overflow_model("ln1", 96)
+    m = ch.GpuModel(cfg, w, max_batch=1, max_len=16)
+    dec = ch.GpuDecoder(m, n_slots=rows, max_len=32, max_rows=16)
+    refs = [cr.RunState(cfg, w, max_len=32, num_threads=4) for _ in range(rows)]
+    for p in range(8):
+        toks = [0 if p == 0 else 4 + (7 * p + 3 * s) % 20 for s in range(rows)]
+        got = dec.decode(list(range(rows)), toks, [p] * rows)
+        for s in range(rows):
+            report(f"rows {rows} slot {s} step {p}", got[s], refs[s].step(toks[s], p))
+    dec.close()
+    m.close()
+
+
+def test_lm_head_input_beyond_limbs_in_prefill():
+    """A 12-row prefill (the MFMA GEMMs, f16 limbs) whose LM-head LayerNorm
+    writes ~7e4: flagged, the rows run again in full range (FP32-MFMA LM
+    head) and match the oracle; the one-row steps after it (FP32 GEMV LM
+    head, no limbs) too."""
+    cfg, w = overflow_model("lm_head", 97)
+    m = ch.GpuModel(cfg, w, max_batch=1, max_len=16)
+    dec = ch.GpuDecoder(m, n_slots=1, max_len=32, max_rows=16)
+    rs = cr.RunState(cfg, w, max_len=32, num_threads=4)
+    toks = [0, 20, 5, 32, 11, 11, 23, 4, 17, 9, 30, 12]
+    rows = dec.decode(np.zeros(len(toks)), toks, np.arange(len(toks)))
+    report("prefill of 12 rows", rows, np.stack([rs.step(t, p) for p, t in enumerate(toks)]))
+    for p in range(len(toks), len(toks) + 3):
+        report(f"step {p}", dec.decode([0], [7], [p])[0], rs.step(7, p))
+    dec.close()
+    m.close()

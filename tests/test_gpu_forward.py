@@ -523,6 +523,36 @@ def test_limb_overflow_runs_full_range(dtype):
     check_batch(cfg, w, seqs, ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT)
 
 
+@pytest.mark.parametrize("where", ["final_ln", "lm_head_ln"])
+def test_lm_head_input_beyond_limbs_runs_full_range(where):
+    """A LayerNorm output the f16 limbs of the LM head's GEMMs cannot hold:
+    column 37 of the final LayerNorm (bias 7e4; the dense weights of that
+    column zero) or of the LM head's own LayerNorm (bias 7e4; the decoder's
+    weights of that column zero) is ~7e4, so the reference's logits do not
+    depend on it, while a hi limb of f16(7e4) = inf gives inf * 0 = NaN.
+    The LayerNorm flags the value, the forward runs again with the FP32-MFMA
+    LM head and the logits match the oracle."""
+    rng = np.random.default_rng(95)
+    cfg = ch.EsmConfig(128, 512, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=95, bias_std=0.02)
+    d, V, c = cfg.dim, cfg.vocab_size, 37
+    cw = np.array(w.classifier_weights, np.float32)  # [ln_w d, ln_b d, dense_w d*d, dense_b d, dec_w V*d, dec_b V]
+    if where == "final_ln":
+        fb = np.array(w.ln_f_bias, np.float32)
+        fb[c] = 7.0e4
+        w.ln_f_bias = fb
+        cw[2 * d:2 * d + d * d].reshape(d, d)[:, c] = 0.0
+    else:
+        cw[d + c] = 7.0e4
+        cw[3 * d + d * d:3 * d + d * d + V * d].reshape(V, d)[:, c] = 0.0
+    w.classifier_weights = cw
+    w = w.quantize_q8()
+    seqs = [rand_tokens(rng, n) for n in (60, 33)]
+    # logits only: a hidden state of ~7e4 carries 1-ulp (0.0078) differences
+    # whenever the rounding of the small part differs
+    check_batch(cfg, w, seqs, ch.OUT_LOGITS)
+
+
 def test_graph_key_follows_kernel_switches(monkeypatch):
     """A captured forward is keyed by the kernel switches read while it was
     enqueued: with graphs on, CIH_ATT=fp32 after a default forward of the same
