@@ -34,8 +34,16 @@ int scratch_of_current_device(unsigned char **out) {
     if (dev < 0 || dev >= MAX_DEVICES) return set_error(CIH_ERR_HIP, "device %d outside [0, %d)", dev, MAX_DEVICES);
     std::lock_guard<std::mutex> lock(g_mu);
     if (!g_ptr[dev]) {
+        // The first call on a device may come while the caller's stream is
+        // being captured into a graph (in any capture mode): the one-time
+        // lookup runs with this thread's capture mode relaxed, as a library's
+        // lazy initialisation must, and the caller's mode is restored.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        HIPCHK(hipThreadExchangeStreamCaptureMode(&mode));
         void *p = nullptr;
-        HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        HIPCHK(hipThreadExchangeStreamCaptureMode(&mode));
+        HIPCHK(e);
         if (!p) return set_error(CIH_ERR_HIP, "no device address for the scratch array");
         g_ptr[dev] = static_cast<unsigned char *>(p);
     }
