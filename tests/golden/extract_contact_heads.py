@@ -1,11 +1,13 @@
-"""Writes contact_heads.json: the ESM-2 contact-head logistic-regression
-weights (L*H weights, l-major, plus one bias per architecture) as data.
+"""Writes codon-infer_amd/codon_hip/data/contact_heads.json: the ESM-2
+contact-head logistic-regression weights (L*H weights, l-major, plus one bias
+per architecture) as data.  An offline generator run once in the build
+container; the package only reads the JSON it wrote.
 
 Source: the `CONTACT_HEAD_*_WEIGHT` / `CONTACT_HEAD_*_BIAS` constant tables of
 codon-infer's src/contact_heads.rs (lines 5, 24, 58, 137, 224), which hold
 Meta's `esm.contact_head.regression` parameters.  The file is parsed as text;
 nothing is executed.  Usage:
-    python extract_contact_heads.py /path/to/codon-infer/src/contact_heads.rs
+    python tests/golden/extract_contact_heads.py /path/to/codon-infer/src/contact_heads.rs
 """
 import json
 import os
@@ -33,7 +35,8 @@ def main():
     src = sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src/contact_heads.rs"
     with open(src) as f:
         data = parse(f.read())
-    dst = os.path.join(os.path.dirname(os.path.abspath(__file__)), "contact_heads.json")
+    repo = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    dst = os.path.join(repo, "codon-infer_amd", "codon_hip", "data", "contact_heads.json")
     with open(dst, "w") as f:
         json.dump(data, f)
     print("wrote", dst, {k: len(v["weight"]) for k, v in data.items()})

@@ -166,3 +166,112 @@ def test_rust_ffi_declares_every_entry_point():
     assert c_funcs and c_funcs == r_funcs, (set(c_funcs) ^ set(r_funcs),
                                             {k: (c_funcs.get(k), r_funcs.get(k)) for k in c_funcs
                                              if c_funcs.get(k) != r_funcs.get(k)})
+
+
+def _header_structs(header):
+    """Field names of each `typedef struct name { ... } name;` in the header."""
+    out = {}
+    for m in re.finditer(r"typedef struct (cih_[a-z_]+) \{(.*?)\} \1;", header, re.S):
+        body = re.sub(r"/\*.*?\*/", "", m.group(2), flags=re.S)
+        names = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if decl:
+                names += [re.sub(r"[^a-z0-9_]", "", p.split()[-1]) for p in decl.split(",")]
+        out[m.group(1)] = names
+    return out
+
+
+def test_integration_extern_block_matches_header():
+    """INTEGRATION.md section 1 shows the extern block a maintainer adds to the
+    crate: every function it declares exists in include/codon_hip.h with the
+    same number of parameters, and its #[repr(C)] structs list the header's
+    fields in the header's order (config, host weights, outputs)."""
+    with open(os.path.join(REPO, "include", "codon_hip.h")) as f:
+        header = f.read()
+    with open(os.path.join(REPO, "INTEGRATION.md")) as f:
+        doc = f.read()
+    sec = doc[doc.index("## 1."):doc.index("## 2.")]
+    block = sec[sec.index("```rust"):sec.index("```", sec.index("```rust") + 7)]
+    c_funcs = {m.group(1): len([a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"])
+               for m in re.finditer(r"\b(?:int|const char \*)\s*(cih_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", header)}
+    r_funcs = {m.group(1): len([a for a in m.group(2).split(",") if a.strip()])
+               for m in re.finditer(r"pub fn (cih_[a-z0-9_]+)\(([^)]*)\)", block)}
+    assert r_funcs, "no declarations found in INTEGRATION.md section 1"
+    bad = {k: (c_funcs.get(k), v) for k, v in r_funcs.items() if c_funcs.get(k) != v}
+    assert not bad, bad
+    structs = _header_structs(header)
+    for rust_name, c_name in (("CihConfig", "cih_config"), ("CihHostWeights", "cih_host_weights"),
+                              ("CihOutputs", "cih_outputs")):
+        m = re.search(r"pub struct " + rust_name + r"\s*\{(.*?)\}", block, re.S)
+        assert m, rust_name
+        fields = re.findall(r"pub ([a-z0-9_]+)\s*:", m.group(1))
+        assert fields == structs[c_name], (rust_name, fields, structs[c_name])
+
+
+# Exact file sizes of the five presets with the full LM head (reference
+# README.md:372-374): FP32 grouped_canonical_v1 (headerless), Q8_0 and Q4_0
+# with the 64-byte CODQ header.
+PRESET_BYTES = {
+    "8M": (30_091_652, 8_864_556, 5_208_516),
+    "35M": (134_067_972, 38_636_896, 22_093_636),
+    "150M": (592_642_692, 168_646_036, 94_978_756),
+    "650M": (2_604_339_332, 738_899_556, 414_617_796),
+    "3B": (11_356_354_692, 3_216_540_676, 1_801_205_956),
+}
+# sequential_hf FP32 sizes the reference detects by length (lib.rs:228-234)
+SEQUENTIAL_HF_BYTES = {"8M": 30_092_168, "35M": 134_068_984, "150M": 592_645_160, "650M": 2_604_342_104,
+                       "3B": 11_356_360_584}
+
+
+def _layout_bytes(cfg, dtype):
+    """Bytes of a file written in EsmWeights* field order (the loader's and
+    save_codq's layout): the layer matrices as 36/20-byte blocks per 32
+    weights (FP32: 4 bytes per weight); the token embedding as Q8_0 blocks in
+    a Q8_0 file and FP32 otherwise (quantize_q8 / quantize_q4, lib.rs:559-607);
+    every vector and the LM head in FP32; plus the CODQ header for quantized
+    files."""
+    d, F, L, V = cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.vocab_size
+    matrices = L * (4 * d * d + 2 * d * F)
+    vectors = L * (9 * d + F) + 2 * d + cfg.lm_head_floats()
+    per32 = {0: 128, 1: 36, 2: 20}[dtype]
+    emb = V * d // 32 * 36 if dtype == 1 else 4 * V * d
+    return (64 if dtype else 0) + matrices // 32 * per32 + emb + 4 * vectors
+
+
+@pytest.mark.parametrize("arch", list(PRESET_BYTES))
+def test_preset_file_sizes_and_length_detection(arch, tmp_path):
+    """Every preset and format: the layout's total is the reference's
+    published file size; a file of exactly that size (header + sparse body)
+    passes every format check of cih_model_create_from_file (without a GPU
+    the first failure is then the device, CIH_ERR_HIP), and a headerless FP32
+    file of the grouped_canonical_v1 or sequential_hf size is recognised by
+    its length alone (EsmConfig::detect_from_file_len, lib.rs:195-273),
+    while 4 bytes more are not."""
+    cfg = ch.EsmConfig.by_name(arch)
+    fp32, q8, q4 = PRESET_BYTES[arch]
+    assert _layout_bytes(cfg, 0) == fp32 == cfg.grouped_canonical_floats() * 4
+    assert _layout_bytes(cfg, 1) == q8 and _layout_bytes(cfg, 2) == q4
+    hd = cfg.dim // cfg.n_heads
+    assert fp32 + 4 * (hd // 2 + cfg.n_layers * cfg.n_heads + 1) == SEQUENTIAL_HF_BYTES[arch]
+    if os.environ.get("CIH_EXPECT_GPU") == "1":
+        pytest.skip("with a GPU these files would be loaded in full")
+    arch_id = ch.model.ARCH_IDS[arch]
+
+    def sparse(name, size, header=None):
+        p = str(tmp_path / name)
+        with open(p, "wb") as f:
+            if header:
+                f.write(header)
+            f.truncate(size)
+        return p
+
+    for dtype, size in ((1, q8), (2, q4)):
+        hdr = _codq_header(dtype, arch_id, cfg)
+        assert _create_from_file(sparse(f"{arch}.{dtype}", size, hdr)) == -5, C.lib().cih_last_error()
+        assert _create_from_file(sparse(f"{arch}.{dtype}.odd", size - 1, hdr)) == -7      # unaligned classifier
+        assert _create_from_file(sparse(f"{arch}.{dtype}.short", 4096, hdr)) == -6        # body cut short
+    for name, size in (("grouped", fp32), ("sequential", SEQUENTIAL_HF_BYTES[arch])):
+        assert _create_from_file(sparse(f"{arch}.{name}", size)) == -5, C.lib().cih_last_error()
+    assert _create_from_file(sparse(f"{arch}.plus4", fp32 + 4)) == -7
+    assert b"unrecognized" in C.lib().cih_last_error()
