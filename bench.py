@@ -378,7 +378,8 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seq-len", type=int, default=512,
                     help="tokens per sequence; --batch 1 --seq-len 8 or less measures the weight-streaming GEMV")
-    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=20.0,
+                    help="seconds of CPU baseline work (the timed forwards after the warm-up)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--model", choices=["8M", "35M", "150M", "650M", "3B"], default="650M")
     ap.add_argument("--dtype", choices=["fp32", "q8", "q4"], default="q8")

@@ -41,7 +41,7 @@ std::string kernel_switches() {
                                         "CIH_QGEMM",   "CIH_ACT",    "CIH_LIMBS",     "CIH_GEMV",
                                         "CIH_GEMV_NB", "CIH_GEMM_LDS", "CIH_GEMM_TILE", "CIH_GEMM_TILE_N",
                                         "CIH_GEMM_TILE_N_GELU", "CIH_ATT_IMG", "CIH_GEMV16", "CIH_GEMV16_KW",
-                                        "CIH_FEW_WO", "CIH_DECODE_LN"};
+                                        "CIH_FEW_WO", "CIH_DECODE_LN", "CIH_ATT_XCD"};
     std::string s = g_full_range ? "R|" : "|";
     for (const char *n : names) {
         const char *v = getenv(n);
@@ -607,8 +607,9 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         HIPCHK(launch_apc_finalize(ws.M, ws.r, ws.coef, m->d_contact_w, L * H, sm, m->contact_b, t_contacts, n_max, st));
     }
     // final LayerNorm: state.x = LN_f(x) (lib.rs:5379-5387).  It also
-    // reports a residual row that is no longer finite: the f16 limbs hold
-    // |x| < 65504 only, and an overflow there makes the residual non-finite.
+    // reports a residual row that is no longer finite (the f16 limbs hold
+    // |x| < 65520 only, and an overflow there makes the residual non-finite)
+    // and an output the LM head's limbs cannot hold.
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
         if (pend_splits)
@@ -623,7 +624,8 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
             HIPCHK(gemm(m, m->dense, ws.ao, d, AF_F32, m->dense_b, ws.hbuf, d, T, EPI_GELU));
             {
                 ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
-                HIPCHK(launch_layernorm(ws.hbuf, m->lm_lnw, m->lm_lnb, ws.xb, AF_F32, T, d, st));
+                // its output feeds the decoder's GEMM, which splits it into f16 limbs
+                HIPCHK(launch_layernorm(ws.hbuf, m->lm_lnw, m->lm_lnb, ws.xb, AF_F32, T, d, st, ws.flag));
             }
             HIPCHK(gemm(m, m->dec, ws.xb, d, AF_F32, m->dec_b, ws.logits, V, T, EPI_NONE));
         } else {

@@ -1179,7 +1179,7 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
     const int *__restrict__ tb, const unsigned char *__restrict__ img, const float *__restrict__ rc,
     const float *__restrict__ rsn, void *__restrict__ out, int out_fmt, float *__restrict__ P, long long pb,
     long long ph, float inv_scale, float *__restrict__ rowsum, int H, int nq, int nfull, int nsplit,
-    float *__restrict__ part) {
+    float *__restrict__ part, int xcd_pairs) {
     // no FMA contraction: the staged and the image kernel round alike
 #pragma clang fp contract(off)
     using I = KvImg<HD>;
@@ -1195,6 +1195,13 @@ __global__ __launch_bounds__(NTH, ONEPASS || HD <= 32 ? 4 : 2) void k_attention_
         task = nfull + t / nsplit;
         ks = t % nsplit;
         ns = nsplit;
+    } else if (xcd_pairs) {
+        // Workgroups go to the 8 XCDs in turn (id % 8); the nq query blocks
+        // of one (sequence, head) read the same K/V images, so they are given
+        // ids 8 apart: one XCD, whose L2 then serves the image to the others.
+        // Ids in groups of 8 nq: block qb of head pair p = 8 g + r at 8 nq g + 8 qb + r.
+        const int g = task / (8 * nq), r = task % (8 * nq);
+        task = (8 * g + r % 8) * nq + r / 8;
     }
     const int qb = task % nq, h = (task / nq) % H, b = task / nq / H;
     const int len = lens[b], base = cu[b];
@@ -1703,10 +1710,13 @@ hipError_t launch_attention_img(const float *qkv, int d, int H, SeqMeta sm, cons
         }
     }
     const int grid = nfull + (tasks - nfull) * nsplit;
+    // the query blocks of a head on one XCD: unsplit grids of whole groups of 8 heads
+    const char *xe = getenv("CIH_ATT_XCD");
+    const int xcd_pairs = nq > 1 && nfull == tasks && (sm.B * H) % 8 == 0 && !(xe && !strcmp(xe, "0"));
 #define CIH_ATI(HDV, ONE, NTH)                                                                                   \
     hipLaunchKernelGGL((k_attention_img<HDV, ONE, NTH>), dim3(grid), dim3(NTH), 0, st, qkv, d, sm.cu, sm.lens,    \
                        sm.S_max, tb, img, rope_cos, rope_sin, out, out_fmt, P, (long long)pb, (long long)ph,      \
-                       inv_scale, rowsum, H, nq, nfull, nsplit, part)
+                       inv_scale, rowsum, H, nq, nfull, nsplit, part, xcd_pairs)
 #define CIH_ATI_HD(HDV)                                                                                          \
     if (P && wide) CIH_ATI(HDV, false, 512);                                                                      \
     else if (P) CIH_ATI(HDV, false, 256);                                                                         \
