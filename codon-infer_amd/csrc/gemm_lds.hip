@@ -305,7 +305,7 @@ __device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned cha
 // SPLIT: workgroup (tile, y) takes k-blocks [y kps, (y + 1) kps) and stores
 // its raw sums (no bias, no epilogue) into part + y M N, row-major [M][N];
 // the caller adds the splits in order (EPI_NONE only).
-template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false>
+template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false, int SCH = 0>
 __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned char *__restrict__ WB, const float *__restrict__ Wsc,
     const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo, int kps = 0) {
@@ -322,10 +322,13 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     constexpr int XTRA = PREF ? BM * 8 + 2 * BM * QHALF * 4 : 0;
     constexpr int EL = QKV ? qkv_epilogue_lds<2 * QHALF, RT, CT, WM, WN>() : 0;
     constexpr int LOFF = 3 * STAGE > EL ? 3 * STAGE : EL;  // start of the prefetched rows
-    static_assert(LOFF + XTRA <= 160 * 1024, "LDS");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[LOFF + XTRA];
+    // the tile's BN bias values, written 64 at a time (whole 256-byte rows)
+    constexpr int BOFF = LOFF + XTRA, BBYTES = (BN * 4 + 255) / 256 * 256;
+    static_assert(BOFF + BBYTES <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[BOFF + BBYTES];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index is uniform: wave-derived offsets (LDS destinations) live in SGPRs
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int li = lane & 31, hh = lane >> 5;
     const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
@@ -378,12 +381,19 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         dstB[i] = SA + j * 1024;
     }
     const float *srcS = Wsc + min(n0 + wave * SL + min(lane, SL - 1), N - 1);
-    // Bias of this lane's columns, loaded before the k loop: the stores of
-    // the epilogue then follow no pending load (a load still pending at a
-    // branch makes the compiler wait for every earlier store as well).
-    float bv[CT];
-#pragma unroll
-    for (int c = 0; c < CT; c++) bv[c] = bias ? bias[min(n0 + (wn * CT + c) * 32 + li, N - 1)] : 0.0f;
+    // The tile's bias values go to LDS before the k loop (copied by the load
+    // unit, ordered by the loop's first wait and barrier): the epilogue reads
+    // them from LDS, so its stores follow no pending global load (a load
+    // pending at a branch makes the compiler wait for every earlier store as
+    // well) and no register holds them through the loop.
+    float *s_bias = reinterpret_cast<float *>(lds + BOFF);
+    if (bias) {
+        if (wave * 64 < BN)
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(bias + min(n0 + wave * 64 + lane, N - 1)),
+                                             (lds_ptr_t *)(lds + BOFF + wave * 256), 4, 0, 0);
+    } else {
+        for (int i = tid; i < BN; i += T::THREADS) s_bias[i] = 0.0f;
+    }
 
     auto request = [&](int kb, int stg) __attribute__((always_inline)) {
         unsigned char *base = lds + stg * STAGE;
@@ -400,8 +410,8 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                                              (lds_ptr_t *)(base + SA + SB + wave * SL * 4), 4, 0, 0);
     };
 
-    // Two schedules with the same arithmetic (per 32 x 32 tile: tmp = both
-    // limbs x both k-halves, then acc += d * tmp in block order):
+    // Schedules with the same arithmetic (per 32 x 32 tile: tmp = both limbs
+    // x both k-halves, then acc += d * tmp in block order):
     //  * RT >= 2: column tile after column tile, RT chains each; the last
     //    column tile's scaling is deferred under the next block's MFMAs (its
     //    FMAs would otherwise trail the block);
@@ -409,7 +419,10 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     //    leave each MFMA waiting for its predecessor); a block's sums are
     //    scaled at the start of the next block, each column tile just before
     //    its chain restarts, so the FMAs run under the LDS reads and MFMAs
-    //    of that block instead of trailing this one (same order of additions).
+    //    of that block instead of trailing this one (same order of additions);
+    //  * RT == 1, CT == 5 on the f16 copy (SCH 1): chains 0-2 as a triple,
+    //    then chains 3-4 as a pair; the previous pair is scaled under the
+    //    operand reads, the triple under the pair's MFMAs (below).
     f32x16 acc[RT][CT];
 #pragma unroll
     for (int r = 0; r < RT; r++)
@@ -505,6 +518,76 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                         for (int q = 0; q < 16; q++) acc[r][c][q] += d * tmp[r][q];
                 }
             }
+        } else if constexpr (SCH == 1 && CT == 5) {
+            // Chains 0-2 as a triple, then chains 3-4 as a pair, each chain's
+            // MFMAs in the same (k-half, limb) order as the default schedule.
+            // The previous block's pair is scaled first, under the latency of
+            // this block's operand reads; this block's triple is scaled under
+            // the pair's MFMAs, so the scaling FMAs run beside MFMAs instead of
+            // ahead of them.  The same additions in the same order.  The order
+            // is written out and fenced (sched_barrier), and the pair's
+            // operands are read once the triple's first k-half is issued.
+            auto rd_b = [&](int c, int kh) __attribute__((always_inline)) {
+                const int col = (wn * CT + c) * 32 + li;
+                return *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((hh * 2 + kh) ^ swB) << 4));
+            };
+            auto fence = [&]() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
+            auto scale = [&](int c, float d, int q0, int q1) __attribute__((always_inline)) {
+#pragma unroll
+                for (int q = q0; q < q1; q++) acc[0][c][q] += d * tcar[c][q];
+            };
+            const f16x8 b00 = rd_b(0, 0), b10 = rd_b(1, 0), b20 = rd_b(2, 0);
+            const f16x8 b01 = rd_b(0, 1), b11 = rd_b(1, 1), b21 = rd_b(2, 1);
+            float dcur[CT];
+#pragma unroll
+            for (int c = 0; c < CT; c++) dcur[c] = scale_of(base, c);
+            fence();
+            scale(3, dcar[3], 0, 16);
+            scale(4, dcar[4], 0, 16);
+            fence();
+            mfma(a[0][0][0], b00, tcar[0], true);
+            mfma(a[0][0][0], b10, tcar[1], true);
+            mfma(a[0][0][0], b20, tcar[2], true);
+            mfma(a[0][1][0], b00, tcar[0], false);
+            mfma(a[0][1][0], b10, tcar[1], false);
+            mfma(a[0][1][0], b20, tcar[2], false);
+            fence();
+            const f16x8 b30 = rd_b(3, 0), b40 = rd_b(4, 0), b31 = rd_b(3, 1), b41 = rd_b(4, 1);
+            fence();
+            mfma(a[1][0][0], b01, tcar[0], false);
+            mfma(a[1][0][0], b11, tcar[1], false);
+            mfma(a[1][0][0], b21, tcar[2], false);
+            mfma(a[1][1][0], b01, tcar[0], false);
+            mfma(a[1][1][0], b11, tcar[1], false);
+            mfma(a[1][1][0], b21, tcar[2], false);
+            fence();
+            mfma(a[0][0][0], b30, tcar[3], true);
+            scale(0, dcur[0], 0, 6);
+            fence();
+            mfma(a[0][0][0], b40, tcar[4], true);
+            scale(0, dcur[0], 6, 12);
+            fence();
+            mfma(a[0][1][0], b30, tcar[3], false);
+            scale(0, dcur[0], 12, 16);
+            scale(1, dcur[1], 0, 2);
+            fence();
+            mfma(a[0][1][0], b40, tcar[4], false);
+            scale(1, dcur[1], 2, 8);
+            fence();
+            mfma(a[1][0][0], b31, tcar[3], false);
+            scale(1, dcur[1], 8, 14);
+            fence();
+            mfma(a[1][0][0], b41, tcar[4], false);
+            scale(1, dcur[1], 14, 16);
+            scale(2, dcur[2], 0, 4);
+            fence();
+            mfma(a[1][1][0], b31, tcar[3], false);
+            scale(2, dcur[2], 4, 10);
+            fence();
+            mfma(a[1][1][0], b41, tcar[4], false);
+            scale(2, dcur[2], 10, 16);
+            dcar[3] = dcur[3];
+            dcar[4] = dcur[4];
         } else {
             f16x8 b[CT][2];
 #pragma unroll
@@ -579,8 +662,9 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[r][CT - 1][q] += dpend * pend[r][q];
     } else {
+        // (SCH 1 scales chains 0-2 inside each block; only the pair is pending)
 #pragma unroll
-        for (int c = 0; c < CT; c++)
+        for (int c = (SCH == 1 && CT == 5) ? 3 : 0; c < CT; c++)
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[0][c][q] += dcar[c] * tcar[c][q];
     }
@@ -603,6 +687,9 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                 }
         }
     }
+    float bv[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++) bv[c] = s_bias[(wn * CT + c) * 32 + li];
 #pragma unroll
     for (int c = 0; c < CT; c++)
 #pragma unroll
@@ -663,6 +750,14 @@ __global__ __launch_bounds__(256) void k_expand_f16(const unsigned char *__restr
     q16[i] = __builtin_bit_cast(unsigned short, (_Float16)(float)v);
 }
 
+// Block order of the 32 x 160 wave tiles reading the f16 copy: 1 (default)
+// the triple + pair order, 0 (CIH_GEMM_SCHED=0) all five chains interleaved.
+// Both give the same bits.
+int gemm_sched() {
+    const char *e = getenv("CIH_GEMM_SCHED");
+    return e ? atoi(e) : 1;
+}
+
 template <int EPI, int RT, int CT, int WM, int WN>
 hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
                     const QkvOut &qo) {
@@ -676,6 +771,10 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     else if (quants && W.fmt == WF_Q4)
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, WF_Q4>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
+    else if (RT == 1 && CT == 5 && gemm_sched() == 1)
+        hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, (RT == 1 && CT == 5) ? 1 : 0>), dim3(tiles),
+                           dim3(T::THREADS), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y,
+                           ldy, M, W.N, W.K, qo, 0);
     else
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
                            reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
