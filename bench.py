@@ -147,7 +147,7 @@ def cpu_baseline(cfg, w, tokens, budget_s, contacts=None):
         return time.perf_counter() - t0
 
     warm = run(seq(0))
-    n = max(1, min(5, int(budget_s // max(warm, 1e-9))))
+    n = max(1, min(5, round(budget_s / max(warm, 1e-9))))
     times, res = [], []
     for i in range(n):
         t = seq(i + 1)
@@ -378,7 +378,7 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seq-len", type=int, default=512,
                     help="tokens per sequence; --batch 1 --seq-len 8 or less measures the weight-streaming GEMV")
-    ap.add_argument("--cpu-budget", type=float, default=20.0,
+    ap.add_argument("--cpu-budget", type=float, default=25.0,
                     help="seconds of CPU baseline work (the timed forwards after the warm-up)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--model", choices=["8M", "35M", "150M", "650M", "3B"], default="650M")

@@ -213,10 +213,57 @@ __global__ __launch_bounds__(256) void k_head_mean(const float *__restrict__ P, 
     }
 }
 
+// The same sums with four keys per thread and every head's load issued
+// before the first addition (HM >= H heads, loads past H predicated off); the
+// additions stay in ascending h, so the bits are k_head_mean's.  Needs P, the
+// strides and S_max 16-byte aligned.
+template <int HM>
+__global__ __launch_bounds__(128) void k_head_mean4(const float *__restrict__ P, long long pb, long long ph, int H,
+                                                    const int *__restrict__ lens, int S_max,
+                                                    float *__restrict__ fa) {
+    const int p = blockIdx.x, b = blockIdx.y;
+    const int len = lens[b];
+    if (p >= len) return;
+    const float hw = 1.0f / (float)H;
+    const float *src = P + b * pb + (size_t)p * S_max;
+    float *dst = fa + ((size_t)b * S_max + p) * S_max;
+    for (int t = threadIdx.x * 4; t < len; t += 512) {
+        float4 v[HM];
+#pragma unroll
+        for (int h = 0; h < HM; h++)
+            v[h] = h < H ? *reinterpret_cast<const float4 *>(src + h * ph + t) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int h = 0; h < HM; h++) {
+            if (h < H) {
+                acc[0] += v[h].x * hw;
+                acc[1] += v[h].y * hw;
+                acc[2] += v[h].z * hw;
+                acc[3] += v[h].w * hw;
+            }
+        }
+        if (t + 4 <= len) {
+            *reinterpret_cast<float4 *>(dst + t) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (t + e < len) dst[t + e] = acc[e];
+        }
+    }
+}
+
 hipError_t launch_head_mean(const float *P, int64_t pb, int64_t ph, int H, SeqMeta sm, float *final_att,
                             hipStream_t st) {
-    hipLaunchKernelGGL(k_head_mean, dim3(sm.S_max, sm.B), dim3(256), 0, st, P, (long long)pb, (long long)ph, H,
-                       sm.lens, sm.S_max, final_att);
+    const bool al = ((uintptr_t)P & 15) == 0 && ((uintptr_t)final_att & 15) == 0 && ((pb | ph | sm.S_max) & 3) == 0;
+    if (al && H <= 20)
+        hipLaunchKernelGGL(k_head_mean4<20>, dim3(sm.S_max, sm.B), dim3(128), 0, st, P, (long long)pb, (long long)ph,
+                           H, sm.lens, sm.S_max, final_att);
+    else if (al && H <= 40)
+        hipLaunchKernelGGL(k_head_mean4<40>, dim3(sm.S_max, sm.B), dim3(128), 0, st, P, (long long)pb, (long long)ph,
+                           H, sm.lens, sm.S_max, final_att);
+    else
+        hipLaunchKernelGGL(k_head_mean, dim3(sm.S_max, sm.B), dim3(256), 0, st, P, (long long)pb, (long long)ph, H,
+                           sm.lens, sm.S_max, final_att);
     return hipGetLastError();
 }
 
