@@ -639,8 +639,9 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         if (int rc = enqueue()) return rc;
     } else {
         // the shape fixes every grid and pointer of the sequence: batch,
-        // padded length, token count, outputs and their destinations
-        const FwdGraphKey key{B, S_max, T, flags | (keep_logits ? 1u << 31 : 0u),
+        // padded length, token count, 32-key tiles, outputs and their
+        // destinations
+        const FwdGraphKey key{B, S_max, T, tile_rows, flags | (keep_logits ? 1u << 31 : 0u),
                               {t_logits, t_hidden, t_final, t_contacts, t_attn, t_layer}, kernel_switches()};
         hipGraphExec_t ex = nullptr;
         for (auto &g : ws.graphs)

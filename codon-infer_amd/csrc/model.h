@@ -26,12 +26,15 @@ struct Layer {
 // What fixes a forward's kernel sequence: grids, pointers, and the kernel
 // switches read while it is enqueued (kernel_switches()).
 struct FwdGraphKey {
-    int B = 0, S_max = 0, T = 0;
+    // tiles: sum over sequences of ceil(len / 32), the grid of the K/V image
+    // prep kernel; lengths with the same B, S_max and T can differ in it
+    int B = 0, S_max = 0, T = 0, tiles = 0;
     uint32_t flags = 0;
     const void *out[6] = {};
     std::string sw;
     bool operator==(const FwdGraphKey &o) const {
-        if (B != o.B || S_max != o.S_max || T != o.T || flags != o.flags || sw != o.sw) return false;
+        if (B != o.B || S_max != o.S_max || T != o.T || tiles != o.tiles || flags != o.flags || sw != o.sw)
+            return false;
         for (int i = 0; i < 6; i++)
             if (out[i] != o.out[i]) return false;
         return true;

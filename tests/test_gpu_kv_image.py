@@ -94,3 +94,29 @@ def test_image_maps_vs_staged(monkeypatch, hd):
     e = float(np.abs(img["attn"][0, :, :, :S, :S] - ref["attn"]).max())
     print(f"hd {hd} maps vs oracle: {e:.2e}", flush=True)
     assert e <= 1e-5
+
+
+def test_graph_replay_with_another_tile_count(monkeypatch):
+    """Two batches with the same size, longest sequence and token count but
+    a different number of 32-key tiles (lengths 34, 31, 31: 4 tiles; 34, 34,
+    28: 5 tiles).  The prep kernel runs one wave per tile and head, so the
+    second batch must not replay the first one's captured forward: its
+    outputs equal a forward launched without graphs."""
+    monkeypatch.setenv("CIH_ATT_IMG", "prep")
+    monkeypatch.setenv("CIH_ATT_SPLIT", "0")
+    cfg = ch.EsmConfig(96, 384, 2, 4)  # head size 24
+    w = ch.EsmWeights.random(cfg, seed=24, bias_std=0.02).quantize_q8()
+    rng = np.random.default_rng(24)
+    first = [rand_tokens(rng, n) for n in (32, 29, 29)]
+    second = [rand_tokens(rng, n) for n in (32, 32, 26)]
+    assert sum(map(len, first)) == sum(map(len, second)) == 96
+    m = ch.GpuModel(cfg, w, max_batch=3, max_len=34, outputs=FLAGS)
+    m.forward(first, FLAGS)
+    got = m.forward(second, FLAGS)
+    monkeypatch.setenv("CIH_FORWARD_GRAPH", "0")
+    ref = m.forward(second, FLAGS)
+    m.close()
+    print("second batch after the first: outputs of the graph path equal a forward without graphs", flush=True)
+    for name in ("logits", "hidden"):
+        for i, s in enumerate(second):
+            assert np.array_equal(got[name][i][:len(s)], ref[name][i][:len(s)]), (name, i)
