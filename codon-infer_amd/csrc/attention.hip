@@ -1567,7 +1567,11 @@ hipError_t launch_attention(const float *qkv, int d, int H, SeqMeta sm, const fl
     // tasks in six ranges, attention 41 -> 27 us per layer).  Splitting only
     // the tasks past the last whole round of a larger batch measured no gain
     // (the headline batch: 640 tasks on 512 slots, 3.85 vs 3.82 ms per
-    // forward): the parts repeat the query staging and add the merge.
+    // forward): the parts repeat the query staging and add the merge.  Nor
+    // did counting only the tasks that hold queries in a ragged batch (35M
+    // B=8, lengths 128-510: 460 of 640 tasks, two ranges each): attention
+    // 0.37 -> 0.51 ms per forward, as two workgroups per CU already keep
+    // this issue-bound kernel busy.
     // CIH_ATT_SPLIT=0 or CIH_SPLITK=0 turn it off.
     int nfull = tasks, nsplit = 1;
     const char *se = getenv("CIH_ATT_SPLIT"), *ke = getenv("CIH_SPLITK");
