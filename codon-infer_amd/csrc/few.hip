@@ -363,20 +363,30 @@ __global__ __launch_bounds__(ATTF_THREADS) void k_attn_few_wo(const float *__res
         r = rem / hq;
         j = 4 * (rem - r * hq);
     }
+    // this workgroup's Wo columns and the head's k-blocks: weights and scales
+    // requested first (they depend on nothing this layer computes), so their
+    // latency runs under the fold's and the attention's
+    const int nkb = hd / 32, c0 = (int)blockIdx.z * ncols, c1 = min(c0 + ncols, N);
+    HeadWo<WF, 1> wo;
+    wo.load(Wq, Wsc, N, h * nkb, nkb, c0, c1);
+    // the QKV projection's splits in chunks of 10 (its GEMV leaves at most 10
+    // for d <= 2560; the additions stay in split order), so that the weights
+    // above fit beside them in registers
+    constexpr int WO_FOLD = 10;
     const float *src = part + (size_t)r * 3 * d + which * d + h * hd + j;
     const int up = pair ? half : 0;
     fold4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = 0; s0 < S; s0 += FOLD_CHUNK) {
-        fold4_t v0[FOLD_CHUNK], v1[FOLD_CHUNK];
+    for (int s0 = 0; s0 < S; s0 += WO_FOLD) {
+        fold4_t v0[WO_FOLD], v1[WO_FOLD];
 #pragma unroll
-        for (int u = 0; u < FOLD_CHUNK; u++) {
+        for (int u = 0; u < WO_FOLD; u++) {
             const bool in = s0 + u < S;
             v0[u] = in ? *reinterpret_cast<const fold4_t *>(src + (size_t)(s0 + u) * stride) : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
             v1[u] = in && pair ? *reinterpret_cast<const fold4_t *>(src + up + (size_t)(s0 + u) * stride)
                                : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
 #pragma unroll
-        for (int u = 0; u < FOLD_CHUNK; u++) {
+        for (int u = 0; u < WO_FOLD; u++) {
             a0 += v0[u];
             a1 += v1[u];
         }
@@ -402,11 +412,6 @@ __global__ __launch_bounds__(ATTF_THREADS) void k_attn_few_wo(const float *__res
         if (pair) *reinterpret_cast<fold4_t *>(&qkv[which][r][j + half]) = a1;
     }
     if (n <= 0) return;  // uniform: no barrier follows for this workgroup
-    // this workgroup's Wo columns and the head's k-blocks: weights and scales
-    // requested now, used after the attention
-    const int nkb = hd / 32, c0 = (int)blockIdx.z * ncols, c1 = min(c0 + ncols, N);
-    HeadWo<WF, 1> wo;
-    wo.load(Wq, Wsc, N, h * nkb, nkb, c0, c1);
     __syncthreads();
     // scores and softmax (as k_attn_few)
     if (threadIdx.x < 64) {
