@@ -282,9 +282,10 @@ def test_few_tokens_attention_with_wo(dtype, hd, monkeypatch):
 @pytest.mark.parametrize("T", [8, 40])
 def test_forward_graph_replays_match_eager(T, monkeypatch):
     """Forwards of a shape seen before replay a captured graph (keyed by
-    batch, padded length, token count and outputs).  Different lengths with
-    the same token count reuse one graph; every replay, with eager forwards
-    and host syncs in between, equals the kernel-by-kernel run bit for bit."""
+    batch, padded length, token count, 32-key tile count and outputs).
+    Different lengths with the same token count reuse one graph; every
+    replay, with eager forwards and host syncs in between, equals the
+    kernel-by-kernel run bit for bit."""
     rng = np.random.default_rng(T)
     cfg = ch.EsmConfig(128, 512, 2, 4)
     w = ch.EsmWeights.random(cfg, seed=T, bias_std=0.02).quantize_q8()
@@ -308,6 +309,45 @@ def test_forward_graph_replays_match_eager(T, monkeypatch):
                 g, r = (g[:n - 2, :n - 2], r[:n - 2, :n - 2]) if k == "contacts" else \
                        ((g[:n, :n], r[:n, :n]) if k == "final_att" else (g[:n], r[:n]))
                 assert np.array_equal(g, r), (T, a, b, k)
+    mg.close()
+    me.close()
+
+
+@pytest.mark.parametrize("path", ["staged", "prep", "epilogue"])
+def test_forward_graph_replays_ragged_lengths(path, monkeypatch):
+    """Ragged batches of one size, longest sequence and token count whose
+    lengths differ in 32-key tiles and in 128- and 256-query blocks, one
+    after another through the graph path, each equal bit for bit to a
+    forward launched kernel by kernel: attention staging K/V itself (head
+    size 32), K/V images from the prep kernel (head size 24), and images
+    from the QKV projection's LDS GEMM epilogue (head size 64, d = 1280)."""
+    flags = ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT
+    if path == "staged":
+        cfg, L, rest = ch.EsmConfig(128, 512, 2, 4), 200, [(99, 60, 41), (96, 64, 40), (130, 35, 35), (97, 66, 37)]
+    elif path == "prep":
+        monkeypatch.setenv("CIH_ATT_IMG", "prep")
+        monkeypatch.setenv("CIH_ATT_SPLIT", "0")
+        cfg, L, rest = ch.EsmConfig(96, 384, 2, 4), 150, [(96, 64, 34), (97, 64, 33), (128, 32, 34), (65, 65, 64)]
+    else:
+        cfg, L, rest = ch.EsmConfig(1280, 5120, 2, 20), 510, [(384, 288, 208), (400, 257, 223), (256, 256, 368),
+                                                              (500, 190, 190)]
+    rng = np.random.default_rng(len(path))
+    w = ch.EsmWeights.random(cfg, seed=len(path), bias_std=0.02).quantize_q8()
+    mg = ch.GpuModel(cfg, w, max_batch=4, max_len=L, outputs=flags)
+    me = ch.GpuModel(cfg, w, max_batch=4, max_len=L, outputs=flags)
+    for lens in rest:
+        assert max(lens) <= L and sum(lens) == sum(rest[0])
+        seqs = [rand_tokens(rng, L - 2)] + [rand_tokens(rng, n - 2) for n in lens]
+        monkeypatch.setenv("CIH_FORWARD_GRAPH", "1")
+        got = mg.forward(seqs, flags)
+        monkeypatch.setenv("CIH_FORWARD_GRAPH", "0")
+        ref = me.forward(seqs, flags)
+        print(path, "lengths", [len(t) for t in seqs], flush=True)
+        for k in ("logits", "hidden", "final_att"):
+            for i, t in enumerate(seqs):
+                n = len(t)
+                g, r = (got[k][i][:n, :n], ref[k][i][:n, :n]) if k == "final_att" else (got[k][i][:n], ref[k][i][:n])
+                assert np.array_equal(g, r), (path, lens, k, i)
     mg.close()
     me.close()
 
