@@ -274,6 +274,25 @@ int cih_model_reserve(cih_model *m, int32_t max_batch, int32_t max_seq_len, uint
         if (flags & CIH_OUT_CONTACTS) good = good && ok(dalloc(ws.o_contacts, B * n * n, dl));
         if (flags & CIH_OUT_ATTN) good = good && ok(dalloc(ws.o_attn, B * L * H * S * S, dl));
         if (flags & CIH_OUT_LAYER_HIDDEN) good = good && ok(dalloc(ws.o_layer, B * L * S * d, dl));
+        // pinned staging: the largest single output, at most 64 MiB (whole
+        // rows at a time; a row is at most max(V, d, S) floats)
+        size_t need = 0;
+        if (flags & CIH_OUT_LOGITS) need = std::max(need, T * V);
+        if (flags & CIH_OUT_HIDDEN) need = std::max(need, T * d);
+        if (flags & CIH_OUT_FINAL_ATT) need = std::max(need, B * S * S);
+        if (flags & CIH_OUT_CONTACTS) need = std::max(need, B * n * n);
+        if (flags & CIH_OUT_ATTN) need = std::max(need, B * L * H * S * S);
+        if (flags & CIH_OUT_LAYER_HIDDEN) need = std::max(need, B * L * S * d);
+        void *hp = nullptr;
+        if (good && need) {
+            need = std::max(std::min(need, (size_t)16 << 20), std::max(std::max(V, d), S));
+            if (!ok(hipHostMalloc(&hp, need * sizeof(float)))) good = false;
+            else {
+                ws.host.push_back(hp);
+                ws.h_stage = (float *)hp;
+                ws.h_stage_floats = need;
+            }
+        }
     }
     if (good) {
         void *hp = nullptr;
@@ -677,36 +696,53 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         return in_full_range([&] { return forward_impl(m, tokens, lens, B, S_max, flags, out, keep_logits); });
 
     if (!dev_io) {
-        auto rows_out = [&](float *dst, const float *src, int width, int64_t bstride) -> int {
-            for (int b = 0; b < B; b++)
-                HIPCHK(hipMemcpy(dst + b * bstride, src + b * bstride, (size_t)lens[b] * width * 4,
-                                 hipMemcpyDeviceToHost));
-            return 0;
-        };
-        auto square_out = [&](float *dst, const float *src, int nb, int stride, int64_t off) -> int {
-            if (nb <= 0) return 0;
-            HIPCHK(hipMemcpy2D(dst + off, (size_t)stride * 4, src + off, (size_t)stride * 4, (size_t)nb * 4, nb,
-                               hipMemcpyDeviceToHost));
+        // Rows [0, nrows) of width floats from the device staging at src to
+        // the caller's dst (same layout), the first keep(r) floats of row r
+        // only (the rest is padding, left untouched): blocks of whole rows
+        // are copied into pinned memory, which runs at link speed (a copy
+        // into pageable memory is bounced row by row), and the kept parts of
+        // each row are copied from there on the host.
+        auto stage_rows = [&](float *dst, const float *src, size_t nrows, size_t width, auto keep) -> int {
+            const size_t per = std::max<size_t>(1, ws.h_stage_floats / width);
+            for (size_t r0 = 0; r0 < nrows; r0 += per) {
+                const size_t nr = std::min(per, nrows - r0);
+                HIPCHK(hipMemcpy(ws.h_stage, src + r0 * width, nr * width * 4, hipMemcpyDeviceToHost));
+                for (size_t r = 0; r < nr; r++) {
+                    const size_t k = keep(r0 + r);
+                    if (k) std::memcpy(dst + (r0 + r) * width, ws.h_stage + r * width, k * 4);
+                }
+            }
             return 0;
         };
         int rc = 0;
-        if (want_logits && (rc = rows_out(out->logits, t_logits, V, (int64_t)S_max * V))) return rc;
-        if (want_hidden && (rc = rows_out(out->hidden, t_hidden, d, (int64_t)S_max * d))) return rc;
-        for (int b = 0; b < B; b++) {
-            if (want_final && (rc = square_out(out->final_att, t_final, lens[b], S_max, (int64_t)b * SS))) return rc;
-            if (want_contacts &&
-                (rc = square_out(out->contacts, t_contacts, lens[b] - 2, n_max, (int64_t)b * n_max * n_max)))
-                return rc;
-            for (int l = 0; l < L; l++) {
-                if (want_layer)
-                    HIPCHK(hipMemcpy(out->layer_hidden + ((int64_t)b * L + l) * S_max * d,
-                                     t_layer + ((int64_t)b * L + l) * S_max * d, (size_t)lens[b] * d * 4,
-                                     hipMemcpyDeviceToHost));
-                for (int h = 0; want_attn && h < H; h++)
-                    if ((rc = square_out(out->attn, t_attn, lens[b], S_max, (((int64_t)b * L + l) * H + h) * SS)))
-                        return rc;
+        for (int b = 0; b < B && !rc; b++) {
+            const size_t nb = lens[b];
+            auto all_of = [](size_t w) { return [w](size_t) { return w; }; };
+            if (want_logits)
+                rc = stage_rows(out->logits + (int64_t)b * S_max * V, t_logits + (int64_t)b * S_max * V, nb, V,
+                                all_of(V));
+            if (!rc && want_hidden)
+                rc = stage_rows(out->hidden + (int64_t)b * S_max * d, t_hidden + (int64_t)b * S_max * d, nb, d,
+                                all_of(d));
+            if (!rc && want_final)
+                rc = stage_rows(out->final_att + b * SS, t_final + b * SS, nb, S_max, all_of(nb));
+            if (!rc && want_contacts && nb > 2) {
+                const size_t nr = nb - 2, nn = (size_t)n_max * n_max;
+                rc = stage_rows(out->contacts + b * nn, t_contacts + b * nn, nr, n_max, all_of(nr));
+            }
+            // a sequence's per-layer rows and maps are contiguous: [L][S_max][d], [L][H][S_max][S_max]
+            if (!rc && want_layer) {
+                const int64_t o = (int64_t)b * L * S_max * d;
+                rc = stage_rows(out->layer_hidden + o, t_layer + o, (size_t)L * S_max, d,
+                                [&](size_t r) { return r % S_max < nb ? (size_t)d : 0; });
+            }
+            if (!rc && want_attn) {
+                const int64_t o = (int64_t)b * L * H * SS;
+                rc = stage_rows(out->attn + o, t_attn + o, (size_t)L * H * S_max, S_max,
+                                [&](size_t r) { return r % S_max < nb ? nb : 0; });
             }
         }
+        if (rc) return rc;
     }
     profile_collect(m);
     return CIH_OK;

@@ -64,6 +64,10 @@ struct Workspace {
     // device staging of outputs for host-pointer calls (padded layouts)
     float *o_logits = nullptr, *o_hidden = nullptr, *o_final = nullptr, *o_contacts = nullptr, *o_attn = nullptr,
           *o_layer = nullptr;
+    // pinned host staging of those outputs on their way to the caller's
+    // (pageable) buffers: blocks of whole rows, h_stage_floats at a time
+    float *h_stage = nullptr;
+    size_t h_stage_floats = 0;
     std::vector<void *> dev, host;
     // captured forwards, by shape
     std::vector<std::pair<FwdGraphKey, hipGraphExec_t>> graphs;

@@ -13,6 +13,8 @@ Tolerances (FP32 accumulate throughout):
                 the argmax provably cannot change); at least 90% of the
                 positions must be compared, and the count is printed
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -350,6 +352,51 @@ def test_forward_graph_replays_ragged_lengths(path, monkeypatch):
                 assert np.array_equal(g, r), (path, lens, k, i)
     mg.close()
     me.close()
+
+
+def test_host_outputs_leave_padding_untouched():
+    """Host-pointer outputs of a ragged batch (every kind) are written inside
+    each sequence's rows, columns and maps only: buffers filled with a
+    sentinel keep it in the padding, and hold the same values as a forward
+    into zeroed buffers everywhere else (the copies run through pinned
+    staging in whole padded rows, of which only the kept part is copied)."""
+    from codon_hip import _lib as C
+    rng = np.random.default_rng(12)
+    cfg = ch.EsmConfig(64, 256, 2, 4)
+    w = ch.EsmWeights.random(cfg, seed=12, bias_std=0.02).quantize_q8()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    flags = (ch.OUT_LOGITS | ch.OUT_HIDDEN | ch.OUT_FINAL_ATT | ch.OUT_CONTACTS | ch.OUT_ATTN |
+             ch.OUT_LAYER_HIDDEN)
+    seqs = [rand_tokens(rng, n) for n in (28, 59, 3)]
+    m = ch.GpuModel(cfg, w, contact_head=(cw, 0.3), max_batch=3, max_len=61, outputs=flags)
+    ref = m.forward(seqs, flags)
+    B, S = len(seqs), max(len(t) for t in seqs)
+    lens = np.array([len(t) for t in seqs], np.int32)
+    toks = np.zeros((B, S), np.int32)
+    for b, t in enumerate(seqs):
+        toks[b, :len(t)] = t
+    d, V, L, H, n = cfg.dim, cfg.vocab_size, cfg.n_layers, cfg.n_heads, S - 2
+    SENT = np.float32(12345.0)
+    got = {"logits": (B, S, V), "hidden": (B, S, d), "final_att": (B, S, S), "contacts": (B, n, n),
+           "attn": (B, L, H, S, S), "layer_hidden": (B, L, S, d)}
+    got = {k: np.full(shape, SENT, np.float32) for k, shape in got.items()}
+    o = C.Outputs()
+    for k, a in got.items():
+        setattr(o, k, a.ctypes.data)
+    C.check(C.lib().cih_forward(m._h, toks.ctypes.data, lens.ctypes.data, B, S, flags, ctypes.byref(o)))
+    m.close()
+    print("sentinel-filled host outputs: written regions equal, padding untouched", flush=True)
+    for b, t in enumerate(seqs):
+        nb, nc = len(t), max(len(t) - 2, 0)
+        inside = {"logits": (np.s_[b, :nb], np.s_[b, nb:]), "hidden": (np.s_[b, :nb], np.s_[b, nb:]),
+                  "layer_hidden": (np.s_[b, :, :nb], np.s_[b, :, nb:])}
+        for k, (ins, pad) in inside.items():
+            assert np.array_equal(got[k][ins], ref[k][ins]), (k, b)
+            assert np.all(got[k][pad] == SENT), (k, b)
+        for k, m_ in (("final_att", nb), ("contacts", nc), ("attn", nb)):
+            a, r = got[k][b], ref[k][b]
+            assert np.array_equal(a[..., :m_, :m_], r[..., :m_, :m_]), (k, b)
+            assert np.all(a[..., m_:, :] == SENT) and np.all(a[..., :m_, m_:] == SENT), (k, b)
 
 
 def test_tied_embedding_decoder():
