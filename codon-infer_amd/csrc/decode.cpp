@@ -24,6 +24,7 @@ struct cih_decoder {
     float *x = nullptr, *xb = nullptr, *qkv = nullptr, *ao = nullptr, *h = nullptr, *logits = nullptr;
     int *d_tokens = nullptr, *d_rows = nullptr, *d_cu = nullptr, *d_lens = nullptr;
     int *h_meta = nullptr;  // pinned: tokens[max_rows] | rows[max_rows][2] | status word read back
+    float *h_logits = nullptr;  // pinned: [max_rows][V] logits read back (then copied to pageable buffers)
     int *d_flag = nullptr;  // device status word of a step (FLAG_* bits)
     cih::PartialBuf part;
     std::vector<int> filled;  // positions written per slot (0..filled-1 valid)
@@ -43,6 +44,7 @@ void destroy(cih_decoder *dc) {
     for (auto &g : dc->graphs) hipGraphExecDestroy(g.second);
     free_list(dc->allocs);
     if (dc->h_meta) hipHostFree(dc->h_meta);
+    if (dc->h_logits) hipHostFree(dc->h_logits);
     delete dc;
 }
 
@@ -390,7 +392,8 @@ int cih_decoder_create(cih_model *m, int32_t n_slots, int32_t max_len, int32_t m
                 dalloc(dc->d_flag, 1, al) == hipSuccess;
     dc->part.floats = model_part_floats(m);
     good = good && dalloc(dc->part.part, dc->part.floats, al) == hipSuccess &&
-           hipHostMalloc((void **)&dc->h_meta, (3 * R + 1) * sizeof(int)) == hipSuccess;
+           hipHostMalloc((void **)&dc->h_meta, (3 * R + 1) * sizeof(int)) == hipSuccess &&
+           hipHostMalloc((void **)&dc->h_logits, R * V * sizeof(float)) == hipSuccess;
     if (!good) {
         destroy(dc);
         return set_error(CIH_ERR_HIP, "decoder allocation failed (%zu MiB of KV cache)", 2 * cache * 4 >> 20);
@@ -429,10 +432,10 @@ int cih_decode(cih_decoder *dc, const int32_t *slots, const int32_t *tokens, con
     if (!dc || !slots || !tokens || !pos) return set_error(CIH_ERR_ARG, "null argument");
     if (int rc = stage_rows(dc, slots, tokens, pos, n)) return rc;
     if (int rc = run_rows(dc, n)) return rc;
-    if (logits)
-        HIPCHK(hipMemcpyAsync(logits, dc->logits, (size_t)n * dc->m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
-                              dc->m->stream));
+    const size_t lb = (size_t)n * dc->m->cfg.vocab_size * 4;
+    if (logits) HIPCHK(hipMemcpyAsync(dc->h_logits, dc->logits, lb, hipMemcpyDeviceToHost, dc->m->stream));
     HIPCHK(hipStreamSynchronize(dc->m->stream));
+    if (logits) std::memcpy(logits, dc->h_logits, lb);
     profile_collect(dc->m);
     return CIH_OK;
 }
@@ -473,9 +476,12 @@ int cih_generate(cih_decoder *dc, int32_t n, const int32_t *slots, const int32_t
             for (int j = 0; j < k; j++) ps[j] = p0 + j;
             if (int rc = stage_rows(dc, sl.data(), tk.data(), ps.data(), k)) return rc;
             if (int rc = run_rows(dc, k)) return rc;
-            if (p0 + k == pos[i])
-                HIPCHK(hipMemcpyAsync(&lg[(size_t)i * V], dc->logits + (size_t)(k - 1) * V, V * 4,
-                                      hipMemcpyDeviceToHost, dc->m->stream));
+            if (p0 + k == pos[i]) {
+                HIPCHK(hipMemcpyAsync(dc->h_logits, dc->logits + (size_t)(k - 1) * V, V * 4, hipMemcpyDeviceToHost,
+                                      dc->m->stream));
+                HIPCHK(hipStreamSynchronize(dc->m->stream));
+                std::memcpy(&lg[(size_t)i * V], dc->h_logits, V * 4);
+            }
         }
     }
     HIPCHK(hipStreamSynchronize(dc->m->stream));
@@ -506,10 +512,9 @@ int cih_generate(cih_decoder *dc, int32_t n, const int32_t *slots, const int32_t
             const int k = (int)std::min<size_t>(dc->max_rows, idx.size() - j0);
             if (int rc = stage_rows(dc, &sl[j0], &tk[j0], &ps[j0], k)) return rc;
             if (int rc = run_rows(dc, k)) return rc;
-            for (int j = 0; j < k; j++)
-                HIPCHK(hipMemcpyAsync(&lg[(size_t)idx[j0 + j] * V], dc->logits + (size_t)j * V, V * 4,
-                                      hipMemcpyDeviceToHost, dc->m->stream));
+            HIPCHK(hipMemcpyAsync(dc->h_logits, dc->logits, (size_t)k * V * 4, hipMemcpyDeviceToHost, dc->m->stream));
             HIPCHK(hipStreamSynchronize(dc->m->stream));
+            for (int j = 0; j < k; j++) std::memcpy(&lg[(size_t)idx[j0 + j] * V], dc->h_logits + (size_t)j * V, V * 4);
             profile_collect(dc->m);
         }
     }
