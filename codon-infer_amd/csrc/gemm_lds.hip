@@ -296,6 +296,15 @@ __device__ __forceinline__ void qkv_epilogue(f32x16 (&acc)[RT][CT], unsigned cha
     }
 }
 
+// a + b computed where it is written (inline asm): per-lane LDS offsets stay
+// loop-invariant and the stage's base is added in the block, instead of an
+// address per (stage, operand) being kept live across the k loop
+__device__ __forceinline__ unsigned add_here(unsigned a, unsigned b) {
+    unsigned r;
+    asm volatile("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(b), "v"(a));
+    return r;
+}
+
 // WQ: 0 = W from the f16 copy (W.q16); WF_Q8 / WF_Q4 = W from its quants
 // (W.q, a model loaded without the f16 copy), turned into f16 on the LDS ->
 // register path: v_perm puts each byte (Q8_0: + 128; Q4_0: the lane's
@@ -347,20 +356,27 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     // [j * 1024, +1024) of its region, lane l the 16 bytes at l * 16: LDS
     // chunk p = 64 j + l holds the (row, chunk) whose swizzled position is p.
     // Rows past M and columns past N read the last row / column (never stored).
-    const unsigned short *srcA[NA];
+    // Sources as 32-bit byte offsets from wave-uniform bases (the tile's
+    // first row of X, its first column of W and of the scales; the block
+    // advances the bases in scalar registers): the loads take the scalar base
+    // + 32-bit offset form, and no 64-bit address lives in vector registers.
+    const unsigned char *const xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KB * 128;
+    const unsigned char *const wbase = WB + (size_t)n0 * BPC;
+    const float *const sbase = Wsc + n0;
+    unsigned offA[NA];
     int dstA[NA];
 #pragma unroll
     for (int i = 0; i < NA; i++) {
         const int j = i * NW + wave < T::LA ? i * NW + wave : wave;
         const int p = j * 64 + lane;
         const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
-        srcA[i] = X + (size_t)min(m0 + row, M - 1) * KB * 64 + chunk * 8;
+        offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KB * 128 + chunk * 16);
         dstA[i] = j * 1024;
     }
     // W: chunk c of column n at c ^ ((n >> 2) & 3) (f16 copy, 4 chunks), at
     // c ^ ((n >> 3) & 1) (Q8_0, 2 chunks); Q4_0: one chunk.  Chunks past the
     // tile's columns (Q4_0 at 160 columns) fill padding nobody reads.
-    const unsigned char *srcB[NB];
+    unsigned offB[NB];
     int dstB[NB];
 #pragma unroll
     for (int i = 0; i < NB; i++) {
@@ -377,10 +393,10 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             col = min(p, BN - 1);
             chunk = 0;
         }
-        srcB[i] = WB + (size_t)min(n0 + col, N - 1) * BPC + chunk * 16;
+        offB[i] = (unsigned)((min(n0 + col, N - 1) - n0) * BPC + chunk * 16);
         dstB[i] = SA + j * 1024;
     }
-    const float *srcS = Wsc + min(n0 + wave * SL + min(lane, SL - 1), N - 1);
+    const unsigned offS = (unsigned)(min(n0 + wave * SL + min(lane, SL - 1), N - 1) - n0) * 4;
     // The tile's bias values go to LDS before the k loop (copied by the load
     // unit, ordered by the loop's first wait and barrier): the epilogue reads
     // them from LDS, so its stores follow no pending global load (a load
@@ -397,17 +413,17 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
 
     auto request = [&](int kb, int stg) __attribute__((always_inline)) {
         unsigned char *base = lds + stg * STAGE;
+        const unsigned char *xb = xbase + (size_t)kb * 128, *wbk = wbase + (size_t)kb * N * BPC;
+        const unsigned char *sbk = reinterpret_cast<const unsigned char *>(sbase + (size_t)kb * N);
 #pragma unroll
         for (int i = 0; i < NA; i++)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcA[i] + (size_t)kb * 64), (lds_ptr_t *)(base + dstA[i]),
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(xb + offA[i]), (lds_ptr_t *)(base + dstA[i]), 16, 0, 0);
 #pragma unroll
         for (int i = 0; i < NB; i++)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcB[i] + (size_t)kb * N * BPC),
-                                             (lds_ptr_t *)(base + dstB[i]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(wbk + offB[i]), (lds_ptr_t *)(base + dstB[i]), 16, 0, 0);
         if (lane < SL)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(srcS + (size_t)kb * N),
-                                             (lds_ptr_t *)(base + SA + SB + wave * SL * 4), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(sbk + offS), (lds_ptr_t *)(base + SA + SB + wave * SL * 4),
+                                             4, 0, 0);
     };
 
     // Schedules with the same arithmetic (per 32 x 32 tile: tmp = both limbs
@@ -474,8 +490,16 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         }
         t = __builtin_amdgcn_mfma_f32_32x32x16_f16(x, w, cc, 0, 0, 0);
     };
+    // LDS read addresses: per-lane parts (loop-invariant) plus the stage's
+    // base, added in the block (add_here), so the loop unrolled over the
+    // three stages keeps one set of per-lane parts instead of one per stage
+    const unsigned lds0 = (unsigned)(size_t)lds;
+    auto at = [&](unsigned lane_part, int uniform) __attribute__((always_inline)) {
+        return lds + (add_here(lane_part, lds0 + uniform) - lds0);
+    };
     auto compute = [&](int stg) __attribute__((always_inline)) {
         const unsigned char *base = lds + stg * STAGE;
+        const int boff = stg * STAGE + SA;  // the stage's B operands
         f16x8 a[2][2][RT];  // [k-half][limb][row tile]
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
@@ -484,7 +508,8 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
                     const int row = (wm * RT + r) * 32 + li, chunk = l * 4 + hh * 2 + kh;
-                    a[kh][l][r] = *reinterpret_cast<const f16x8 *>(base + row * 128 + ((chunk ^ swA) << 4));
+                    a[kh][l][r] = *reinterpret_cast<const f16x8 *>(
+                        at((unsigned)(row * 128 + ((chunk ^ swA) << 4)), stg * STAGE));
                 }
         if constexpr (RT >= 2) {
 #pragma unroll
@@ -527,9 +552,12 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             // ahead of them.  The same additions in the same order.  The order
             // is written out and fenced (sched_barrier), and the pair's
             // operands are read once the triple's first k-half is issued.
+            // B: one address per k-half (column tile c is 2048 bytes further)
+            const unsigned char *bk[2] = {at((unsigned)((wn * CT * 32 + li) * 64 + (((hh * 2) ^ swB) << 4)), boff),
+                                          at((unsigned)((wn * CT * 32 + li) * 64 + (((hh * 2 + 1) ^ swB) << 4)),
+                                             boff)};
             auto rd_b = [&](int c, int kh) __attribute__((always_inline)) {
-                const int col = (wn * CT + c) * 32 + li;
-                return *reinterpret_cast<const f16x8 *>(base + SA + col * 64 + (((hh * 2 + kh) ^ swB) << 4));
+                return *reinterpret_cast<const f16x8 *>(bk[kh] + c * 2048);
             };
             auto fence = [&]() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
             auto scale = [&](int c, float d, int q0, int q1) __attribute__((always_inline)) {
@@ -539,8 +567,9 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             const f16x8 b00 = rd_b(0, 0), b10 = rd_b(1, 0), b20 = rd_b(2, 0);
             const f16x8 b01 = rd_b(0, 1), b11 = rd_b(1, 1), b21 = rd_b(2, 1);
             float dcur[CT];
+            const unsigned char *sc = at((unsigned)((wn * CT * 32 + li) * 4), stg * STAGE + SA + SB);
 #pragma unroll
-            for (int c = 0; c < CT; c++) dcur[c] = scale_of(base, c);
+            for (int c = 0; c < CT; c++) dcur[c] = *reinterpret_cast<const float *>(sc + c * 128);
             fence();
             scale(3, dcar[3], 0, 16);
             scale(4, dcar[4], 0, 16);
