@@ -24,9 +24,12 @@
 //     at chunk c ^ ((r >> 1) & 7), chunk c of W column n at c ^ ((n >> 2) & 3),
 //     so the 16 lanes of each MFMA operand read hit 16 distinct bank groups.
 //
-// Workgroup: (BM/64) x (BN/64) waves, each owning a 64 x 64 output tile
-// (2 x 2 MFMA tiles of 32 x 32); 128 x 128 (4 waves, two workgroups per CU)
-// or 128 x 256 (8 waves, one per CU).
+// Workgroup tiles (BM x BN, waves x wave tile): 128 x 320 (8 x 32 x 160) and
+// 128 x 256 (8 x 64 x 64), one workgroup per CU; 128 x 160 (4 x 32 x 160);
+// 128 x 128 (4 x 64 x 64, two per CU); and, for problems too small to fill
+// the device with those, 64 x 128 (4 x 32 x 64, three per CU) and 64 x 64
+// (4 x 32 x 32, four per CU), read from the f16 copy only.  Every tile sums the same products in the same
+// order, so the tile never changes a result.
 #include <stdlib.h>
 #include <string.h>
 
@@ -787,6 +790,10 @@ int gemm_sched() {
     return e ? atoi(e) : 1;
 }
 
+// The small tiles (RT == 1, CT <= 2: 64 x 64 and 64 x 128) read the f16
+// copy only.
+template <int RT, int CT> constexpr bool copy_only() { return RT == 1 && CT <= 2; }
+
 template <int EPI, int RT, int CT, int WM, int WN>
 hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
                     const QkvOut &qo) {
@@ -794,7 +801,11 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
     const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
     const bool quants = !W.q16;
-    if (quants && W.fmt == WF_Q8)
+    if constexpr (copy_only<RT, CT>()) {
+        if (quants) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
+                           reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
+    } else if (quants && W.fmt == WF_Q8)
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, WF_Q8>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
     else if (quants && W.fmt == WF_Q4)
@@ -810,70 +821,111 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     return hipGetLastError();
 }
 
-// Split-K form on 128 x 128 tiles: grid (tiles, S), raw partial sums into part.
-hipError_t launch_split(const DevMatrix &W, const void *X, int M, float *part, int S, int kps, hipStream_t st) {
-    using T = LdsTile<2, 2, 2, 2>;
+// Split-K form: grid (tiles, S), raw partial sums into part.  128 x 128 tiles
+// (4 waves) for every weight form; 64 x 128 and 64 x 64 from the f16 copy.
+template <int RT, int CT, int WM, int WN>
+hipError_t launch_split_t(const DevMatrix &W, const void *X, int M, float *part, int S, int kps, hipStream_t st) {
+    using T = LdsTile<RT, CT, WM, WN>;
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
     const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
     const dim3 grid(tiles, S), block(T::THREADS);
-    if (!W.q16 && W.fmt == WF_Q8)
-        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, 2, 2, 2, 2, WF_Q8, true>), grid, block, 0, st, Xh,
+    if constexpr (copy_only<RT, CT>()) {
+        if (!W.q16) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true>), grid, block, 0, st, Xh,
+                           reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
+                           QkvOut(), kps);
+    } else if (!W.q16 && W.fmt == WF_Q8)
+        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, WF_Q8, true>), grid, block, 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, nullptr, part, W.N, M, W.N, W.K, QkvOut(),
                            kps);
     else if (!W.q16)
-        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, 2, 2, 2, 2, WF_Q4, true>), grid, block, 0, st, Xh,
+        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, WF_Q4, true>), grid, block, 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, nullptr, part, W.N, M, W.N, W.K, QkvOut(),
                            kps);
     else
-        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, 2, 2, 2, 2, 0, true>), grid, block, 0, st, Xh,
+        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true>), grid, block, 0, st, Xh,
                            reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
                            QkvOut(), kps);
     return hipGetLastError();
 }
 
-// Tile choice by a model of the time the rounds of workgroups take on the
-// device's CUs.  Candidates, in order of preference (fewest operand bytes per
-// output first): 128 x 320 and 128 x 256 (8 waves, one workgroup per CU),
-// 128 x 160 and 128 x 128 (4 waves, two per CU).  A full round costs the
-// tile area times the workgroups sharing a CU; a last round that leaves a
-// 4-wave workgroup alone on its CU runs it at about 1/1.4 of a CU's rate.
-// At M = 8192 this picks 128 x 320 for every ESM-2 650M projection (QKV:
-// 3 rounds instead of 3.75; N = 1280: one round instead of 1.25); at
-// M = 2552 (a ragged 8-sequence batch) 128 x 320 for QKV, 128 x 256 for FC1,
-// 128 x 128 for Wo and FC2, as measured.
-int tile_choice(int M, int N) {
+hipError_t launch_split(const DevMatrix &W, const void *X, int M, float *part, int S, int kps, int tile,
+                        hipStream_t st) {
+    if (tile == LDS_TILE_64x64) return launch_split_t<1, 1, 2, 2>(W, X, M, part, S, kps, st);
+    if (tile == LDS_TILE_64x128) return launch_split_t<1, 2, 2, 2>(W, X, M, part, S, kps, st);
+    return launch_split_t<2, 2, 2, 2>(W, X, M, part, S, kps, st);
+}
+
+// Tile choice for problems that fill the device with 128-row tiles, by a
+// model of the time the rounds of workgroups take on the device's CUs.
+// Candidates, in order of preference (fewest operand bytes per output
+// first): 128 x 320 and 128 x 256 (8 waves, one workgroup per CU), 128 x 160
+// (4 waves; two per CU with 1-byte quants, one with the f16 copy, whose
+// three stages take 81 KiB: then it is left out) and 128 x 128 (4 waves,
+// two per CU).  A full round costs the tile area times the workgroups
+// sharing a CU; a last round that leaves a 4-wave workgroup alone on its CU
+// runs it at about 1/1.4 of a CU's rate.  At M = 8192 this picks 128 x 320
+// for every ESM-2 650M projection (QKV: 3 rounds instead of 3.75; N = 1280:
+// one round instead of 1.25).
+int tile_choice(int M, int N, bool copy) {
     const int cus = device_cus();
     const long mt = (M + 127) / 128;
     struct Cand {
-        int bn, per_cu;
+        int tile, bn, per_cu;
     };
-    const Cand cand[4] = {{320, 1}, {256, 1}, {160, 2}, {128, 2}};
-    int best = 128;
+    const Cand cand[4] = {{LDS_TILE_128x320, 320, 1}, {LDS_TILE_128x256, 256, 1}, {LDS_TILE_128x160, 160, 2},
+                          {LDS_TILE_128x128, 128, 2}};
+    int best = LDS_TILE_128x128;
     double best_cost = 0;
     for (const Cand &c : cand) {
+        if (copy && c.bn == 160) continue;
         const long tiles = mt * ((N + c.bn - 1) / c.bn), slots = (long)c.per_cu * cus;
         const double area = 128.0 * c.bn;
         const long full = tiles / slots, rest = tiles % slots;
         double cost = full * area * c.per_cu;
         if (rest) cost += (c.per_cu == 2 && rest <= cus) ? 1.4 * area : area * c.per_cu;
         if (best_cost == 0 || cost < best_cost) {
-            best = c.bn;
+            best = c.tile;
             best_cost = cost;
         }
     }
     return best;
 }
 
+// CIH_GEMM_TILE_N (CIH_GEMM_TILE_N_GELU for the FC1 + GELU GEMM): 320, 256,
+// 160, 128 (128-row tiles of that width), 64x128 or 64 (64 x 64); 0 when
+// unset.
+int tile_env(int epi) {
+    const char *e = getenv("CIH_GEMM_TILE_N");
+    if (const char *eg = getenv("CIH_GEMM_TILE_N_GELU"); eg && epi == EPI_GELU_H2) e = eg;
+    if (!e) return 0;
+    if (!strcmp(e, "64x128")) return LDS_TILE_64x128;
+    switch (atoi(e)) {
+    case 320: return LDS_TILE_128x320;
+    case 256: return LDS_TILE_128x256;
+    case 160: return LDS_TILE_128x160;
+    case 64: return LDS_TILE_64x64;
+    default: return LDS_TILE_128x128;
+    }
+}
+
+// tile 0: CIH_GEMM_TILE_N, else the round model's choice.  The small tiles
+// and 128 x 160 serve the plain epilogues only (in the QKV epilogue a
+// workgroup's columns must hold whole heads); a small tile without the f16
+// copy becomes 128 x 128.
 template <int EPI>
 hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
-                      const QkvOut &qo) {
-    const char *e = getenv("CIH_GEMM_TILE_N");
-    if (const char *eg = getenv("CIH_GEMM_TILE_N_GELU"); eg && EPI == EPI_GELU_H2) e = eg;
-    const int bn = e ? atoi(e) : tile_choice(M, W.N);
-    if (bn == 320) return launch_t<EPI, 1, 5, 4, 2>(W, X, bias, Y, ldy, M, st, qo);
-    if (bn == 256) return launch_t<EPI, 2, 2, 2, 4>(W, X, bias, Y, ldy, M, st, qo);
-    if constexpr (EPI < EPI_QKV16) {  // 160-column tiles would split heads between workgroups
-        if (bn == 160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st, qo);
+                      const QkvOut &qo, int tile) {
+    if (!tile) tile = tile_env(EPI);
+    if (!tile) tile = tile_choice(M, W.N, W.q16 != nullptr);
+    if (tile == LDS_TILE_128x320) return launch_t<EPI, 1, 5, 4, 2>(W, X, bias, Y, ldy, M, st, qo);
+    if (tile == LDS_TILE_128x256) return launch_t<EPI, 2, 2, 2, 4>(W, X, bias, Y, ldy, M, st, qo);
+    if constexpr (EPI < EPI_QKV16) {
+        if (tile == LDS_TILE_128x160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st, qo);
+        if (W.q16) {
+            if (tile == LDS_TILE_64x128) return launch_t<EPI, 1, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+            if (tile == LDS_TILE_64x64) return launch_t<EPI, 1, 1, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+        }
     }
     return launch_t<EPI, 2, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
 }
@@ -931,7 +983,90 @@ hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const
     const int kps = (KB + S - 1) / S;
     S = (KB + kps - 1) / kps;
     *splits = S;
-    return launch_split(W, X, M, pb.part, S, kps, st);
+    return launch_split(W, X, M, pb.part, S, kps, LDS_TILE_128x128, st);
+}
+
+// Routing of the problems that do not fill the device with 128-row tiles,
+// from a sweep of every tile and split over the ESM-2 8M-3B projections at
+// 256-8192 tokens on MI355X (256 CUs; the thresholds scale with the CU
+// count).  One 4-wave workgroup per CU exposes the per-block barrier and
+// operand-read latency to its lone wave per SIMD; smaller tiles put three or
+// four workgroups on each CU and leave fewer CUs idle in the last round:
+//   * residual projections with K >= 2560 (80 blocks) whose caller adds
+//     splits: up to 100 tiles of 128 x 128, 64 x 128 tiles in 3 k-splits;
+//     fewer 128 x 128 tiles than CUs, those in min(2 CUs / tiles, 3) splits;
+//     up to 4/3 CUs of them, 3 splits; else the round model's tile unsplit;
+//   * up to 5 CUs tiles of 64 x 64: that tile, residual projections split
+//     into min(2 CUs / tiles, 6, blocks / 4) (5 -> 4);
+//   * else the round model's large tile (unchanged at the 650M 8192-token
+//     shapes).
+// ESM-2 35M at 2552 tokens (8 ragged sequences), against the register-staged
+// kernel and 128 x 160 before: QKV 17.3 -> 14.4, Wo 8.9 -> 8.2, FC1 24.8 ->
+// 20.1, FC2 20.8 -> 21.3 us, and Wo and FC2 no longer leave 3 splits each to
+// the LayerNorm after them.
+bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_floats, LdsPlan &p) {
+    p = LdsPlan();
+    if (a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || !W.q16 || W.K % 32 || W.K <= 0 || W.N <= 0) return false;
+    if (epi != EPI_NONE && epi != EPI_RESIDUAL && epi != EPI_GELU_H2) return false;
+    if (M < 256) return false;  // below the sweep: the register-staged kernel and its splits
+    const char *le = getenv("CIH_GEMM_LDS"), *pe = getenv("CIH_GEMM_PLAN"), *ke = getenv("CIH_SPLITK");
+    if (le || (pe && !strcmp(pe, "0"))) return false;  // CIH_GEMM_LDS=0 / force: the routes without the plan
+    const long cus = device_cus();
+    const long t64 = (long)((M + 63) / 64) * ((W.N + 63) / 64), t128 = (long)((M + 127) / 128) * ((W.N + 127) / 128);
+    const int KB = W.K / 32;
+    const bool can_split = epi == EPI_RESIDUAL && part_floats > 0 && !(ke && !strcmp(ke, "0"));
+    int tile, S = 1;
+    if (const int forced = tile_env(epi)) {
+        tile = forced;
+    } else if (can_split && KB >= 80) {
+        if (t128 * 256 <= 100 * cus) {
+            tile = LDS_TILE_64x128;
+            S = 3;
+        } else if (t128 < cus) {
+            tile = LDS_TILE_128x128;
+            S = (int)std::min<long>(2 * cus / t128, 3);
+        } else if (t128 * 3 <= 4 * cus) {
+            tile = LDS_TILE_128x128;
+            S = 3;
+        } else {
+            tile = tile_choice(M, W.N, true);
+        }
+    } else if (t64 <= 5 * cus) {
+        tile = LDS_TILE_64x64;
+        if (can_split) {
+            S = (int)std::max<long>(1, std::min<long>({2 * cus / t64, 6, KB / 4}));
+            if (S == 5) S = 4;
+        }
+    } else {
+        tile = tile_choice(M, W.N, true);
+    }
+    while (S > 1 && (size_t)S * M * W.N > part_floats) S--;
+    if (S > 1) {
+        p.kps = (KB + S - 1) / S;
+        S = (KB + p.kps - 1) / p.kps;
+    }
+    p.tile = tile;
+    p.splits = S;
+    return true;
+}
+
+hipError_t launch_gemm_lds_plan(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
+                                const LdsPlan &p, const PartialBuf *pb, hipStream_t st) {
+    if ((W.fmt != WF_Q8 && W.fmt != WF_Q4) || !W.q16 || W.K % 32 || W.K <= 0 || M <= 0 || W.N <= 0 || !p.tile)
+        return hipErrorInvalidValue;
+    if (p.splits > 1) {
+        if (epi != EPI_RESIDUAL || !pb || !pb->part || p.kps <= 0 || (size_t)p.splits * M * W.N > pb->floats ||
+            (p.splits - 1) * p.kps >= W.K / 32)
+            return hipErrorInvalidValue;
+        return launch_split(W, X, M, pb->part, p.splits, p.kps, p.tile, st);
+    }
+    if (epi == EPI_GELU_H2 && W.N % 32) return hipErrorInvalidValue;
+    switch (epi) {
+    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile);
+    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile);
+    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
@@ -945,12 +1080,12 @@ hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias,
             return hipErrorInvalidValue;
     }
     switch (epi) {
-    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st, QkvOut());
-    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st, QkvOut());
-    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st, QkvOut());
-    case EPI_QKV16: return launch_epi<EPI_QKV16>(W, X, bias, Y, ldy, M, st, *qo);
-    case EPI_QKV32: return launch_epi<EPI_QKV32>(W, X, bias, Y, ldy, M, st, *qo);
-    case EPI_QKV64: return launch_epi<EPI_QKV64>(W, X, bias, Y, ldy, M, st, *qo);
+    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st, QkvOut(), 0);
+    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st, QkvOut(), 0);
+    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st, QkvOut(), 0);
+    case EPI_QKV16: return launch_epi<EPI_QKV16>(W, X, bias, Y, ldy, M, st, *qo, 0);
+    case EPI_QKV32: return launch_epi<EPI_QKV32>(W, X, bias, Y, ldy, M, st, *qo, 0);
+    case EPI_QKV64: return launch_epi<EPI_QKV64>(W, X, bias, Y, ldy, M, st, *qo, 0);
     default: return hipErrorInvalidValue;
     }
 }

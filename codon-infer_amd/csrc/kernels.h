@@ -250,6 +250,20 @@ hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias,
 bool gemm_lds_split_applies(const DevMatrix &W, int a_fmt, int M, int epi);
 hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const PartialBuf &pb, int *splits,
                                  hipStream_t st);
+// Workgroup tiles of the LDS-staged GEMM (BM x BN).
+enum LdsTileId { LDS_TILE_128x128 = 1, LDS_TILE_128x160, LDS_TILE_128x256, LDS_TILE_128x320, LDS_TILE_64x128, LDS_TILE_64x64 };
+// Tile and k-splits for an f16-limb GEMM with the f16 copy from 256 rows on
+// (false: not such a GEMM, or CIH_GEMM_LDS / CIH_GEMM_PLAN=0 set).  Splits
+// only for EPI_RESIDUAL with room for them (part_floats > 0; the caller
+// adds them, as launch_gemm_lds_split's).
+struct LdsPlan {
+    int tile = 0, splits = 1, kps = 0;
+};
+bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_floats, LdsPlan &p);
+// The planned GEMM: with p.splits > 1 the raw partial sums [p.splits][M][N]
+// into pb->part (bias and epilogue left to the caller), else Y = epi(...).
+hipError_t launch_gemm_lds_plan(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
+                                const LdsPlan &p, const PartialBuf *pb, hipStream_t st);
 // W.q16 from W.q (quantized W, k-block-major), on stream st.
 hipError_t launch_expand_f16(const DevMatrix &W, unsigned short *q16, hipStream_t st);
 // The pair copy (p16, psc) of an FP32 matrix W, on stream st.

@@ -187,6 +187,21 @@ def test_forward_preset_archs(arch, dtype, B, lo, hi):
     check_batch(cfg, w, seqs, flags, contact=cfg.contact_head_weights())
 
 
+@pytest.mark.parametrize("lens", [(300, 220), (650, 650, 650, 650)])
+def test_planned_splits_vs_oracle(lens):
+    """ESM-2 150M projection widths (d = 640, FC2 K = 2560) over two layers,
+    Q8_0: the planned k-splits of the residual projections, which leave their
+    partial sums to the LayerNorm after them.  524 tokens: Wo on 64 x 64
+    tiles in 4 splits, FC2 on 64 x 128 tiles in 3; 2608 tokens: FC2 on
+    128 x 128 tiles in 3."""
+    rng = np.random.default_rng(21)
+    cfg = ch.EsmConfig(640, 2560, 2, 20)
+    w = ch.EsmWeights.random(cfg, seed=21, bias_std=0.02).quantize_q8()
+    seqs = [rand_tokens(rng, n) for n in lens]
+    print(f"planned splits, {sum(lens) + 2 * len(lens)} tokens", flush=True)
+    check_batch(cfg, w, seqs, ch.OUT_LOGITS | ch.OUT_HIDDEN, nthreads=16)
+
+
 def test_forward_650m_q8_short():
     """The headline architecture (650M, Q8_0) on two short sequences, then on
     six residues alone (8 tokens: every linear layer on the GEMV path)."""

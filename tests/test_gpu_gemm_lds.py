@@ -47,13 +47,14 @@ def assert_same(got, ref, seqs, what):
             assert np.array_equal(g, r), (what, i, k, float(np.abs(g - r).max()))
 
 
-@pytest.mark.parametrize("tile", ["model", "128", "160", "256", "320"])
+@pytest.mark.parametrize("tile", ["model", "128", "160", "256", "320", "64x128", "64"])
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_forced_lds_gemm_is_bit_identical(fmt, tile, monkeypatch):
     """Ragged shapes: token count 687 and projection widths 576 / 192 / 768
-    are not multiples of any tile (128 x 128, 128 x 160, 128 x 256 and
-    128 x 320, forced through CIH_GEMM_TILE_N, or the round model's choice),
-    FC2 has K = 768."""
+    are not multiples of any tile (128 x 128, 128 x 160, 128 x 256,
+    128 x 320, 64 x 128 and 64 x 64, forced through CIH_GEMM_TILE_N, or the
+    round model's choice), FC2 has K = 768.  The two small tiles read the f16
+    copy only: the model without it takes 128 x 128 for them."""
     if tile != "model":
         monkeypatch.setenv("CIH_GEMM_TILE_N", tile)
     rng = np.random.default_rng(11)
@@ -96,3 +97,32 @@ def test_650m_headline_batch_is_bit_identical(monkeypatch):
     assert_same(c, a, seqs, "650M quants")
     ref.close()
     lds.close()
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_planned_routing_is_bit_identical(fmt, monkeypatch):
+    """The default route of f16-limb GEMMs from 256 rows on (gemm_lds_plan:
+    64 x 64 tiles here, 687 and 273 tokens) gives the register-staged
+    kernel's bits with every split off, as does the route without the plan
+    (CIH_GEMM_PLAN=0)."""
+    rng = np.random.default_rng(13)
+    cfg = ch.EsmConfig(192, 768, 2, 3)
+    w = ch.EsmWeights.random(cfg, seed=13, bias_std=0.02)
+    w = w.quantize_q8() if fmt == "q8" else w.quantize_q4()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    m = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=3, max_len=300, outputs=FLAGS)
+    monkeypatch.setenv("CIH_SPLITK", "0")
+    for lens in ((298, 255, 128), (150, 117)):
+        seqs = [rand_tokens(rng, n) for n in lens]
+        monkeypatch.setenv("CIH_GEMM_LDS", "0")
+        a = m.forward(seqs, FLAGS)
+        monkeypatch.delenv("CIH_GEMM_LDS")
+        b = m.forward(seqs, FLAGS)
+        monkeypatch.setenv("CIH_GEMM_PLAN", "0")
+        c = m.forward(seqs, FLAGS)
+        monkeypatch.delenv("CIH_GEMM_PLAN")
+        print(f"{fmt} {sum(lens) + 2 * len(lens)} tokens: planned and unplanned routes equal the register-staged one",
+              flush=True)
+        assert_same(b, a, seqs, fmt + " planned")
+        assert_same(c, a, seqs, fmt + " unplanned")
+    m.close()
