@@ -991,13 +991,16 @@ hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const
 // 256-8192 tokens on MI355X (256 CUs; the thresholds scale with the CU
 // count).  One 4-wave workgroup per CU exposes the per-block barrier and
 // operand-read latency to its lone wave per SIMD; smaller tiles put three or
-// four workgroups on each CU and leave fewer CUs idle in the last round:
-//   * residual projections with K >= 2560 (80 blocks) whose caller adds
+// four workgroups on each CU and leave fewer CUs idle in the last round.  A
+// split's partial sums cost the LayerNorm that adds them about S M N 4 bytes
+// at 2 TB/s (3B, 2048 x 2560, 3 splits: 10.1 -> 41.6 us), so splits pay only
+// where the unsplit GEMM leaves most of the device idle:
+//   * residual projections with K >= 5120 (160 blocks) whose caller adds
 //     splits: up to 100 tiles of 128 x 128, 64 x 128 tiles in 3 k-splits;
-//     fewer 128 x 128 tiles than CUs, those in min(2 CUs / tiles, 3) splits;
-//     up to 4/3 CUs of them, 3 splits; else the round model's tile unsplit;
+//     fewer 128 x 128 tiles than CUs, those in min(2 CUs / tiles, 3)
+//     splits; else the round model's tile, unsplit;
 //   * up to 5 CUs tiles of 64 x 64: that tile, residual projections split
-//     into min(2 CUs / tiles, 6, blocks / 4) (5 -> 4);
+//     into min(CUs / tiles, 6, blocks / 4) (5 -> 4);
 //   * else the round model's large tile (unchanged at the 650M 8192-token
 //     shapes).
 // ESM-2 35M at 2552 tokens (8 ragged sequences), against the register-staged
@@ -1018,23 +1021,20 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     int tile, S = 1;
     if (const int forced = tile_env(epi)) {
         tile = forced;
-    } else if (can_split && KB >= 80) {
+    } else if (can_split && KB >= 160) {
         if (t128 * 256 <= 100 * cus) {
             tile = LDS_TILE_64x128;
             S = 3;
         } else if (t128 < cus) {
             tile = LDS_TILE_128x128;
             S = (int)std::min<long>(2 * cus / t128, 3);
-        } else if (t128 * 3 <= 4 * cus) {
-            tile = LDS_TILE_128x128;
-            S = 3;
         } else {
             tile = tile_choice(M, W.N, true);
         }
     } else if (t64 <= 5 * cus) {
         tile = LDS_TILE_64x64;
         if (can_split) {
-            S = (int)std::max<long>(1, std::min<long>({2 * cus / t64, 6, KB / 4}));
+            S = (int)std::max<long>(1, std::min<long>({cus / t64, 6, KB / 4}));
             if (S == 5) S = 4;
         }
     } else {

@@ -189,13 +189,13 @@ def test_forward_preset_archs(arch, dtype, B, lo, hi):
 
 @pytest.mark.parametrize("lens", [(300, 220), (650, 650, 650, 650)])
 def test_planned_splits_vs_oracle(lens):
-    """ESM-2 150M projection widths (d = 640, FC2 K = 2560) over two layers,
-    Q8_0: the planned k-splits of the residual projections, which leave their
-    partial sums to the LayerNorm after them.  524 tokens: Wo on 64 x 64
-    tiles in 4 splits, FC2 on 64 x 128 tiles in 3; 2608 tokens: FC2 on
-    128 x 128 tiles in 3."""
+    """d = 640 with FC2 K = 5120 over two layers, Q8_0: the planned k-splits
+    of the residual projections, which leave their partial sums to the
+    LayerNorm after them.  524 tokens: Wo on 64 x 64 tiles in 2 splits, FC2
+    on 64 x 128 tiles in 3; 2608 tokens: Wo unsplit, FC2 on 128 x 128 tiles
+    in 3."""
     rng = np.random.default_rng(21)
-    cfg = ch.EsmConfig(640, 2560, 2, 20)
+    cfg = ch.EsmConfig(640, 5120, 2, 20)
     w = ch.EsmWeights.random(cfg, seed=21, bias_std=0.02).quantize_q8()
     seqs = [rand_tokens(rng, n) for n in lens]
     print(f"planned splits, {sum(lens) + 2 * len(lens)} tokens", flush=True)
