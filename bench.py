@@ -50,14 +50,23 @@ DTYPE_NOTE = ("GEMM activations as two f16 limbs (hi = f16(x), lo = f16(x - hi):
 
 def qgemm_name(wname, T, d):
     """Which quantized GEMM the forward's projections take at T tokens: the
-    LDS-staged kernel when even the narrowest projection (N = d) gives a full
-    round of 128 x 128 tiles (reading the f16 copy of the quants, or the quants
-    of a model loaded with CIH_GEMM_F16=0), else the register-staged one
-    (split-K for small T)."""
-    lds = (os.environ.get("CIH_GEMM_LDS") != "0"
-           and (os.environ.get("CIH_GEMM_LDS") == "force" or -(-T // 128) * -(-d // 128) >= 256))
+    LDS-staged kernel from 256 tokens on while the f16 copy of the quants is
+    there (its plan picks 64 x 64 tiles below about five per CU, the large
+    tiles above), or, for a model loaded with CIH_GEMM_F16=0, when even the
+    narrowest projection (N = d) gives a full round of 128 x 128 tiles; else
+    the register-staged one (split-K for small T)."""
+    env = os.environ.get
+    copy = env("CIH_GEMM_F16") != "0"
+    if env("CIH_GEMM_LDS") == "0":
+        lds = False
+    elif env("CIH_GEMM_LDS") == "force":
+        lds = True
+    elif copy and env("CIH_GEMM_PLAN") != "0":
+        lds = T >= 256
+    else:
+        lds = -(-T // 128) * -(-d // 128) >= 256
     if lds:
-        src = "quants" if os.environ.get("CIH_GEMM_F16") == "0" else "f16 copy of the quants"
+        src = "f16 copy of the quants" if copy else "quants"
         return f"k_gemm_lds<{wname}> f16 MFMA, 2 limbs, operands global->LDS, W from the {src} (QKV, Wo, FC1, FC2)"
     return f"k_gemm_x3<{wname}> f16 MFMA, 2 limbs (QKV, Wo, FC1, FC2)"
 
