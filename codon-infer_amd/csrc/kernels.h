@@ -234,12 +234,15 @@ hipError_t launch_gemv16(const DevMatrix &W, const unsigned short *X, int M, con
 // FP32 [M][K] (16-byte aligned, K % 32 == 0) -> H2 limbs [M][K/32][64]
 hipError_t launch_to_h2(const float *x, int M, int K, unsigned short *out, hipStream_t st);
 
-// The same GEMM for activations in f16 limbs (AF_H2) and W.q16 present, with
-// operands copied global -> LDS by the load unit (no staging registers).
-// Epilogues EPI_NONE / EPI_RESIDUAL / EPI_GELU_H2.  gemm_lds_applies says
-// whether launch_gemm_x3 routes a call there: the shape must give at least
-// one full round of 128x128 tiles (smaller problems keep the split-K path);
-// CIH_GEMM_LDS=0 never, =force whenever the formats allow.
+// The same GEMM for activations in f16 limbs (AF_H2), with operands copied
+// global -> LDS by the load unit (no staging registers), W read from W.q16
+// or, without it, from the quants.  Epilogues EPI_NONE / EPI_RESIDUAL /
+// EPI_GELU_H2 (and the QKV image epilogues).  With W.q16, launch_gemm_x3
+// routes f16-limb calls of 256 rows and more by gemm_lds_plan (below);
+// otherwise gemm_lds_applies says whether it routes a call here: the shape
+// must give at least one full round of 128x128 tiles (smaller problems keep
+// the split-K path).  CIH_GEMM_LDS=0 never, =force whenever the formats
+// allow (tile: CIH_GEMM_TILE_N or the round model).
 bool gemm_lds_applies(const DevMatrix &W, int a_fmt, int M, int epi);
 hipError_t launch_gemm_lds(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
                            hipStream_t st, const QkvOut *qo = nullptr);
