@@ -317,7 +317,7 @@ __device__ __forceinline__ unsigned add_here(unsigned a, unsigned b) {
 // SPLIT: workgroup (tile, y) takes k-blocks [y kps, (y + 1) kps) and stores
 // its raw sums (no bias, no epilogue) into part + y M N, row-major [M][N];
 // the caller adds the splits in order (EPI_NONE only).
-template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false, int SCH = 0>
+template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false, int SCH = 0, bool PERS = false>
 __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned char *__restrict__ WB, const float *__restrict__ Wsc,
     const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo, int kps = 0) {
@@ -335,9 +335,12 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     constexpr int EL = QKV ? qkv_epilogue_lds<2 * QHALF, RT, CT, WM, WN>() : 0;
     constexpr int LOFF = 3 * STAGE > EL ? 3 * STAGE : EL;  // start of the prefetched rows
     // the tile's BN bias values, written 64 at a time (whole 256-byte rows)
-    constexpr int BOFF = LOFF + XTRA, BBYTES = (BN * 4 + 255) / 256 * 256;
-    static_assert(BOFF + BBYTES <= 160 * 1024, "LDS");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[BOFF + BBYTES];
+    // (two buffers of it in the persistent form: the next tile's is fetched
+    // while this tile's epilogue reads its own)
+    constexpr int BOFF = LOFF + XTRA, BBYTES = (BN * 4 + 255) / 256 * 256, NBB = PERS ? 2 : 1;
+    static_assert(!PERS || (!QKV && !SPLIT && WQ == 0), "persistent form: plain epilogues, f16 copy");
+    static_assert(BOFF + NBB * BBYTES <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[BOFF + NBB * BBYTES];
 
     // the wave index is uniform: wave-derived offsets (LDS destinations) live in SGPRs
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -346,7 +349,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
     int mt, nt;
     tile_xcd(blockIdx.x, nM * nN, nM, nN, mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
+    int m0 = mt * BM, n0 = nt * BN;  // (the persistent form moves them to the next tile)
     const int KB = K / 32;
     // k-blocks [kb0, kb1) of this workgroup
     const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kb1 = SPLIT ? min(KB, kb0 + kps) : KB;
@@ -363,9 +366,9 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     // first row of X, its first column of W and of the scales; the block
     // advances the bases in scalar registers): the loads take the scalar base
     // + 32-bit offset form, and no 64-bit address lives in vector registers.
-    const unsigned char *const xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KB * 128;
-    const unsigned char *const wbase = WB + (size_t)n0 * BPC;
-    const float *const sbase = Wsc + n0;
+    const unsigned char *xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KB * 128;
+    const unsigned char *wbase = WB + (size_t)n0 * BPC;
+    const float *sbase = Wsc + n0;
     unsigned offA[NA];
     int dstA[NA];
 #pragma unroll
@@ -399,20 +402,48 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         offB[i] = (unsigned)((min(n0 + col, N - 1) - n0) * BPC + chunk * 16);
         dstB[i] = SA + j * 1024;
     }
-    const unsigned offS = (unsigned)(min(n0 + wave * SL + min(lane, SL - 1), N - 1) - n0) * 4;
+    unsigned offS = (unsigned)(min(n0 + wave * SL + min(lane, SL - 1), N - 1) - n0) * 4;
+    // the sources of tile t, as above (persistent form)
+    auto set_tile = [&](int t) __attribute__((always_inline)) {
+        int tm, tn;
+        tile_xcd(t, nM * nN, nM, nN, tm, tn);
+        m0 = tm * BM;
+        n0 = tn * BN;
+        xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KB * 128;
+        wbase = WB + (size_t)n0 * BPC;
+        sbase = Wsc + n0;
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int j = i * NW + wave < T::LA ? i * NW + wave : wave;
+            const int p = j * 64 + lane;
+            const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
+            offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KB * 128 + chunk * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int j = i * NW + wave < T::LB ? i * NW + wave : wave % T::LB;
+            const int p = j * 64 + lane;
+            const int col = p >> 2, chunk = (p & 3) ^ ((col >> 2) & 3);
+            offB[i] = (unsigned)((min(n0 + col, N - 1) - n0) * BPC + chunk * 16);
+        }
+        offS = (unsigned)(min(n0 + wave * SL + min(lane, SL - 1), N - 1) - n0) * 4;
+    };
     // The tile's bias values go to LDS before the k loop (copied by the load
     // unit, ordered by the loop's first wait and barrier): the epilogue reads
     // them from LDS, so its stores follow no pending global load (a load
     // pending at a branch makes the compiler wait for every earlier store as
     // well) and no register holds them through the loop.
     float *s_bias = reinterpret_cast<float *>(lds + BOFF);
-    if (bias) {
-        if (wave * 64 < BN)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(bias + min(n0 + wave * 64 + lane, N - 1)),
-                                             (lds_ptr_t *)(lds + BOFF + wave * 256), 4, 0, 0);
-    } else {
-        for (int i = tid; i < BN; i += T::THREADS) s_bias[i] = 0.0f;
-    }
+    auto load_bias = [&](int buf) __attribute__((always_inline)) {
+        if (bias) {
+            if (wave * 64 < BN)
+                __builtin_amdgcn_global_load_lds((glb_ptr_t *)(bias + min(n0 + wave * 64 + lane, N - 1)),
+                                                 (lds_ptr_t *)(lds + BOFF + buf * BBYTES + wave * 256), 4, 0, 0);
+        } else if (buf == 0) {
+            for (int i = tid; i < NBB * BBYTES / 4; i += T::THREADS) s_bias[i] = 0.0f;
+        }
+    };
+    load_bias(0);
 
     auto request = [&](int kb, int stg) __attribute__((always_inline)) {
         unsigned char *base = lds + stg * STAGE;
@@ -650,6 +681,139 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     auto sync = [&]() __attribute__((always_inline)) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(T::NI) : "memory");
     };
+    if constexpr (PERS) {
+        // Persistent workgroups (grid <= tiles, tiles strided by the grid;
+        // the plain epilogues from the f16 copy): the stage ring runs on
+        // across tiles, so the next tile's first two blocks and its bias are
+        // fetched under this tile's last two blocks and its epilogue instead
+        // of after a new workgroup's start.  Needs KB >= 3 (the bias buffer a
+        // tile's epilogue reads is refilled two tiles later, after a barrier
+        // of the tile between).  The same sums in the same order.
+        auto finish = [&]() __attribute__((always_inline)) {
+            if constexpr (RT >= 2) {
+#pragma unroll
+                for (int r = 0; r < RT; r++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[r][CT - 1][q] += dpend * pend[r][q];
+            } else {
+                // (SCH 1 scales chains 0-2 inside each block; only the pair is pending)
+#pragma unroll
+                for (int c = (SCH == 1 && CT == 5) ? 3 : 0; c < CT; c++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[0][c][q] += dcar[c] * tcar[c][q];
+            }
+        };
+        auto epilogue = [&](const int em0, const int en0, const float *sb) __attribute__((always_inline)) {
+            // Epilogue: every output value is formed before the first store (the
+            // residual reads share one wait, and no store follows a pending load, which
+            // would make the compiler wait for each earlier store at every bounds
+            // branch); tiles inside the matrix store without bounds branches.
+            float res[CT][RT][16];
+            if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+                for (int c = 0; c < CT; c++) {
+                    const int col = min(en0 + (wn * CT + c) * 32 + li, N - 1);
+#pragma unroll
+                    for (int r = 0; r < RT; r++)
+#pragma unroll
+                        for (int q = 0; q < 16; q++) {
+                            const int row = min(em0 + (wm * RT + r) * 32 + 8 * (q >> 2) + 4 * hh + (q & 3), M - 1);
+                            res[c][r][q] = reinterpret_cast<const float *>(Yv)[(size_t)row * ldy + col];
+                        }
+                }
+            }
+            float bv[CT];
+#pragma unroll
+            for (int c = 0; c < CT; c++) bv[c] = sb[(wn * CT + c) * 32 + li];
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int r = 0; r < RT; r++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) {
+                        float v = acc[r][c][q] + bv[c];
+                        if constexpr (EPI == EPI_GELU_H2) v = gelu_as(v);
+                        if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
+                        acc[r][c][q] = v;
+                    }
+            auto store = [&](bool guard) __attribute__((always_inline)) {
+#pragma unroll
+                for (int c = 0; c < CT; c++) {
+                    const int col = en0 + (wn * CT + c) * 32 + li;
+                    if (guard && col >= N) continue;
+#pragma unroll
+                    for (int r = 0; r < RT; r++)
+#pragma unroll
+                        for (int q = 0; q < 16; q++) {
+                            const int row = em0 + (wm * RT + r) * 32 + 8 * (q >> 2) + 4 * hh + (q & 3);
+                            if (guard && row >= M) continue;
+                            if constexpr (EPI == EPI_GELU_H2)
+                                h2_store(reinterpret_cast<unsigned short *>(Yv), row, col, N, acc[r][c][q]);
+                            else
+                                reinterpret_cast<float *>(Yv)[(size_t)row * ldy + col] = acc[r][c][q];
+                        }
+                }
+            };
+            if (em0 + BM <= M && en0 + BN <= N)
+                store(false);
+            else
+                store(true);
+        };
+        const int ntiles = nM * nN;
+        int rt = blockIdx.x, rkb = 0, rbuf = 0;  // request cursor: tile, block, bias buffer
+        bool rlive = true;
+        // blocks in tile order across this workgroup's tiles; past its last
+        // tile the requests re-read that tile's last block (stages nobody reads)
+        auto issue = [&](int stgq) __attribute__((always_inline)) {
+            request(rlive ? rkb : KB - 1, stgq);
+            if (rlive && ++rkb == KB) {
+                rkb = 0;
+                rt += gridDim.x;
+                if (rt < ntiles) {
+                    set_tile(rt);
+                    rbuf ^= 1;
+                    load_bias(rbuf);
+                } else {
+                    rlive = false;
+                }
+            }
+        };
+        issue(0);
+        issue(1);
+        int stg = 0, buf = 0;
+        for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
+            int tm, tn;
+            tile_xcd(t, ntiles, nM, nN, tm, tn);
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[r][c][q] = 0.0f;
+            dpend = 0.0f;
+#pragma unroll
+            for (int r = 0; r < (RT >= 2 ? RT : 1); r++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) pend[r][q] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < (RT >= 2 ? 1 : CT); c++) {
+                dcar[c] = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) tcar[c][q] = 0.0f;
+            }
+            for (int kb = 0; kb < KB; kb++) {
+                sync();
+                issue(stg == 0 ? 2 : stg - 1);
+                compute(stg);
+                stg = stg == 2 ? 0 : stg + 1;
+            }
+            finish();
+            epilogue(tm * BM, tn * BN, reinterpret_cast<const float *>(lds + BOFF + buf * BBYTES));
+            buf ^= 1;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
     // Requests past the last block re-read it into a stage nobody reads again,
     // so every wave issues the same instructions and the counts hold.
     request(kb0, 0);
@@ -794,6 +958,20 @@ int gemm_sched() {
 // copy only.
 template <int RT, int CT> constexpr bool copy_only() { return RT == 1 && CT <= 2; }
 
+// Workgroups of the persistent form for a launch of `tiles` tiles of KB
+// blocks, 0 for one tile per workgroup: one per CU (a multiple of the 8
+// XCDs, so that a workgroup's tiles stay on its XCD) when the tiles take
+// more than one round.  CIH_GEMM_PERSIST=0: never; =force: 8 workgroups
+// whenever the form applies (many tiles each, for tests).
+int persist_grid(int tiles, int KB) {
+    if (KB < 3) return 0;
+    const char *e = getenv("CIH_GEMM_PERSIST");
+    if (e && !strcmp(e, "0")) return 0;
+    if (e && !strcmp(e, "force")) return std::min(tiles, 8);
+    const int g = device_cus() / 8 * 8;
+    return g > 0 && tiles > g ? g : 0;
+}
+
 template <int EPI, int RT, int CT, int WM, int WN>
 hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
                     const QkvOut &qo) {
@@ -811,10 +989,23 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     else if (quants && W.fmt == WF_Q4)
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, WF_Q4>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
-    else if (RT == 1 && CT == 5 && gemm_sched() == 1)
+    else if (RT == 1 && CT == 5 && gemm_sched() == 1) {
+        // 128 x 320 with a plain GELU or no epilogue over more than one round:
+        // persistent workgroups (FC1 at 8192 tokens of ESM-2 650M, 4 rounds:
+        // 290 -> 280 us in isolation; Wo and FC2 are one round, and the
+        // residual form would spill)
+        if constexpr (WM == 4 && WN == 2 && (EPI == EPI_GELU_H2 || EPI == EPI_NONE)) {
+            if (const int g = persist_grid(tiles, W.K / 32)) {
+                hipLaunchKernelGGL((k_gemm_lds<EPI, 1, 5, 4, 2, 0, false, 1, true>), dim3(g), dim3(T::THREADS), 0, st,
+                                   Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N,
+                                   W.K, qo, 0);
+                return hipGetLastError();
+            }
+        }
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, (RT == 1 && CT == 5) ? 1 : 0>), dim3(tiles),
                            dim3(T::THREADS), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y,
                            ldy, M, W.N, W.K, qo, 0);
+    }
     else
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
                            reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K, qo);

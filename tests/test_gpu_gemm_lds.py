@@ -126,3 +126,32 @@ def test_planned_routing_is_bit_identical(fmt, monkeypatch):
         assert_same(b, a, seqs, fmt + " planned")
         assert_same(c, a, seqs, fmt + " unplanned")
     m.close()
+
+
+@pytest.mark.parametrize("dims", [(192, 768, 3), (96, 384, 4)])
+def test_persistent_workgroups_are_bit_identical(dims, monkeypatch):
+    """The persistent form of the 128 x 320 tile (FC1 + GELU, and the plain
+    QKV projection of head size 24, which has no image epilogue): 8
+    workgroups stride over all tiles (CIH_GEMM_PERSIST=force), each running
+    the stage ring on from one tile into the next, and the forwards equal
+    the register-staged kernel's bit for bit."""
+    d, f, H = dims
+    rng = np.random.default_rng(17)
+    cfg = ch.EsmConfig(d, f, 2, H)
+    w = ch.EsmWeights.random(cfg, seed=17, bias_std=0.02).quantize_q8()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    seqs = [rand_tokens(rng, 298), rand_tokens(rng, 255), rand_tokens(rng, 128)]
+    m = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=3, max_len=300, outputs=FLAGS)
+    monkeypatch.setenv("CIH_SPLITK", "0")
+    monkeypatch.setenv("CIH_GEMM_LDS", "0")
+    a = m.forward(seqs, FLAGS)
+    monkeypatch.setenv("CIH_GEMM_LDS", "force")
+    monkeypatch.setenv("CIH_GEMM_TILE_N", "320")
+    monkeypatch.setenv("CIH_GEMM_PERSIST", "force")
+    b = m.forward(seqs, FLAGS)
+    monkeypatch.setenv("CIH_GEMM_PERSIST", "0")
+    c = m.forward(seqs, FLAGS)
+    print(f"d={d}: persistent and one-tile workgroups equal the register-staged forward", flush=True)
+    assert_same(b, a, seqs, "persistent")
+    assert_same(c, a, seqs, "one tile per workgroup")
+    m.close()
