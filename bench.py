@@ -50,7 +50,7 @@ DTYPE_NOTE = ("GEMM activations as two f16 limbs (hi = f16(x), lo = f16(x - hi):
 
 def qgemm_name(wname, T, d):
     """Which quantized GEMM the forward's projections take at T tokens: the
-    LDS-staged kernel from 256 tokens on while the f16 copy of the quants is
+    LDS-staged kernel from 64 tokens on while the f16 copy of the quants is
     there (its plan picks 64 x 64 tiles below about five per CU, the large
     tiles above), or, for a model loaded with CIH_GEMM_F16=0, when even the
     narrowest projection (N = d) gives a full round of 128 x 128 tiles; else
@@ -62,7 +62,7 @@ def qgemm_name(wname, T, d):
     elif env("CIH_GEMM_LDS") == "force":
         lds = True
     elif copy and env("CIH_GEMM_PLAN") != "0":
-        lds = T >= 256
+        lds = T >= 64
     else:
         lds = -(-T // 128) * -(-d // 128) >= 256
     if lds:

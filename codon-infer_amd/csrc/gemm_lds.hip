@@ -1179,15 +1179,16 @@ hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const
 
 // Routing of the problems that do not fill the device with 128-row tiles,
 // from a sweep of every tile and split over the ESM-2 8M-3B projections at
-// 256-8192 tokens on MI355X (256 CUs; the thresholds scale with the CU
-// count).  One 4-wave workgroup per CU exposes the per-block barrier and
+// 16-8192 tokens on MI355X (256 CUs; the thresholds scale with the CU
+// count); below 64 rows the register-staged kernel stays.  One 4-wave workgroup per CU exposes the per-block barrier and
 // operand-read latency to its lone wave per SIMD; smaller tiles put three or
 // four workgroups on each CU and leave fewer CUs idle in the last round.  A
 // split's partial sums cost the LayerNorm that adds them about S M N 4 bytes
 // at 2 TB/s (3B, 2048 x 2560, 3 splits: 10.1 -> 41.6 us), so splits pay only
 // where the unsplit GEMM leaves most of the device idle:
 //   * residual projections with K >= 5120 (160 blocks) whose caller adds
-//     splits: up to 100 tiles of 128 x 128, 64 x 128 tiles in 3 k-splits;
+//     splits, from 25 tiles of 128 x 128 on (fewer: the 64 x 64 rule
+//     below): up to 100 such tiles, 64 x 128 tiles in 3 k-splits;
 //     fewer 128 x 128 tiles than CUs, those in min(2 CUs / tiles, 3)
 //     splits; else the round model's tile, unsplit;
 //   * up to 5 CUs tiles of 64 x 64: that tile, residual projections split
@@ -1202,7 +1203,7 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     p = LdsPlan();
     if (a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || !W.q16 || W.K % 32 || W.K <= 0 || W.N <= 0) return false;
     if (epi != EPI_NONE && epi != EPI_RESIDUAL && epi != EPI_GELU_H2) return false;
-    if (M < 256) return false;  // below the sweep: the register-staged kernel and its splits
+    if (M < 64) return false;  // fewer rows: the register-staged kernel (and its splits) is as fast or faster
     const char *le = getenv("CIH_GEMM_LDS"), *pe = getenv("CIH_GEMM_PLAN"), *ke = getenv("CIH_SPLITK");
     if (le || (pe && !strcmp(pe, "0"))) return false;  // CIH_GEMM_LDS=0 / force: the routes without the plan
     const long cus = device_cus();
@@ -1212,7 +1213,7 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     int tile, S = 1;
     if (const int forced = tile_env(epi)) {
         tile = forced;
-    } else if (can_split && KB >= 160) {
+    } else if (can_split && KB >= 160 && t128 * 256 > 25 * cus) {
         if (t128 * 256 <= 100 * cus) {
             tile = LDS_TILE_64x128;
             S = 3;

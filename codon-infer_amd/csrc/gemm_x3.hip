@@ -582,7 +582,7 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     if (M <= 0) return hipSuccess;
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
     if ((epi == EPI_GELU_X3 || epi == EPI_GELU_H2) && W.N % 32 != 0) return hipErrorInvalidValue;
-    // f16 limbs with the f16 copy of the quants, 256 rows and more: the LDS
+    // f16 limbs with the f16 copy of the quants, 64 rows and more: the LDS
     // kernel's tile (and split) for the shape
     if (LdsPlan p; gemm_lds_plan(W, a_fmt, M, epi, defer && pb && pb->part ? pb->floats : 0, p)) {
         const hipError_t e = launch_gemm_lds_plan(W, X, bias, Y, ldy, M, epi, p, pb, st);

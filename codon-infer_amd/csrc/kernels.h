@@ -238,7 +238,7 @@ hipError_t launch_to_h2(const float *x, int M, int K, unsigned short *out, hipSt
 // global -> LDS by the load unit (no staging registers), W read from W.q16
 // or, without it, from the quants.  Epilogues EPI_NONE / EPI_RESIDUAL /
 // EPI_GELU_H2 (and the QKV image epilogues).  With W.q16, launch_gemm_x3
-// routes f16-limb calls of 256 rows and more by gemm_lds_plan (below);
+// routes f16-limb calls of 64 rows and more by gemm_lds_plan (below);
 // otherwise gemm_lds_applies says whether it routes a call here: the shape
 // must give at least one full round of 128x128 tiles (smaller problems keep
 // the split-K path).  CIH_GEMM_LDS=0 never, =force whenever the formats
@@ -255,7 +255,7 @@ hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const
                                  hipStream_t st);
 // Workgroup tiles of the LDS-staged GEMM (BM x BN).
 enum LdsTileId { LDS_TILE_128x128 = 1, LDS_TILE_128x160, LDS_TILE_128x256, LDS_TILE_128x320, LDS_TILE_64x128, LDS_TILE_64x64 };
-// Tile and k-splits for an f16-limb GEMM with the f16 copy from 256 rows on
+// Tile and k-splits for an f16-limb GEMM with the f16 copy from 64 rows on
 // (false: not such a GEMM, or CIH_GEMM_LDS / CIH_GEMM_PLAN=0 set).  Splits
 // only for EPI_RESIDUAL with room for them (part_floats > 0; the caller
 // adds them, as launch_gemm_lds_split's).

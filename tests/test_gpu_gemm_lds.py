@@ -101,7 +101,7 @@ def test_650m_headline_batch_is_bit_identical(monkeypatch):
 
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_planned_routing_is_bit_identical(fmt, monkeypatch):
-    """The default route of f16-limb GEMMs from 256 rows on (gemm_lds_plan:
+    """The default route of f16-limb GEMMs from 64 rows on (gemm_lds_plan:
     64 x 64 tiles here, 687 and 273 tokens) gives the register-staged
     kernel's bits with every split off, as does the route without the plan
     (CIH_GEMM_PLAN=0)."""
