@@ -100,7 +100,9 @@ __global__ __launch_bounds__(RLN_MAX_THREADS) void k_rln(float *__restrict__ x, 
 // The same for many rows: one wave per row, four rows per workgroup, lane l
 // owning column quads l, l + 64, ... (PER of them) as k_layernorm4 does; the
 // fold, the mean and variance sums and their order are k_rln's, so both give
-// the same bits.
+// the same bits.  The splits are folded 8 at a time and the LayerNorm's
+// weights read after the row's statistics, so that the kernel keeps a few
+// waves per SIMD at d = 2560 (PER 10: 256 -> ~100 VGPRs).
 template <int PER, int OF>
 __global__ __launch_bounds__(256) void k_rln4(float *__restrict__ x, const float *__restrict__ part, int S,
                                               const float *__restrict__ pb, const float *__restrict__ w,
@@ -110,20 +112,15 @@ __global__ __launch_bounds__(256) void k_rln4(float *__restrict__ x, const float
     if (row >= rows) return;
     const int n4 = d >> 2;
     f32x4 *xr = reinterpret_cast<f32x4 *>(x + (size_t)row * d);
-    f32x4 v[PER], g[PER], be[PER];
+    f32x4 v[PER];
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const int c = min(lane + 64 * i, n4 - 1);  // past the row: re-read, masked below
-        v[i] = xr[c];
-        g[i] = reinterpret_cast<const f32x4 *>(w)[c];
-        be[i] = reinterpret_cast<const f32x4 *>(b)[c];
-    }
+    for (int i = 0; i < PER; i++) v[i] = xr[min(lane + 64 * i, n4 - 1)];  // past the row: re-read, masked below
     if (part) {
         const size_t stride = (size_t)rows * d;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             const int c = min(lane + 64 * i, n4 - 1);
-            const f32x4 acc = fold_splits4(part + (size_t)row * d + 4 * c, S, stride);
+            const f32x4 acc = fold_splits4<8>(part + (size_t)row * d + 4 * c, S, stride);
             const f32x4 bb = reinterpret_cast<const f32x4 *>(pb)[c];
             v[i] = v[i] + (acc + bb);
             if (lane + 64 * i < n4) xr[c] = v[i];
@@ -151,10 +148,11 @@ __global__ __launch_bounds__(256) void k_rln4(float *__restrict__ x, const float
     for (int i = 0; i < PER; i++) {
         const int c = lane + 64 * i;
         if (c >= n4) break;
+        const f32x4 g = reinterpret_cast<const f32x4 *>(w)[c], be = reinterpret_cast<const f32x4 *>(b)[c];
         f32x4 y;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            y[e] = g[i][e] * (v[i][e] - mean) * inv + be[i][e];
+            y[e] = g[e] * (v[i][e] - mean) * inv + be[e];
             flag_limb_range(flag, y[e]);
         }
         if constexpr (OF == AF_H2)

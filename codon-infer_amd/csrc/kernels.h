@@ -97,16 +97,19 @@ __device__ __forceinline__ void row_stats64(const fold4_t *xs, int n4, int d, in
     for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
     var = q / (float)d;
 }
+// (CH loads in flight at a time: fewer registers for kernels that fold many
+// column quads per lane; the additions stay in split order)
+template <int CH = FOLD_CHUNK>
 __device__ __forceinline__ fold4_t fold_splits4(const float *__restrict__ p, int S, size_t stride) {
     fold4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = 0; s0 < S; s0 += FOLD_CHUNK) {
-        fold4_t v[FOLD_CHUNK];
+    for (int s0 = 0; s0 < S; s0 += CH) {
+        fold4_t v[CH];
 #pragma unroll
-        for (int u = 0; u < FOLD_CHUNK; u++)
+        for (int u = 0; u < CH; u++)
             v[u] = s0 + u < S ? *reinterpret_cast<const fold4_t *>(p + (size_t)(s0 + u) * stride)
                               : fold4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < FOLD_CHUNK; u++) acc += v[u];
+        for (int u = 0; u < CH; u++) acc += v[u];
     }
     return acc;
 }
