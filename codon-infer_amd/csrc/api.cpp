@@ -388,6 +388,12 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
         if (m->dtype != DT_FP32 && !fp32_gemm && T > GEMV_MAX_M) {
             if ((apath && !std::strcmp(apath, "x3")) || full_range_mode()) af = AF_X3;
             else if (!(apath && !std::strcmp(apath, "f32")) && !bf16) af = AF_H2;
+        } else if (m->dtype == DT_FP32 && !fp32_gemm && !bf16 && !apath && !full_range_mode() && T > GEMV_MAX_M &&
+                   L > 0 && m->layers[0].wqkv.p16) {
+            // FP32 weights through their f16 pair copies: the activations as
+            // f16 limbs too (the same split the GEMM makes of FP32 ones, so the
+            // same bits), which the LDS-staged GEMM reads; CIH_ACT=f32: FP32
+            af = AF_H2;
         } else if (m->dtype != DT_FP32 && !fp32_gemm && !apath && !bf16 && !full_range_mode() && L > 0 &&
                    gemv16_applies(m->layers[0].wqkv, AF_H2, T, EPI_NONE) &&
                    gemv16_applies(m->layers[0].wo, AF_H2, T, EPI_NONE) &&

@@ -317,10 +317,12 @@ __device__ __forceinline__ unsigned add_here(unsigned a, unsigned b) {
 // SPLIT: workgroup (tile, y) takes k-blocks [y kps, (y + 1) kps) and stores
 // its raw sums (no bias, no epilogue) into part + y M N, row-major [M][N];
 // the caller adds the splits in order (EPI_NONE only).
-template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false, int SCH = 0, bool PERS = false>
+template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false, int SCH = 0, bool PERS = false,
+          bool PX = false>
 __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned char *__restrict__ WB, const float *__restrict__ Wsc,
-    const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo, int kps = 0) {
+    const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo, int kps = 0,
+    int kbx = 0) {
     static_assert(!SPLIT || EPI == EPI_NONE, "split partial sums carry no epilogue");
     constexpr int BPC = WQ == WF_Q8 ? 32 : (WQ == WF_Q4 ? 16 : 64);
     using T = LdsTile<RT, CT, WM, WN, BPC>;
@@ -351,6 +353,10 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     tile_xcd(blockIdx.x, nM * nN, nM, nN, mt, nt);
     int m0 = mt * BM, n0 = nt * BN;  // (the persistent form moves them to the next tile)
     const int KB = K / 32;
+    // activation blocks of a row (PX: a pair copy, whose weight block kb
+    // meets activation block kb mod kbx)
+    const int KBX = PX ? kbx : KB;
+    if (PX && (kbx <= 0 || 2 * kbx != KB)) return;  // (the host passes kbx = K / 64 with a pair copy)
     // k-blocks [kb0, kb1) of this workgroup
     const int kb0 = SPLIT ? (int)blockIdx.y * kps : 0, kb1 = SPLIT ? min(KB, kb0 + kps) : KB;
     if constexpr (SPLIT) {
@@ -366,7 +372,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     // first row of X, its first column of W and of the scales; the block
     // advances the bases in scalar registers): the loads take the scalar base
     // + 32-bit offset form, and no 64-bit address lives in vector registers.
-    const unsigned char *xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KB * 128;
+    const unsigned char *xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KBX * 128;
     const unsigned char *wbase = WB + (size_t)n0 * BPC;
     const float *sbase = Wsc + n0;
     unsigned offA[NA];
@@ -376,7 +382,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         const int j = i * NW + wave < T::LA ? i * NW + wave : wave;
         const int p = j * 64 + lane;
         const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
-        offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KB * 128 + chunk * 16);
+        offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KBX * 128 + chunk * 16);
         dstA[i] = j * 1024;
     }
     // W: chunk c of column n at c ^ ((n >> 2) & 3) (f16 copy, 4 chunks), at
@@ -409,7 +415,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         tile_xcd(t, nM * nN, nM, nN, tm, tn);
         m0 = tm * BM;
         n0 = tn * BN;
-        xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KB * 128;
+        xbase = reinterpret_cast<const unsigned char *>(X) + (size_t)m0 * KBX * 128;
         wbase = WB + (size_t)n0 * BPC;
         sbase = Wsc + n0;
 #pragma unroll
@@ -417,7 +423,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             const int j = i * NW + wave < T::LA ? i * NW + wave : wave;
             const int p = j * 64 + lane;
             const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
-            offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KB * 128 + chunk * 16);
+            offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KBX * 128 + chunk * 16);
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
@@ -447,7 +453,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
 
     auto request = [&](int kb, int stg) __attribute__((always_inline)) {
         unsigned char *base = lds + stg * STAGE;
-        const unsigned char *xb = xbase + (size_t)kb * 128, *wbk = wbase + (size_t)kb * N * BPC;
+        const unsigned char *xb = xbase + (size_t)(PX && kb >= KBX ? kb - KBX : kb) * 128, *wbk = wbase + (size_t)kb * N * BPC;
         const unsigned char *sbk = reinterpret_cast<const unsigned char *>(sbase + (size_t)kb * N);
 #pragma unroll
         for (int i = 0; i < NA; i++)
@@ -979,10 +985,17 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
     const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
     const bool quants = !W.q16;
+    const int kbx = W.kx / 32;
+    if (kbx && !copy_only<RT, CT>()) return hipErrorInvalidValue;  // pair copies: the small tiles only
     if constexpr (copy_only<RT, CT>()) {
         if (quants) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
-                           reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
+        if (kbx)
+            hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, 0, false, true>), dim3(tiles),
+                               dim3(T::THREADS), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias,
+                               Y, ldy, M, W.N, W.K, qo, 0, kbx);
+        else
+            hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
+                               reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
     } else if (quants && W.fmt == WF_Q8)
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, WF_Q8>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
@@ -1020,11 +1033,18 @@ hipError_t launch_split_t(const DevMatrix &W, const void *X, int M, float *part,
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
     const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
     const dim3 grid(tiles, S), block(T::THREADS);
+    const int kbx = W.kx / 32;
+    if (kbx && !copy_only<RT, CT>()) return hipErrorInvalidValue;  // pair copies: the small tiles only
     if constexpr (copy_only<RT, CT>()) {
         if (!W.q16) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true>), grid, block, 0, st, Xh,
-                           reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
-                           QkvOut(), kps);
+        if (kbx)
+            hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true, 0, false, true>), grid, block, 0, st, Xh,
+                               reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
+                               QkvOut(), kps, kbx);
+        else
+            hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true>), grid, block, 0, st, Xh,
+                               reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
+                               QkvOut(), kps);
     } else if (!W.q16 && W.fmt == WF_Q8)
         hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, WF_Q8, true>), grid, block, 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, nullptr, part, W.N, M, W.N, W.K, QkvOut(),
@@ -1201,7 +1221,9 @@ hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const
 // the LayerNorm after them.
 bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_floats, LdsPlan &p) {
     p = LdsPlan();
-    if (a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4) || !W.q16 || W.K % 32 || W.K <= 0 || W.N <= 0) return false;
+    if (a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4 && W.fmt != WF_F16P) || !W.q16 || W.K % 32 || W.K <= 0 ||
+        W.N <= 0 || W.kx % 32)
+        return false;
     if (epi != EPI_NONE && epi != EPI_RESIDUAL && epi != EPI_GELU_H2) return false;
     if (M < 64) return false;  // fewer rows: the register-staged kernel (and its splits) is as fast or faster
     const char *le = getenv("CIH_GEMM_LDS"), *pe = getenv("CIH_GEMM_PLAN"), *ke = getenv("CIH_SPLITK");
@@ -1232,6 +1254,9 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     } else {
         tile = tile_choice(M, W.N, true);
     }
+    // a pair copy (W.kx): the 64-row tiles only (the large ones keep the
+    // register-staged pair path)
+    if (W.kx && tile != LDS_TILE_64x64 && tile != LDS_TILE_64x128) return false;
     while (S > 1 && (size_t)S * M * W.N > part_floats) S--;
     if (S > 1) {
         p.kps = (KB + S - 1) / S;
@@ -1244,7 +1269,8 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
 
 hipError_t launch_gemm_lds_plan(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, int epi,
                                 const LdsPlan &p, const PartialBuf *pb, hipStream_t st) {
-    if ((W.fmt != WF_Q8 && W.fmt != WF_Q4) || !W.q16 || W.K % 32 || W.K <= 0 || M <= 0 || W.N <= 0 || !p.tile)
+    if ((W.fmt != WF_Q8 && W.fmt != WF_Q4 && W.fmt != WF_F16P) || !W.q16 || W.K % 32 || W.K <= 0 || M <= 0 ||
+        W.N <= 0 || !p.tile || W.kx % 32 || (W.kx && 2 * W.kx != W.K))
         return hipErrorInvalidValue;
     if (p.splits > 1) {
         if (epi != EPI_RESIDUAL || !pb || !pb->part || p.kps <= 0 || (size_t)p.splits * M * W.N > pb->floats ||

@@ -583,9 +583,20 @@ hipError_t launch_gemm_x3(const DevMatrix &W, const void *X, int ldx, int a_fmt,
     if (W.K % 32 != 0 || (a_fmt == AF_F32 && ldx % 4 != 0)) return hipErrorInvalidValue;
     if ((epi == EPI_GELU_X3 || epi == EPI_GELU_H2) && W.N % 32 != 0) return hipErrorInvalidValue;
     // f16 limbs with the f16 copy of the quants, 64 rows and more: the LDS
-    // kernel's tile (and split) for the shape
-    if (LdsPlan p; gemm_lds_plan(W, a_fmt, M, epi, defer && pb && pb->part ? pb->floats : 0, p)) {
-        const hipError_t e = launch_gemm_lds_plan(W, X, bias, Y, ldy, M, epi, p, pb, st);
+    // kernel's tile (and split) for the shape.  An FP32 matrix's pair copy
+    // (W.q: [2K/32][N][32] f16) goes the same way as an f16 matrix of 2K
+    // whose block kb meets activation block kb mod K/32.
+    DevMatrix pv;
+    const DevMatrix *lw = &W;
+    if (W.fmt == WF_F16P && a_fmt == AF_H2) {
+        pv = W;
+        pv.K = 2 * W.K;
+        pv.kx = W.K;
+        pv.q16 = static_cast<const unsigned short *>(W.q);
+        lw = &pv;
+    }
+    if (LdsPlan p; gemm_lds_plan(*lw, a_fmt, M, epi, defer && pb && pb->part ? pb->floats : 0, p)) {
+        const hipError_t e = launch_gemm_lds_plan(*lw, X, bias, Y, ldy, M, epi, p, pb, st);
         if (e == hipSuccess && defer && p.splits > 1) *defer = p.splits;
         return e;
     }

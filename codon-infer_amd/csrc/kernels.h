@@ -130,6 +130,10 @@ struct DevMatrix {
     // instead of FP32 MFMA (CIH_QGEMM=fp32 or full range: the FP32 kernel).
     const unsigned short *p16 = nullptr;
     const float *psc = nullptr;
+    // Activation length when it differs from K: a pair copy handed to the
+    // LDS-staged GEMM as an f16 matrix of K = 2 kx (weight block kb meets
+    // activation block kb mod kx / 32); 0: the activations have K elements.
+    int kx = 0;
 };
 
 // Workgroup -> output tile: consecutive workgroup ids go to the 8 XCDs in

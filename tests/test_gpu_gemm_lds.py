@@ -155,3 +155,31 @@ def test_persistent_workgroups_are_bit_identical(dims, monkeypatch):
     assert_same(b, a, seqs, "persistent")
     assert_same(c, a, seqs, "one tile per workgroup")
     m.close()
+
+
+def test_fp32_pair_copy_is_bit_identical(monkeypatch):
+    """FP32 weights run as f16 pair copies (an f16 matrix of 2K whose block
+    kb meets activation block kb mod K/32) with the activations handed over
+    as f16 limbs; from 64 rows on they take the LDS GEMM's planned tiles,
+    and the forward equals the register-staged kernel's pair path bit for
+    bit, with limbs or with FP32 activations split inside it (CIH_ACT=f32;
+    splits off; ESM-2 8M widths)."""
+    rng = np.random.default_rng(19)
+    cfg = ch.EsmConfig(320, 1280, 2, 20)
+    w = ch.EsmWeights.random(cfg, seed=19, bias_std=0.02)
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    m = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=2, max_len=300, outputs=FLAGS)
+    monkeypatch.setenv("CIH_SPLITK", "0")
+    for lens in ((298, 120), (70,)):
+        seqs = [rand_tokens(rng, n) for n in lens]
+        monkeypatch.setenv("CIH_GEMM_LDS", "0")
+        a = m.forward(seqs, FLAGS)
+        monkeypatch.setenv("CIH_ACT", "f32")  # FP32 hand-off, split inside the register-staged GEMM
+        c = m.forward(seqs, FLAGS)
+        monkeypatch.delenv("CIH_ACT")
+        monkeypatch.delenv("CIH_GEMM_LDS")
+        b = m.forward(seqs, FLAGS)
+        print(f"FP32 pair copy, {sum(lens) + 2 * len(lens)} tokens: LDS GEMM equals the register-staged one", flush=True)
+        assert_same(b, a, seqs, "fp32 pair")
+        assert_same(c, a, seqs, "fp32 hand-off")
+    m.close()
