@@ -536,9 +536,18 @@ def main():
         peak, limbs = PEAK_HBM_GBS, None
     else:
         achieved = q["flops"] / (q["total_ms"] * 1e-3) / 1e12 if q["total_ms"] > 0 else 0.0
-        if fp32_path or fp32_model:
+        env = os.environ.get
+        fp32_mfma = fp32_path or (fp32_model and (env("CIH_F32_PAIR") == "0" or env("CIH_LIMBS") == "bf16x3"))
+        if fp32_mfma:
             kname, peak, limbs = f"k_gemm<{wname}> FP32 MFMA (QKV, Wo, FC1, FC2, LM head)", PEAK_FP32_MFMA_TFLOPS, 1
-        elif os.environ.get("CIH_LIMBS") == "bf16x3":
+        elif fp32_model:
+            # the f16 pair copy of the FP32 weights (hi and lo halves, K doubled)
+            # times the activations' two f16 limbs: 4 f16 MFMA MACs per MAC
+            lds = T >= 64 and env("CIH_GEMM_LDS") != "0" and env("CIH_GEMM_PLAN") != "0" and env("CIH_ACT") != "f32"
+            kname = (("k_gemm_lds" if lds else "k_gemm_x3") + "<FP32 pair copy> f16 MFMA, 2 activation limbs x "
+                     "2 weight halves (QKV, Wo, FC1, FC2, LM head)")
+            peak, limbs = PEAK_F16_MFMA_TFLOPS, 4
+        elif env("CIH_LIMBS") == "bf16x3":
             kname, peak, limbs = f"k_gemm_x3<{wname}> bf16 MFMA, 3 limbs (QKV, Wo, FC1, FC2)", PEAK_BF16_MFMA_TFLOPS, 3
         else:
             kname, peak, limbs = qgemm_name(wname, T, cfg.dim), PEAK_F16_MFMA_TFLOPS, 2
