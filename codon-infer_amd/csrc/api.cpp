@@ -42,7 +42,7 @@ std::string kernel_switches() {
                                         "CIH_GEMV_NB", "CIH_GEMM_LDS", "CIH_GEMM_TILE", "CIH_GEMM_TILE_N",
                                         "CIH_GEMM_TILE_N_GELU", "CIH_ATT_IMG", "CIH_GEMV16", "CIH_GEMV16_KW",
                                         "CIH_FEW_WO", "CIH_DECODE_LN", "CIH_ATT_XCD", "CIH_GEMM_SCHED",
-                                        "CIH_GEMM_PLAN", "CIH_GEMM_PERSIST"};
+                                        "CIH_GEMM_PLAN", "CIH_GEMM_PERSIST", "CIH_GEMM_KW"};
     std::string s = g_full_range ? "R|" : "|";
     for (const char *n : names) {
         const char *v = getenv(n);

@@ -29,7 +29,10 @@
 // 128 x 128 (4 x 64 x 64, two per CU); and, for problems too small to fill
 // the device with those, 64 x 128 (4 x 32 x 64, three per CU) and 64 x 64
 // (4 x 32 x 32, four per CU), read from the f16 copy only.  Every tile sums the same products in the same
-// order, so the tile never changes a result.
+// order, so the tile never changes a result.  The 64 x 64 tile can also run
+// on 2 or 4 groups of its 4 waves (KW), which take alternate k-blocks
+// through stages of their own and add their sums at the end: the k-sum
+// regrouped, as a k-split regroups it.
 #include <stdlib.h>
 #include <string.h>
 
@@ -66,6 +69,9 @@ template <int RT, int CT, int WM, int WN, int BPC = 64> struct LdsTile {
     static constexpr int NI = NA + NB + 1;  // load instructions per wave and block
     static constexpr int OCC = THREADS >= 512 ? 1 : 512 / THREADS;  // workgroups per CU
     static constexpr int WPE = NW / 4 * OCC;  // waves per SIMD (HIP's second launch bound)
+    // KW groups of NW waves on one tile, each group with its own three
+    // stages: waves per SIMD when as many such workgroups as fit the LDS share a CU
+    static constexpr int wpe(int kw) { return kw == 1 ? WPE : NW * kw / 4 * (160 * 1024 / (kw * 3 * STAGE + 1024)); }
     static_assert(SA % 1024 == 0 && LA >= NW, "loads");
     static_assert(BN % NW == 0 && SL <= 64 && OCC * 3 * STAGE <= 160 * 1024, "tile");
 };
@@ -318,8 +324,8 @@ __device__ __forceinline__ unsigned add_here(unsigned a, unsigned b) {
 // its raw sums (no bias, no epilogue) into part + y M N, row-major [M][N];
 // the caller adds the splits in order (EPI_NONE only).
 template <int EPI, int RT, int CT, int WM, int WN, int WQ, bool SPLIT = false, int SCH = 0, bool PERS = false,
-          bool PX = false>
-__global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT, WM, WN>::WPE)) void k_gemm_lds(
+          bool PX = false, int KW = 1>
+__global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS * KW), (LdsTile<RT, CT, WM, WN>::wpe(KW))) void k_gemm_lds(
     const unsigned short *__restrict__ X, const unsigned char *__restrict__ WB, const float *__restrict__ Wsc,
     const float *__restrict__ bias, void *__restrict__ Yv, int ldy, int M, int N, int K, const QkvOut qo, int kps = 0,
     int kbx = 0) {
@@ -331,11 +337,17 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     // QKV epilogue with one workgroup per CU: the rows' padded key indices,
     // positions and RoPE table rows are fetched into LDS behind the k loop
     constexpr bool QKV = EPI == EPI_QKV16 || EPI == EPI_QKV32 || EPI == EPI_QKV64;
+    // KW > 1: KW groups of NW waves share the tile; group g takes k-blocks
+    // kb0 + g, kb0 + g + KW, ... through three stages of its own, and the
+    // groups' sums are added in group order at the end (through the stages)
+    static_assert(KW == 1 || (RT == 1 && CT <= 2 && WQ == 0 && !PERS && !QKV), "k-groups: small tiles, f16 copy");
+    static_assert((KW - 1) * NW * CT * 16 * 64 * 4 <= 3 * KW * STAGE, "group sums fit the stages");
+    constexpr int NTH = T::THREADS * KW;
     constexpr int QHALF = EPI == EPI_QKV16 ? 8 : (EPI == EPI_QKV32 ? 16 : 32);
     constexpr bool PREF = QKV && T::OCC == 1;
     constexpr int XTRA = PREF ? BM * 8 + 2 * BM * QHALF * 4 : 0;
     constexpr int EL = QKV ? qkv_epilogue_lds<2 * QHALF, RT, CT, WM, WN>() : 0;
-    constexpr int LOFF = 3 * STAGE > EL ? 3 * STAGE : EL;  // start of the prefetched rows
+    constexpr int LOFF = 3 * KW * STAGE > EL ? 3 * KW * STAGE : EL;  // start of the prefetched rows
     // the tile's BN bias values, written 64 at a time (whole 256-byte rows)
     // (two buffers of it in the persistent form: the next tile's is fetched
     // while this tile's epilogue reads its own)
@@ -346,7 +358,10 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
 
     // the wave index is uniform: wave-derived offsets (LDS destinations) live in SGPRs
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
+    // group grp and the wave lw within it (KW == 1: one group)
+    const int grp = KW > 1 ? wave / NW : 0, lw = KW > 1 ? wave % NW : wave;
+    const int wm = lw / WN, wn = lw % WN;
+    const int goff = grp * 3 * STAGE;  // the group's stages
     const int li = lane & 31, hh = lane >> 5;
     const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
     int mt, nt;
@@ -379,7 +394,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     int dstA[NA];
 #pragma unroll
     for (int i = 0; i < NA; i++) {
-        const int j = i * NW + wave < T::LA ? i * NW + wave : wave;
+        const int j = i * NW + lw < T::LA ? i * NW + lw : lw;
         const int p = j * 64 + lane;
         const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
         offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KBX * 128 + chunk * 16);
@@ -392,7 +407,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     int dstB[NB];
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-        const int j = i * NW + wave < T::LB ? i * NW + wave : wave % T::LB;
+        const int j = i * NW + lw < T::LB ? i * NW + lw : lw % T::LB;
         const int p = j * 64 + lane;
         int col, chunk;
         if constexpr (BPC == 64) {
@@ -408,7 +423,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         offB[i] = (unsigned)((min(n0 + col, N - 1) - n0) * BPC + chunk * 16);
         dstB[i] = SA + j * 1024;
     }
-    unsigned offS = (unsigned)(min(n0 + wave * SL + min(lane, SL - 1), N - 1) - n0) * 4;
+    unsigned offS = (unsigned)(min(n0 + lw * SL + min(lane, SL - 1), N - 1) - n0) * 4;
     // the sources of tile t, as above (persistent form)
     auto set_tile = [&](int t) __attribute__((always_inline)) {
         int tm, tn;
@@ -420,19 +435,19 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         sbase = Wsc + n0;
 #pragma unroll
         for (int i = 0; i < NA; i++) {
-            const int j = i * NW + wave < T::LA ? i * NW + wave : wave;
+            const int j = i * NW + lw < T::LA ? i * NW + lw : lw;
             const int p = j * 64 + lane;
             const int row = p >> 3, chunk = (p & 7) ^ ((row >> 1) & 7);
             offA[i] = (unsigned)((min(m0 + row, M - 1) - m0) * KBX * 128 + chunk * 16);
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
-            const int j = i * NW + wave < T::LB ? i * NW + wave : wave % T::LB;
+            const int j = i * NW + lw < T::LB ? i * NW + lw : lw % T::LB;
             const int p = j * 64 + lane;
             const int col = p >> 2, chunk = (p & 3) ^ ((col >> 2) & 3);
             offB[i] = (unsigned)((min(n0 + col, N - 1) - n0) * BPC + chunk * 16);
         }
-        offS = (unsigned)(min(n0 + wave * SL + min(lane, SL - 1), N - 1) - n0) * 4;
+        offS = (unsigned)(min(n0 + lw * SL + min(lane, SL - 1), N - 1) - n0) * 4;
     };
     // The tile's bias values go to LDS before the k loop (copied by the load
     // unit, ordered by the loop's first wait and barrier): the epilogue reads
@@ -446,13 +461,13 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                 __builtin_amdgcn_global_load_lds((glb_ptr_t *)(bias + min(n0 + wave * 64 + lane, N - 1)),
                                                  (lds_ptr_t *)(lds + BOFF + buf * BBYTES + wave * 256), 4, 0, 0);
         } else if (buf == 0) {
-            for (int i = tid; i < NBB * BBYTES / 4; i += T::THREADS) s_bias[i] = 0.0f;
+            for (int i = tid; i < NBB * BBYTES / 4; i += NTH) s_bias[i] = 0.0f;
         }
     };
     load_bias(0);
 
     auto request = [&](int kb, int stg) __attribute__((always_inline)) {
-        unsigned char *base = lds + stg * STAGE;
+        unsigned char *base = lds + goff + stg * STAGE;
         const unsigned char *xb = xbase + (size_t)(PX && kb >= KBX ? kb - KBX : kb) * 128, *wbk = wbase + (size_t)kb * N * BPC;
         const unsigned char *sbk = reinterpret_cast<const unsigned char *>(sbase + (size_t)kb * N);
 #pragma unroll
@@ -462,7 +477,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         for (int i = 0; i < NB; i++)
             __builtin_amdgcn_global_load_lds((glb_ptr_t *)(wbk + offB[i]), (lds_ptr_t *)(base + dstB[i]), 16, 0, 0);
         if (lane < SL)
-            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(sbk + offS), (lds_ptr_t *)(base + SA + SB + wave * SL * 4),
+            __builtin_amdgcn_global_load_lds((glb_ptr_t *)(sbk + offS), (lds_ptr_t *)(base + SA + SB + lw * SL * 4),
                                              4, 0, 0);
     };
 
@@ -538,8 +553,8 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         return lds + (add_here(lane_part, lds0 + uniform) - lds0);
     };
     auto compute = [&](int stg) __attribute__((always_inline)) {
-        const unsigned char *base = lds + stg * STAGE;
-        const int boff = stg * STAGE + SA;  // the stage's B operands
+        const unsigned char *base = lds + goff + stg * STAGE;
+        const int boff = goff + stg * STAGE + SA;  // the stage's B operands
         f16x8 a[2][2][RT];  // [k-half][limb][row tile]
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
@@ -549,7 +564,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
                 for (int r = 0; r < RT; r++) {
                     const int row = (wm * RT + r) * 32 + li, chunk = l * 4 + hh * 2 + kh;
                     a[kh][l][r] = *reinterpret_cast<const f16x8 *>(
-                        at((unsigned)(row * 128 + ((chunk ^ swA) << 4)), stg * STAGE));
+                        at((unsigned)(row * 128 + ((chunk ^ swA) << 4)), goff + stg * STAGE));
                 }
         if constexpr (RT >= 2) {
 #pragma unroll
@@ -607,7 +622,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             const f16x8 b00 = rd_b(0, 0), b10 = rd_b(1, 0), b20 = rd_b(2, 0);
             const f16x8 b01 = rd_b(0, 1), b11 = rd_b(1, 1), b21 = rd_b(2, 1);
             float dcur[CT];
-            const unsigned char *sc = at((unsigned)((wn * CT * 32 + li) * 4), stg * STAGE + SA + SB);
+            const unsigned char *sc = at((unsigned)((wn * CT * 32 + li) * 4), goff + stg * STAGE + SA + SB);
 #pragma unroll
             for (int c = 0; c < CT; c++) dcur[c] = *reinterpret_cast<const float *>(sc + c * 128);
             fence();
@@ -822,8 +837,18 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
     }
     // Requests past the last block re-read it into a stage nobody reads again,
     // so every wave issues the same instructions and the counts hold.
-    request(kb0, 0);
-    request(min(kb0 + 1, kb1 - 1), 1);
+    // KW > 1: group grp's step i is block kb0 + grp + KW i; every group runs
+    // the same nit steps (the same barriers in every wave), and a step whose
+    // block lies past kb1 requests the last block and computes nothing.
+    const int nit = (kb1 - kb0 + KW - 1) / KW;
+    auto gblk = [&](int i) __attribute__((always_inline)) { return min(kb0 + grp + KW * i, kb1 - 1); };
+    if constexpr (KW > 1) {
+        request(gblk(0), 0);
+        request(gblk(1), 1);
+    } else {
+        request(kb0, 0);
+        request(min(kb0 + 1, kb1 - 1), 1);
+    }
     if constexpr (PREF) {
         int *s_pk = reinterpret_cast<int *>(lds + LOFF), *s_pos = s_pk + BM;
         if (tid < BM) {
@@ -843,19 +868,39 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
             }
         }
     }
-    for (int kb = kb0;;) {
-        sync();
-        request(min(kb + 2, kb1 - 1), 2);
-        compute(0);
-        if (++kb == kb1) break;
-        sync();
-        request(min(kb + 2, kb1 - 1), 0);
-        compute(1);
-        if (++kb == kb1) break;
-        sync();
-        request(min(kb + 2, kb1 - 1), 1);
-        compute(2);
-        if (++kb == kb1) break;
+    if constexpr (KW > 1) {
+        for (int i = 0;;) {
+            const bool l0 = kb0 + grp + KW * i < kb1;
+            sync();
+            request(gblk(i + 2), 2);
+            if (l0) compute(0);
+            if (++i == nit) break;
+            const bool l1 = kb0 + grp + KW * i < kb1;
+            sync();
+            request(gblk(i + 2), 0);
+            if (l1) compute(1);
+            if (++i == nit) break;
+            const bool l2 = kb0 + grp + KW * i < kb1;
+            sync();
+            request(gblk(i + 2), 1);
+            if (l2) compute(2);
+            if (++i == nit) break;
+        }
+    } else {
+        for (int kb = kb0;;) {
+            sync();
+            request(min(kb + 2, kb1 - 1), 2);
+            compute(0);
+            if (++kb == kb1) break;
+            sync();
+            request(min(kb + 2, kb1 - 1), 0);
+            compute(1);
+            if (++kb == kb1) break;
+            sync();
+            request(min(kb + 2, kb1 - 1), 1);
+            compute(2);
+            if (++kb == kb1) break;
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if constexpr (RT >= 2) {
@@ -869,6 +914,27 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS), (LdsTile<RT, CT
         for (int c = (SCH == 1 && CT == 5) ? 3 : 0; c < CT; c++)
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[0][c][q] += dcar[c] * tcar[c][q];
+    }
+    if constexpr (KW > 1) {
+        // The groups' sums, added in group order by group 0, through the
+        // stages: after the first barrier every wave's copies have landed and
+        // every wave is done reading the stages.
+        float *red = reinterpret_cast<float *>(lds);
+        __syncthreads();
+        if (grp > 0) {
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) red[((((grp - 1) * NW + lw) * CT + c) * 16 + q) * 64 + lane] = acc[0][c][q];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g = 1; g < KW; g++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) acc[0][c][q] += red[((((g - 1) * NW + lw) * CT + c) * 16 + q) * 64 + lane];
     }
 
     // Epilogue: every output value is formed before the first store (the
@@ -978,10 +1044,11 @@ int persist_grid(int tiles, int KB) {
     return g > 0 && tiles > g ? g : 0;
 }
 
-template <int EPI, int RT, int CT, int WM, int WN>
+template <int EPI, int RT, int CT, int WM, int WN, int KW = 1>
 hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
                     const QkvOut &qo) {
     using T = LdsTile<RT, CT, WM, WN>;
+    static_assert(KW == 1 || copy_only<RT, CT>(), "k-groups: the small tiles");
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
     const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
     const bool quants = !W.q16;
@@ -990,12 +1057,13 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     if constexpr (copy_only<RT, CT>()) {
         if (quants) return hipErrorInvalidValue;
         if (kbx)
-            hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, 0, false, true>), dim3(tiles),
-                               dim3(T::THREADS), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias,
-                               Y, ldy, M, W.N, W.K, qo, 0, kbx);
+            hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, 0, false, true, KW>), dim3(tiles),
+                               dim3(T::THREADS * KW), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc,
+                               bias, Y, ldy, M, W.N, W.K, qo, 0, kbx);
         else
-            hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
-                               reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
+            hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, 0, false, false, KW>), dim3(tiles),
+                               dim3(T::THREADS * KW), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc,
+                               bias, Y, ldy, M, W.N, W.K, qo);
     } else if (quants && W.fmt == WF_Q8)
         hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, WF_Q8>), dim3(tiles), dim3(T::THREADS), 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, bias, Y, ldy, M, W.N, W.K, qo);
@@ -1027,24 +1095,25 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
 
 // Split-K form: grid (tiles, S), raw partial sums into part.  128 x 128 tiles
 // (4 waves) for every weight form; 64 x 128 and 64 x 64 from the f16 copy.
-template <int RT, int CT, int WM, int WN>
+template <int RT, int CT, int WM, int WN, int KW = 1>
 hipError_t launch_split_t(const DevMatrix &W, const void *X, int M, float *part, int S, int kps, hipStream_t st) {
     using T = LdsTile<RT, CT, WM, WN>;
+    static_assert(KW == 1 || copy_only<RT, CT>(), "k-groups: the small tiles");
     const int tiles = ((M + T::BM - 1) / T::BM) * ((W.N + T::BN - 1) / T::BN);
     const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
-    const dim3 grid(tiles, S), block(T::THREADS);
+    const dim3 grid(tiles, S), block(T::THREADS * KW);
     const int kbx = W.kx / 32;
     if (kbx && !copy_only<RT, CT>()) return hipErrorInvalidValue;  // pair copies: the small tiles only
     if constexpr (copy_only<RT, CT>()) {
         if (!W.q16) return hipErrorInvalidValue;
         if (kbx)
-            hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true, 0, false, true>), grid, block, 0, st, Xh,
-                               reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
-                               QkvOut(), kps, kbx);
+            hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true, 0, false, true, KW>), grid, block, 0, st,
+                               Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N,
+                               W.K, QkvOut(), kps, kbx);
         else
-            hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true>), grid, block, 0, st, Xh,
-                               reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N, W.K,
-                               QkvOut(), kps);
+            hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, 0, true, 0, false, false, KW>), grid, block, 0, st,
+                               Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, nullptr, part, W.N, M, W.N,
+                               W.K, QkvOut(), kps);
     } else if (!W.q16 && W.fmt == WF_Q8)
         hipLaunchKernelGGL((k_gemm_lds<EPI_NONE, RT, CT, WM, WN, WF_Q8, true>), grid, block, 0, st, Xh,
                            static_cast<const unsigned char *>(W.q), W.sc, nullptr, part, W.N, M, W.N, W.K, QkvOut(),
@@ -1060,9 +1129,13 @@ hipError_t launch_split_t(const DevMatrix &W, const void *X, int M, float *part,
     return hipGetLastError();
 }
 
-hipError_t launch_split(const DevMatrix &W, const void *X, int M, float *part, int S, int kps, int tile,
+hipError_t launch_split(const DevMatrix &W, const void *X, int M, float *part, int S, int kps, int tile, int kw,
                         hipStream_t st) {
-    if (tile == LDS_TILE_64x64) return launch_split_t<1, 1, 2, 2>(W, X, M, part, S, kps, st);
+    if (tile == LDS_TILE_64x64) {
+        if (kw == 4) return launch_split_t<1, 1, 2, 2, 4>(W, X, M, part, S, kps, st);
+        if (kw == 2) return launch_split_t<1, 1, 2, 2, 2>(W, X, M, part, S, kps, st);
+        return launch_split_t<1, 1, 2, 2>(W, X, M, part, S, kps, st);
+    }
     if (tile == LDS_TILE_64x128) return launch_split_t<1, 2, 2, 2>(W, X, M, part, S, kps, st);
     return launch_split_t<2, 2, 2, 2>(W, X, M, part, S, kps, st);
 }
@@ -1126,7 +1199,7 @@ int tile_env(int epi) {
 // copy becomes 128 x 128.
 template <int EPI>
 hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void *Y, int ldy, int M, hipStream_t st,
-                      const QkvOut &qo, int tile) {
+                      const QkvOut &qo, int tile, int kw = 1) {
     if (!tile) tile = tile_env(EPI);
     if (!tile) tile = tile_choice(M, W.N, W.q16 != nullptr);
     if (tile == LDS_TILE_128x320) return launch_t<EPI, 1, 5, 4, 2>(W, X, bias, Y, ldy, M, st, qo);
@@ -1135,7 +1208,11 @@ hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void
         if (tile == LDS_TILE_128x160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st, qo);
         if (W.q16) {
             if (tile == LDS_TILE_64x128) return launch_t<EPI, 1, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
-            if (tile == LDS_TILE_64x64) return launch_t<EPI, 1, 1, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+            if (tile == LDS_TILE_64x64) {
+                if (kw == 4) return launch_t<EPI, 1, 1, 2, 2, 4>(W, X, bias, Y, ldy, M, st, qo);
+                if (kw == 2) return launch_t<EPI, 1, 1, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+                return launch_t<EPI, 1, 1, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+            }
         }
     }
     return launch_t<EPI, 2, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
@@ -1194,7 +1271,7 @@ hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const
     const int kps = (KB + S - 1) / S;
     S = (KB + kps - 1) / kps;
     *splits = S;
-    return launch_split(W, X, M, pb.part, S, kps, LDS_TILE_128x128, st);
+    return launch_split(W, X, M, pb.part, S, kps, LDS_TILE_128x128, 1, st);
 }
 
 // Routing of the problems that do not fill the device with 128-row tiles,
@@ -1212,7 +1289,9 @@ hipError_t launch_gemm_lds_split(const DevMatrix &W, const void *X, int M, const
 //     fewer 128 x 128 tiles than CUs, those in min(2 CUs / tiles, 3)
 //     splits; else the round model's tile, unsplit;
 //   * up to 5 CUs tiles of 64 x 64: that tile, residual projections split
-//     into min(CUs / tiles, 6, blocks / 4) (5 -> 4);
+//     into min(CUs / tiles, 6, blocks / 4) (5 -> 4); when the workgroups
+//     (tiles x splits) leave each CU at most one, two groups of 4 waves share
+//     each tile's k-blocks (below);
 //   * else the round model's large tile (unchanged at the 650M 8192-token
 //     shapes).
 // ESM-2 35M at 2552 tokens (8 ragged sequences), against the register-staged
@@ -1264,6 +1343,24 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     }
     p.tile = tile;
     p.splits = S;
+    if (tile == LDS_TILE_64x64) {
+        // Two groups of 4 waves on each 64 x 64 tile when the workgroups
+        // leave each CU at most one (a lone 4-wave workgroup has one wave per
+        // SIMD).  ESM-2 650M Q8_0 forwards, one sequence: L = 130 2.61 -> 2.26
+        // ms, L = 66 2.40 -> 2.08, L = 402 4.06 -> 3.97; 150M B = 2 L = 100
+        // 1.50 -> 1.41; 8M FP32 L = 256 0.377 -> 0.368.  More workgroups than
+        // CUs (35M B = 8 ragged: Wo, FC2 at 328 tiles) gain nothing or lose:
+        // a CU that runs two tiles moves the same operands through its LDS
+        // either way.  Four groups: equal or slower everywhere.  The groups
+        // regroup the k-sum as a split does, so CIH_SPLITK=0 keeps one group
+        // (CIH_GEMM_KW=1, 2 or 4 sets the count).
+        const long wg = t64 * S;
+        const int kb = S > 1 ? p.kps : KB;
+        int kw = wg <= cus && kb >= 4 ? 2 : 1;  // two blocks per group at least
+        if (ke && !strcmp(ke, "0")) kw = 1;
+        if (const char *we = getenv("CIH_GEMM_KW")) kw = atoi(we) == 4 ? 4 : (atoi(we) == 2 ? 2 : 1);
+        p.kw = kw;
+    }
     return true;
 }
 
@@ -1276,13 +1373,13 @@ hipError_t launch_gemm_lds_plan(const DevMatrix &W, const void *X, const float *
         if (epi != EPI_RESIDUAL || !pb || !pb->part || p.kps <= 0 || (size_t)p.splits * M * W.N > pb->floats ||
             (p.splits - 1) * p.kps >= W.K / 32)
             return hipErrorInvalidValue;
-        return launch_split(W, X, M, pb->part, p.splits, p.kps, p.tile, st);
+        return launch_split(W, X, M, pb->part, p.splits, p.kps, p.tile, p.kw, st);
     }
     if (epi == EPI_GELU_H2 && W.N % 32) return hipErrorInvalidValue;
     switch (epi) {
-    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile);
-    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile);
-    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile);
+    case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile, p.kw);
+    case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile, p.kw);
+    case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile, p.kw);
     default: return hipErrorInvalidValue;
     }
 }

@@ -265,9 +265,10 @@ enum LdsTileId { LDS_TILE_128x128 = 1, LDS_TILE_128x160, LDS_TILE_128x256, LDS_T
 // Tile and k-splits for an f16-limb GEMM with the f16 copy from 64 rows on
 // (false: not such a GEMM, or CIH_GEMM_LDS / CIH_GEMM_PLAN=0 set).  Splits
 // only for EPI_RESIDUAL with room for them (part_floats > 0; the caller
-// adds them, as launch_gemm_lds_split's).
+// adds them, as launch_gemm_lds_split's).  kw: groups of 4 waves that share
+// a 64 x 64 tile's k-blocks (1, 2 or 4).
 struct LdsPlan {
-    int tile = 0, splits = 1, kps = 0;
+    int tile = 0, splits = 1, kps = 0, kw = 1;
 };
 bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_floats, LdsPlan &p);
 // The planned GEMM: with p.splits > 1 the raw partial sums [p.splits][M][N]

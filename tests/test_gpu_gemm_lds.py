@@ -183,3 +183,47 @@ def test_fp32_pair_copy_is_bit_identical(monkeypatch):
         assert_same(b, a, seqs, "fp32 pair")
         assert_same(c, a, seqs, "fp32 hand-off")
     m.close()
+
+
+def assert_close(got, ref, seqs, what, tol=2e-5):
+    for i, s in enumerate(seqs):
+        n = len(s)
+        for k in ("logits", "hidden", "contacts"):
+            g, r = got[k][i], ref[k][i]
+            g, r = (g[:n - 2, :n - 2], r[:n - 2, :n - 2]) if k == "contacts" else (g[:n], r[:n])
+            e = float(np.abs(g.astype(np.float64) - r).max())
+            assert e <= tol * max(1.0, float(np.abs(r).max())), (what, i, k, e)
+
+
+@pytest.mark.parametrize("kw", ["2", "4"])
+@pytest.mark.parametrize("case", ["q8", "q4", "f32", "q8-d480"])
+def test_k_groups_match_one_group(case, kw, monkeypatch):
+    """Groups of 4 waves sharing a 64 x 64 tile's k-blocks (group g takes
+    blocks kb0 + g, kb0 + g + KW, ...; the groups' sums are added in group
+    order): the k-sum is regrouped, so the forward agrees with one group to
+    2e-5 of the largest value, not bit for bit, with the residual k-splits
+    off and on, from the f16 copy of the quants and from FP32 pair copies.
+    d = 480 gives Wo 15 k-blocks, which 2 and 4 groups do not divide (a
+    group's last step computes nothing)."""
+    rng = np.random.default_rng(23)
+    d, f, H = {"f32": (320, 1280, 20), "q8-d480": (480, 1920, 20)}.get(case, (192, 768, 3))
+    cfg = ch.EsmConfig(d, f, 2, H)
+    w = ch.EsmWeights.random(cfg, seed=23, bias_std=0.02)
+    if case != "f32":
+        w = w.quantize_q4() if case == "q4" else w.quantize_q8()
+    cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
+    lens = (298, 255, 128) if d == 192 else (298, 200)
+    seqs = [rand_tokens(rng, n) for n in lens]
+    m = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=3, max_len=300, outputs=FLAGS)
+    monkeypatch.setenv("CIH_SPLITK", "0")
+    monkeypatch.setenv("CIH_GEMM_KW", "1")
+    a = m.forward(seqs, FLAGS)
+    monkeypatch.setenv("CIH_GEMM_KW", kw)
+    b = m.forward(seqs, FLAGS)
+    monkeypatch.delenv("CIH_SPLITK")
+    c = m.forward(seqs, FLAGS)
+    print(f"{case}, {sum(lens) + 2 * len(lens)} tokens: {kw} k-groups agree with one group, splits off and on",
+          flush=True)
+    assert_close(b, a, seqs, case + " groups")
+    assert_close(c, a, seqs, case + " groups + splits")
+    m.close()
