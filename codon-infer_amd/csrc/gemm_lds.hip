@@ -30,7 +30,7 @@
 // the device with those, 64 x 128 (4 x 32 x 64, three per CU) and 64 x 64
 // (4 x 32 x 32, four per CU), read from the f16 copy only.  Every tile sums the same products in the same
 // order, so the tile never changes a result.  The 64 x 64 tile can also run
-// on 2 or 4 groups of its 4 waves (KW), which take alternate k-blocks
+// on 2 or 4 groups of its 4 waves (KW; 64 x 128: 2), which take alternate k-blocks
 // through stages of their own and add their sums at the end: the k-sum
 // regrouped, as a k-split regroups it.
 #include <stdlib.h>
@@ -1136,7 +1136,10 @@ hipError_t launch_split(const DevMatrix &W, const void *X, int M, float *part, i
         if (kw == 2) return launch_split_t<1, 1, 2, 2, 2>(W, X, M, part, S, kps, st);
         return launch_split_t<1, 1, 2, 2>(W, X, M, part, S, kps, st);
     }
-    if (tile == LDS_TILE_64x128) return launch_split_t<1, 2, 2, 2>(W, X, M, part, S, kps, st);
+    if (tile == LDS_TILE_64x128) {
+        if (kw == 2) return launch_split_t<1, 2, 2, 2, 2>(W, X, M, part, S, kps, st);
+        return launch_split_t<1, 2, 2, 2>(W, X, M, part, S, kps, st);
+    }
     return launch_split_t<2, 2, 2, 2>(W, X, M, part, S, kps, st);
 }
 
@@ -1207,7 +1210,10 @@ hipError_t launch_epi(const DevMatrix &W, const void *X, const float *bias, void
     if constexpr (EPI < EPI_QKV16) {
         if (tile == LDS_TILE_128x160) return launch_t<EPI, 1, 5, 4, 1>(W, X, bias, Y, ldy, M, st, qo);
         if (W.q16) {
-            if (tile == LDS_TILE_64x128) return launch_t<EPI, 1, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+            if (tile == LDS_TILE_64x128) {
+                if (kw == 2) return launch_t<EPI, 1, 2, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+                return launch_t<EPI, 1, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
+            }
             if (tile == LDS_TILE_64x64) {
                 if (kw == 4) return launch_t<EPI, 1, 1, 2, 2, 4>(W, X, bias, Y, ldy, M, st, qo);
                 if (kw == 2) return launch_t<EPI, 1, 1, 2, 2, 2>(W, X, bias, Y, ldy, M, st, qo);
@@ -1343,6 +1349,14 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     }
     p.tile = tile;
     p.splits = S;
+    if (tile == LDS_TILE_64x128) {
+        // the 64 x 128 tile (deep residual projections in 3 splits) likewise
+        const long wg = (long)((M + 63) / 64) * ((W.N + 127) / 128) * S;
+        int kw = wg <= cus && (S > 1 ? p.kps : KB) >= 4 ? 2 : 1;
+        if (ke && !strcmp(ke, "0")) kw = 1;
+        if (const char *we = getenv("CIH_GEMM_KW")) kw = atoi(we) >= 2 ? 2 : 1;
+        p.kw = kw;
+    }
     if (tile == LDS_TILE_64x64) {
         // Two groups of 4 waves on each 64 x 64 tile when the workgroups
         // leave each CU at most one (a lone 4-wave workgroup has one wave per

@@ -187,13 +187,14 @@ def test_forward_preset_archs(arch, dtype, B, lo, hi):
     check_batch(cfg, w, seqs, flags, contact=cfg.contact_head_weights())
 
 
-@pytest.mark.parametrize("lens", [(300, 220), (650, 650, 650, 650)])
+@pytest.mark.parametrize("lens", [(300, 220), (300, 400), (650, 650, 650, 650)])
 def test_planned_splits_vs_oracle(lens):
     """d = 640 with FC2 K = 5120 over two layers, Q8_0: the planned k-splits
     of the residual projections, which leave their partial sums to the
     LayerNorm after them.  524 tokens: Wo and FC2 on 64 x 64 tiles in 2
     splits, each tile's k-blocks shared by two groups of 4 waves (180
-    workgroups); 2608 tokens: Wo unsplit, FC2 on 128 x 128 tiles in 3."""
+    workgroups); 704 tokens: FC2 on 64 x 128 tiles in 3 splits, also on two
+    wave groups; 2608 tokens: Wo unsplit, FC2 on 128 x 128 tiles in 3."""
     rng = np.random.default_rng(21)
     cfg = ch.EsmConfig(640, 5120, 2, 20)
     w = ch.EsmWeights.random(cfg, seed=21, bias_std=0.02).quantize_q8()

@@ -196,7 +196,7 @@ def assert_close(got, ref, seqs, what, tol=2e-5):
 
 
 @pytest.mark.parametrize("kw", ["2", "4"])
-@pytest.mark.parametrize("case", ["q8", "q4", "f32", "q8-d480"])
+@pytest.mark.parametrize("case", ["q8", "q4", "f32", "q8-d480", "q8-deep"])
 def test_k_groups_match_one_group(case, kw, monkeypatch):
     """Groups of 4 waves sharing a 64 x 64 tile's k-blocks (group g takes
     blocks kb0 + g, kb0 + g + KW, ...; the groups' sums are added in group
@@ -204,17 +204,19 @@ def test_k_groups_match_one_group(case, kw, monkeypatch):
     2e-5 of the largest value, not bit for bit, with the residual k-splits
     off and on, from the f16 copy of the quants and from FP32 pair copies.
     d = 480 gives Wo 15 k-blocks, which 2 and 4 groups do not divide (a
-    group's last step computes nothing)."""
+    group's last step computes nothing); d = 640 with K = 5120 at 704 tokens
+    puts FC2 on 64 x 128 tiles in 3 splits (which take 2 groups for either
+    count)."""
     rng = np.random.default_rng(23)
-    d, f, H = {"f32": (320, 1280, 20), "q8-d480": (480, 1920, 20)}.get(case, (192, 768, 3))
+    d, f, H = {"f32": (320, 1280, 20), "q8-d480": (480, 1920, 20), "q8-deep": (640, 5120, 20)}.get(case, (192, 768, 3))
     cfg = ch.EsmConfig(d, f, 2, H)
     w = ch.EsmWeights.random(cfg, seed=23, bias_std=0.02)
     if case != "f32":
         w = w.quantize_q4() if case == "q4" else w.quantize_q8()
     cw = (rng.standard_normal(cfg.n_layers * cfg.n_heads) * 0.1).astype(np.float32)
-    lens = (298, 255, 128) if d == 192 else (298, 200)
+    lens = (298, 255, 128) if d == 192 else ((300, 400) if d == 640 else (298, 200))
     seqs = [rand_tokens(rng, n) for n in lens]
-    m = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=3, max_len=300, outputs=FLAGS)
+    m = ch.GpuModel(cfg, w, contact_head=(cw, 0.2), max_batch=3, max_len=402, outputs=FLAGS)
     monkeypatch.setenv("CIH_SPLITK", "0")
     monkeypatch.setenv("CIH_GEMM_KW", "1")
     a = m.forward(seqs, FLAGS)
