@@ -635,19 +635,25 @@ int forward_impl(cih_model *m, const int32_t *tokens, const int32_t *lens, int32
     // final LayerNorm: state.x = LN_f(x) (lib.rs:5379-5387).  It also
     // reports a residual row that is no longer finite (the f16 limbs hold
     // |x| < 65520 only, and an overflow there makes the residual non-finite)
-    // and an output the LM head's limbs cannot hold.
+    // and an output the LM head's limbs cannot hold.  Without a hidden-state
+    // export it hands the LM head's dense layer (FP32 weights through their
+    // pair copy) f16 limbs: the split that GEMM makes of FP32 rows, so the
+    // same bits, and from 64 rows on the LDS-staged kernel reads them.
+    const bool lm_h2 = (want_logits || keep_logits) && m->has_head && !want_hidden && af == AF_H2 &&
+                       T > GEMV_MAX_M && m->dense.fmt == WF_F32 && m->dense.p16 && m->dense.psc && d % 32 == 0;
     {
         ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
+        const int lf = lm_h2 ? AF_H2 : AF_F32;
         if (pend_splits)
-            HIPCHK(launch_residual_layernorm(ws.x, part_a, pend_splits, pend_bias, m->lnfw, m->lnfb, ws.ao, AF_F32, T,
-                                             d, st, ws.flag));
+            HIPCHK(launch_residual_layernorm(ws.x, part_a, pend_splits, pend_bias, m->lnfw, m->lnfb, ws.ao, lf, T, d,
+                                             st, ws.flag));
         else
-            HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, AF_F32, T, d, st, ws.flag));
+            HIPCHK(launch_layernorm(ws.x, m->lnfw, m->lnfb, ws.ao, lf, T, d, st, ws.flag));
     }
     if (want_hidden) HIPCHK(launch_scatter_rows(ws.ao, d, sm, t_hidden, (int64_t)S_max * d, st));
     if (want_logits || keep_logits) {
         if (m->has_head) {
-            HIPCHK(gemm(m, m->dense, ws.ao, d, AF_F32, m->dense_b, ws.hbuf, d, T, EPI_GELU));
+            HIPCHK(gemm(m, m->dense, ws.ao, d, lm_h2 ? AF_H2 : AF_F32, m->dense_b, ws.hbuf, d, T, EPI_GELU));
             {
                 ProfScope ps(m, CIH_KC_OTHER, 0, 8.0 * T * d);
                 // its output feeds the decoder's GEMM, which splits it into f16 limbs

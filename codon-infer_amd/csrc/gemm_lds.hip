@@ -753,7 +753,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS * KW), (LdsTile<R
 #pragma unroll
                     for (int q = 0; q < 16; q++) {
                         float v = acc[r][c][q] + bv[c];
-                        if constexpr (EPI == EPI_GELU_H2) v = gelu_as(v);
+                        if constexpr (EPI == EPI_GELU_H2 || EPI == EPI_GELU) v = gelu_as(v);
                         if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
                         acc[r][c][q] = v;
                     }
@@ -965,7 +965,7 @@ __global__ __launch_bounds__((LdsTile<RT, CT, WM, WN>::THREADS * KW), (LdsTile<R
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 float v = acc[r][c][q] + bv[c];
-                if constexpr (EPI == EPI_GELU_H2) v = gelu_as(v);
+                if constexpr (EPI == EPI_GELU_H2 || EPI == EPI_GELU) v = gelu_as(v);
                 if constexpr (EPI == EPI_RESIDUAL) v = res[c][r][q] + v;
                 acc[r][c][q] = v;
             }
@@ -1053,14 +1053,28 @@ hipError_t launch_t(const DevMatrix &W, const void *X, const float *bias, void *
     const unsigned short *Xh = reinterpret_cast<const unsigned short *>(X);
     const bool quants = !W.q16;
     const int kbx = W.kx / 32;
-    if (kbx && !copy_only<RT, CT>()) return hipErrorInvalidValue;  // pair copies: the small tiles only
-    if constexpr (copy_only<RT, CT>()) {
+    // FP32 weights' pair copies (kbx): the small tiles and 128 x 320; the FP32
+    // GELU epilogue (the LM head's dense layer) only with a pair copy
+    constexpr bool PX320 = RT == 1 && CT == 5 && WM == 4 && WN == 2 && EPI < EPI_QKV16;
+    if ((kbx && !copy_only<RT, CT>() && !PX320) || (EPI == EPI_GELU && (!kbx || quants))) return hipErrorInvalidValue;
+    if constexpr (PX320) {
+        if (kbx) {
+            if (quants) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((k_gemm_lds<EPI, 1, 5, 4, 2, 0, false, 1, false, true>), dim3(tiles), dim3(T::THREADS), 0,
+                               st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc, bias, Y, ldy, M, W.N, W.K,
+                               qo, 0, kbx);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (EPI == EPI_GELU && !copy_only<RT, CT>()) {
+        return hipErrorInvalidValue;  // (rejected above)
+    } else if constexpr (copy_only<RT, CT>()) {
         if (quants) return hipErrorInvalidValue;
         if (kbx)
             hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, 0, false, true, KW>), dim3(tiles),
                                dim3(T::THREADS * KW), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc,
                                bias, Y, ldy, M, W.N, W.K, qo, 0, kbx);
-        else
+        else if constexpr (EPI != EPI_GELU)
             hipLaunchKernelGGL((k_gemm_lds<EPI, RT, CT, WM, WN, 0, false, 0, false, false, KW>), dim3(tiles),
                                dim3(T::THREADS * KW), 0, st, Xh, reinterpret_cast<const unsigned char *>(W.q16), W.sc,
                                bias, Y, ldy, M, W.N, W.K, qo);
@@ -1309,7 +1323,7 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     if (a_fmt != AF_H2 || (W.fmt != WF_Q8 && W.fmt != WF_Q4 && W.fmt != WF_F16P) || !W.q16 || W.K % 32 || W.K <= 0 ||
         W.N <= 0 || W.kx % 32)
         return false;
-    if (epi != EPI_NONE && epi != EPI_RESIDUAL && epi != EPI_GELU_H2) return false;
+    if (epi != EPI_NONE && epi != EPI_RESIDUAL && epi != EPI_GELU_H2 && !(epi == EPI_GELU && W.kx)) return false;
     if (M < 64) return false;  // fewer rows: the register-staged kernel (and its splits) is as fast or faster
     const char *le = getenv("CIH_GEMM_LDS"), *pe = getenv("CIH_GEMM_PLAN"), *ke = getenv("CIH_SPLITK");
     if (le || (pe && !strcmp(pe, "0"))) return false;  // CIH_GEMM_LDS=0 / force: the routes without the plan
@@ -1339,9 +1353,9 @@ bool gemm_lds_plan(const DevMatrix &W, int a_fmt, int M, int epi, size_t part_fl
     } else {
         tile = tile_choice(M, W.N, true);
     }
-    // a pair copy (W.kx): the 64-row tiles only (the large ones keep the
+    // a pair copy (W.kx): the 64-row tiles and 128 x 320 (the others keep the
     // register-staged pair path)
-    if (W.kx && tile != LDS_TILE_64x64 && tile != LDS_TILE_64x128) return false;
+    if (W.kx && tile != LDS_TILE_64x64 && tile != LDS_TILE_64x128 && tile != LDS_TILE_128x320) return false;
     while (S > 1 && (size_t)S * M * W.N > part_floats) S--;
     if (S > 1) {
         p.kps = (KB + S - 1) / S;
@@ -1394,6 +1408,7 @@ hipError_t launch_gemm_lds_plan(const DevMatrix &W, const void *X, const float *
     case EPI_NONE: return launch_epi<EPI_NONE>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile, p.kw);
     case EPI_RESIDUAL: return launch_epi<EPI_RESIDUAL>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile, p.kw);
     case EPI_GELU_H2: return launch_epi<EPI_GELU_H2>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile, p.kw);
+    case EPI_GELU: return launch_epi<EPI_GELU>(W, X, bias, Y, ldy, M, st, QkvOut(), p.tile, p.kw);
     default: return hipErrorInvalidValue;
     }
 }

@@ -229,3 +229,39 @@ def test_k_groups_match_one_group(case, kw, monkeypatch):
     assert_close(b, a, seqs, case + " groups")
     assert_close(c, a, seqs, case + " groups + splits")
     m.close()
+
+
+@pytest.mark.parametrize("case", ["8m-fp32", "650m-width-q8"])
+def test_lm_head_limb_handoff_is_bit_identical(case, monkeypatch):
+    """Without a hidden-state export the final LayerNorm hands the LM head's
+    dense layer (FP32 weights through their pair copy) f16 limbs instead of
+    FP32 rows; the GEMM made the same split itself, so with every k-split off
+    (CIH_SPLITK=0: the register-staged kernel splits the FP32-row form at
+    small batches) the logits equal the FP32 hand-off's (a forward that also
+    exports the hidden state) bit for bit, on the LDS-staged kernel and on
+    the register-staged one (CIH_GEMM_LDS=0).  d = 320 FP32 at 422 tokens:
+    the 64 x 64 tiles; d = 1280 at 4608 tokens: 128 x 320 tiles with the pair
+    copy's wrap."""
+    rng = np.random.default_rng(29)
+    if case == "8m-fp32":
+        cfg = ch.EsmConfig(320, 1280, 2, 20)
+        w = ch.EsmWeights.random(cfg, seed=29, bias_std=0.02)
+        lens = (298, 120)
+    else:
+        cfg = ch.EsmConfig(1280, 5120, 2, 20)
+        w = ch.EsmWeights.random(cfg, seed=29, bias_std=0.02).quantize_q8()
+        lens = (510,) * 9
+    seqs = [rand_tokens(rng, n) for n in lens]
+    both = ch.OUT_LOGITS | ch.OUT_HIDDEN
+    m = ch.GpuModel(cfg, w, max_batch=len(seqs), max_len=max(len(s) for s in seqs), outputs=both)
+    monkeypatch.setenv("CIH_SPLITK", "0")
+    a = m.forward(seqs, ch.OUT_LOGITS)
+    b = m.forward(seqs, both)
+    monkeypatch.setenv("CIH_GEMM_LDS", "0")
+    c = m.forward(seqs, ch.OUT_LOGITS)
+    m.close()
+    print(f"{case}, {sum(len(s) for s in seqs)} tokens: LM head on limbs equals the FP32 hand-off", flush=True)
+    for i, s in enumerate(seqs):
+        n = len(s)
+        assert np.array_equal(a["logits"][i, :n], b["logits"][i, :n]), (case, i)
+        assert np.array_equal(c["logits"][i, :n], b["logits"][i, :n]), (case, i)
